@@ -1,0 +1,245 @@
+"""Benchmark of porch's fused-graph path on one MI355X.
+
+A step is one materialisation of a benchmark graph over one batch of
+inputs already resident in HBM: porch_materialize on the graph's node
+table (graph-cache lookup, stream-ordered output allocation, kernel launch)
+and the release of the output.  Consecutive steps rotate over enough input
+copies that no step finds its inputs in L2 or the 256 MB Infinity Cache.
+
+The headline line is config c2 (the strided-slice + transpose + concat view
+chain over x fp32 [4096, 4096]): HBM GB/s of algorithmic bytes (all of x
+read, the output written).  The other configs are reported beside it under
+"configs", each with its roofline fraction and JIT latency.  The host
+evaluator (the oracle, OpenMP) is timed on this machine's cores as the CPU
+baseline.
+
+    python bench.py [--steps K] [--warmup W] [--configs c1,c2,...] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+FP32_MFMA_PEAK_TFLOPS = 157.3    # 256 CU x 256 flop/clk x 2.4 GHz
+
+METRIC = "fused-graph HBM GB/s (% of peak); fp32 matmul TFLOP/s (% MFMA peak); JIT ms"
+
+# Algorithmic work per step (bytes for HBM-bound graphs, flops for c5).
+WORK = {
+    "c1": ("hbm", 3 * 4 * (1 << 20)),
+    "c2": ("hbm", 4096 * 4096 * 4 + 4096 * 2048 * 4),
+    "c3": ("hbm", 2 * 8192 * 4096 * 4),
+    "c4": ("hbm", 16384 * 2048 * 4 + 2 * 2048 * 4 + 16384 * 4),
+    "c5": ("mfma", 2 * 4096 ** 3),
+}
+DESCRIPTION = {
+    "c1": "(a + b) * 2 - 1, a, b fp32 [1048576]",
+    "c2": "concat(transpose(x[0::2,1::2]), transpose(x[1::2,0::2]), 0) + 1, x fp32 [4096,4096]",
+    "c3": "softmax(x, 1), x fp32 [8192,4096]",
+    "c4": "sum(logistic(relu(x*bcast(w) + bcast(bias))), 1), x fp32 [16384,2048]",
+    "c5": "relu(A @ B + bcast(bias)) - 0.5, A, B fp32 [4096,4096]",
+}
+# Input copies rotated through so that a step never re-reads cached data.
+ROTATION = {"c1": 48, "c2": 8, "c3": 4, "c4": 6, "c5": 1}
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def run_config(porch, name: str, steps: int, warmup: int) -> dict:
+    from porch_amd import _lib, synth
+    from porch_amd.workloads import config_graph, config_inputs, config_shapes
+
+    shapes = config_shapes(name)
+    host = config_inputs(name)
+    copies = ROTATION[name]
+    sets = [[porch.tensor(s, v) for s, v in zip(shapes, host)] for _ in range(copies)]
+    expr = config_graph(name, sets[0])
+    nodes, dims, n_dims, inputs, _ = porch.serialize(expr)
+    graph = porch._graph(nodes, dims, n_dims)
+    # The node table is the same for every copy; only the buffers differ.
+    handles = []
+    for s in sets:
+        _, _, _, ins, _ = porch.serialize(config_graph(name, s))
+        handles.append((ctypes.c_void_p * len(ins))(*[t.device_data().handle for t in ins]))
+    n_in = len(inputs)
+    out = ctypes.c_void_p()
+
+    def step(i: int) -> None:
+        _lib.check(_lib.lib.porch_materialize(ctypes.byref(graph), handles[i % copies], n_in,
+                                              ctypes.byref(out), None, 0, None))
+        _lib.lib.porch_buffer_release(out)
+
+    # Cold JIT: codegen + hiprtc + module load of this graph in this process.
+    porch.reset_jit_cache()
+    step(0)
+    porch.synchronize()
+    cold_ms = porch.jit_stats()["last_miss_ms"]
+
+    for i in range(warmup):
+        step(i)
+    porch.synchronize()
+
+    # Timed region: K steps, one HIP event pair per step on porch's stream.
+    starts = [synth.Event() for _ in range(steps)]
+    stops = [synth.Event() for _ in range(steps)]
+    hit_us = []
+    porch.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        step(i)
+        stops[i].record()
+        hit_us.append(porch.jit_stats()["last_hit_us"])
+    porch.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernel_ms = [a.elapsed_ms(b) for a, b in zip(starts, stops)]
+
+    bound, work = WORK[name]
+    mean_kernel_s = float(np.mean(kernel_ms)) / 1e3
+    if bound == "hbm":
+        achieved = work / mean_kernel_s / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+        whole_job = work * steps / elapsed / 1e9
+    else:
+        achieved = work / mean_kernel_s / 1e12
+        peak, unit = FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
+        whole_job = work * steps / elapsed / 1e12
+    plan = porch.plan(expr)
+    return {
+        "workload": DESCRIPTION[name],
+        "kernels": [k["kind"] for k in plan["kernels"]],
+        "value": whole_job,
+        "unit": unit,
+        "ms_per_step": elapsed / steps * 1e3,
+        "kernel_ms_mean": float(np.mean(kernel_ms)),
+        "kernel_ms_median": float(np.median(kernel_ms)),
+        "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+                     "frac": achieved / peak, "traffic": None},
+        "jit_ms": {"cold": cold_ms, "hit": float(np.median(hit_us)) / 1e3},
+        "steps": steps,
+    }
+
+
+def cpu_baseline(name: str, max_seconds: float = 20.0) -> dict:
+    from oracle import host
+    from porch_amd.workloads import config_graph, config_inputs, config_shapes
+
+    import porch_amd as porch
+
+    shapes = config_shapes(name)
+    values = config_inputs(name)
+    tensors = []
+    for s, v in zip(shapes, values):
+        t = porch.tensor.__new__(porch.tensor)
+        t._state = porch._State(s, porch.device())
+        t._state.storage = porch._Storage(None, v)
+        tensors.append(t)
+    sample = "full workload"
+    scale = 1.0
+    if name == "c5":
+        rows = 256  # 1/16 of the rows of A; time scaled by 16
+        a, b, bias = values
+        tensors[0]._state = porch._State([rows, 4096], porch.device())
+        tensors[0]._state.storage = porch._Storage(None, a[: rows * 4096])
+        expr = porch.relu(porch.matmul(tensors[0], tensors[1]) +
+                          porch.broadcast_to(tensors[2], [rows, 4096])) - 0.5
+        sample = f"{rows} of 4096 rows of C (time x {4096 // rows})"
+        scale = 4096 / rows
+    else:
+        expr = config_graph(name, tensors)
+    times = []
+    host.evaluate(expr)  # warm-up
+    start = time.perf_counter()
+    while len(times) < 5 and time.perf_counter() - start < max_seconds:
+        t0 = time.perf_counter()
+        host.evaluate(expr)
+        times.append((time.perf_counter() - t0) * scale)
+    seconds = float(np.median(times))
+    bound, work = WORK[name]
+    value = work / seconds / (1e9 if bound == "hbm" else 1e12)
+    return {"value": value, "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+            "cores": host.threads(), "kind": "port",
+            "sample": f"host evaluator, {sample}, median of {len(times)} runs",
+            "seconds": seconds}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    parser.add_argument("--no-cpu", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: porch's fused-graph path has no multi-GPU "
+              "execution (see DESIGN.md for how it would shard); run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import porch_amd as porch
+    from porch_amd import synth
+
+    if not porch.is_available():
+        print("porch_amd: the HIP backend is not available", file=sys.stderr)
+        return 1
+    info = synth.device_info()
+    log(f"device: {info}")
+    configs = [c for c in args.configs.split(",") if c]
+    results = {}
+    for name in configs:
+        # c5 steps are long; keep its timed region short.
+        steps = args.steps if WORK[name][0] == "hbm" else max(3, args.steps // 40)
+        warmup = args.warmup if WORK[name][0] == "hbm" else max(1, args.warmup // 10)
+        log(f"{name}: {DESCRIPTION[name]} ({steps} steps)")
+        results[name] = run_config(porch, name, steps, warmup)
+        r = results[name]
+        log(f"{name}: {r['value']:.1f} {r['unit']} whole-job, kernel {r['kernel_ms_mean']*1e3:.1f} us, "
+            f"roofline {r['roofline']['frac']*100:.1f}%, JIT cold {r['jit_ms']['cold']:.1f} ms "
+            f"hit {r['jit_ms']['hit']*1e3:.1f} us")
+        if not args.no_cpu:
+            results[name]["cpu_baseline"] = cpu_baseline(name)
+            log(f"{name}: cpu {results[name]['cpu_baseline']['value']:.2f} "
+                f"{results[name]['cpu_baseline']['unit']} on {results[name]['cpu_baseline']['cores']} threads")
+
+    head = "c2" if "c2" in results else configs[0]
+    h = results[head]
+    line = {
+        "metric": METRIC,
+        "value": h["value"],
+        "unit": h["unit"],
+        "n_gpus": 1,
+        "steps": h["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (splitmix64 seeded inputs resident in HBM)",
+        "config": {"workload": f"{head}: {h['workload']}", "parallelism": "single GPU",
+                   "device": info["arch"], "compute_units": info["compute_units"]},
+        "roofline": h["roofline"],
+        "cpu_baseline": h.get("cpu_baseline"),
+        "jit_ms": h["jit_ms"],
+        "configs": results,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

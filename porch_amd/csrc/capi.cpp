@@ -1,0 +1,409 @@
+// The extern "C" boundary declared in include/porch_amd.h.
+
+#include "porch_amd.h"
+
+#include "internal.hpp"
+#include "planner.hpp"
+
+#include <chrono>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+struct porch_buffer {
+    porch::hip_jit::device_buffer handle;
+};
+
+struct porch_code_object {
+    std::shared_ptr<const porch::rt::code_object> object;
+};
+
+struct porch_event {
+    porch::hip::event_t event = nullptr;
+};
+
+namespace {
+
+    using namespace porch;
+
+    std::string& last_error() {
+        thread_local std::string message;
+        return message;
+    }
+
+    template <typename F>
+    porch_status guarded(F&& body) {
+        try {
+            body();
+            last_error().clear();
+            return PORCH_OK;
+        }
+        catch (const hip_jit::compilation_error& e) {
+            last_error() = e.log();
+            return PORCH_ERR_COMPILATION;
+        }
+        catch (const std::invalid_argument& e) {
+            last_error() = e.what();
+            return PORCH_ERR_INVALID_ARGUMENT;
+        }
+        catch (const std::out_of_range& e) {
+            last_error() = e.what();
+            return PORCH_ERR_OUT_OF_RANGE;
+        }
+        catch (const std::exception& e) {
+            last_error() = e.what();
+            return PORCH_ERR_RUNTIME;
+        }
+        catch (...) {
+            last_error() = "unknown error";
+            return PORCH_ERR_RUNTIME;
+        }
+    }
+
+    void require(bool condition, const char* message) {
+        if (!condition) throw std::invalid_argument(message);
+    }
+
+    ir::graph validated(const porch_graph* table) {
+        ir::graph g = ir::from_c(table);
+        ir::infer(g);
+        if (g.n_inputs == 0) {
+            // Only nodes reachable from the root count as references.
+            bool any = false;
+            for (const ir::node& n : g.nodes) any = any || n.kind == ir::op::input;
+            if (!any)
+                throw std::invalid_argument(
+                    "tensor expression must reference at least one tensor"
+                );
+        }
+        return g;
+    }
+
+    void write_shape(const std::vector<int64_t>& shape, int64_t* out, int32_t capacity,
+                     int32_t* rank) {
+        if (rank) *rank = static_cast<int32_t>(shape.size());
+        if (out == nullptr) return;
+        for (size_t i = 0; i < shape.size() && static_cast<int32_t>(i) < capacity; ++i)
+            out[i] = shape[i];
+    }
+
+    void copy_text(const std::string& text, char* out, size_t capacity) {
+        if (out == nullptr || capacity == 0) return;
+        const size_t n = std::min(text.size(), capacity - 1);
+        std::memcpy(out, text.data(), n);
+        out[n] = '\0';
+    }
+
+} // namespace
+
+extern "C" {
+
+const char* porch_last_error(void) { return last_error().c_str(); }
+
+int32_t porch_is_available(void) { return hip_jit::is_available() ? 1 : 0; }
+
+porch_status porch_synchronize(void) {
+    return guarded([] { hip_jit::synchronize(); });
+}
+
+porch_status porch_device_info(int32_t* compute_units, int32_t* clock_khz, char* arch,
+                               size_t arch_capacity) {
+    return guarded([&] {
+        const rt::device_info& info = rt::device();
+        if (compute_units) *compute_units = info.compute_units;
+        if (clock_khz) *clock_khz = info.clock_khz;
+        copy_text(info.arch, arch, arch_capacity);
+    });
+}
+
+porch_status porch_buffer_create(size_t bytes, porch_buffer** out) {
+    return guarded([&] {
+        require(out != nullptr, "output pointer is null");
+        *out = nullptr;
+        auto* b = new porch_buffer();
+        try {
+            b->handle = hip_jit::device_buffer{bytes};
+        }
+        catch (...) {
+            delete b;
+            throw;
+        }
+        *out = b;
+    });
+}
+
+void porch_buffer_release(porch_buffer* buffer) { delete buffer; }
+
+size_t porch_buffer_size(const porch_buffer* buffer) {
+    return buffer == nullptr ? 0 : buffer->handle.size_bytes();
+}
+
+uint64_t porch_buffer_device_pointer(const porch_buffer* buffer) {
+    return buffer == nullptr
+               ? 0
+               : static_cast<uint64_t>(
+                     reinterpret_cast<uintptr_t>(buffer->handle.device_pointer())
+                 );
+}
+
+porch_status porch_copy_to_device(porch_buffer* buffer, const float* source, size_t count) {
+    return guarded([&] {
+        require(buffer != nullptr, "buffer is null");
+        require(source != nullptr || count == 0, "source is null");
+        hip_jit::copy_to_device(buffer->handle, {source, count});
+    });
+}
+
+porch_status porch_copy_to_host(const porch_buffer* buffer, float* target, size_t count) {
+    return guarded([&] {
+        require(buffer != nullptr, "buffer is null");
+        require(target != nullptr || count == 0, "target is null");
+        hip_jit::copy_to_host(buffer->handle, {target, count});
+    });
+}
+
+porch_status porch_compile(const char* source, const char* const* options, int32_t n_options,
+                           porch_code_object** out) {
+    return guarded([&] {
+        require(source != nullptr, "source is null");
+        require(out != nullptr, "output pointer is null");
+        require(n_options >= 0 && (n_options == 0 || options != nullptr), "options are malformed");
+        std::vector<std::string> extra;
+        for (int32_t i = 0; i < n_options; ++i) {
+            require(options[i] != nullptr, "option is null");
+            extra.emplace_back(options[i]);
+        }
+        auto* code = new porch_code_object();
+        try {
+            code->object = rt::compile(source, extra);
+        }
+        catch (...) {
+            delete code;
+            throw;
+        }
+        *out = code;
+    });
+}
+
+size_t porch_code_object_size(const porch_code_object* code) {
+    return code == nullptr ? 0 : code->object->bytes.size();
+}
+
+const void* porch_code_object_data(const porch_code_object* code) {
+    return code == nullptr ? nullptr : code->object->bytes.data();
+}
+
+void porch_code_object_release(porch_code_object* code) { delete code; }
+
+namespace {
+    porch_status raw_launch(const void* code, size_t code_size, const char* function,
+                            const porch_buffer* const* inputs, int32_t n_inputs,
+                            porch_buffer* out, size_t count, bool reduction) {
+        return guarded([&] {
+            require(code != nullptr && code_size > 0, "code object is empty");
+            require(function != nullptr, "function name is null");
+            require(out != nullptr, "output buffer is null");
+            require(n_inputs >= 0 && (n_inputs == 0 || inputs != nullptr), "inputs are malformed");
+            std::vector<const hip_jit::device_buffer*> list;
+            for (int32_t i = 0; i < n_inputs; ++i)
+                list.push_back(inputs[i] == nullptr ? nullptr : &inputs[i]->handle);
+            const std::string_view bytes{static_cast<const char*>(code), code_size};
+            if (reduction)
+                hip_jit::launch_fused_reduction(bytes, function, list, out->handle, count);
+            else
+                hip_jit::launch_fused_elementwise(bytes, function, list, out->handle, count);
+        });
+    }
+} // namespace
+
+porch_status porch_launch_fused_elementwise(const void* code, size_t code_size,
+                                            const char* function,
+                                            const porch_buffer* const* inputs,
+                                            int32_t n_inputs, porch_buffer* out,
+                                            size_t count) {
+    return raw_launch(code, code_size, function, inputs, n_inputs, out, count, false);
+}
+
+porch_status porch_launch_fused_reduction(const void* code, size_t code_size,
+                                          const char* function,
+                                          const porch_buffer* const* inputs,
+                                          int32_t n_inputs, porch_buffer* out,
+                                          size_t count) {
+    return raw_launch(code, code_size, function, inputs, n_inputs, out, count, true);
+}
+
+porch_status porch_infer_shape(const porch_graph* graph, int64_t* shape, int32_t capacity,
+                               int32_t* rank, int32_t* is_scalar) {
+    return guarded([&] {
+        ir::graph g = ir::from_c(graph);
+        ir::infer(g);
+        const ir::node& root = g.at(g.root());
+        write_shape(root.out, shape, capacity, rank);
+        if (is_scalar) *is_scalar = root.is_scalar ? 1 : 0;
+    });
+}
+
+porch_status porch_materialize(const porch_graph* graph, const porch_buffer* const* inputs,
+                               int32_t n_inputs, porch_buffer** out, int64_t* out_shape,
+                               int32_t capacity, int32_t* out_rank) {
+    return guarded([&] {
+        const auto start = std::chrono::steady_clock::now();
+        require(out != nullptr, "output pointer is null");
+        *out = nullptr;
+        ir::graph g = validated(graph);
+        const ir::node& root = g.at(g.root());
+        if (root.is_scalar)
+            throw std::invalid_argument("scalar expression cannot materialize to a tensor");
+        require(n_inputs >= g.n_inputs, "graph needs more input buffers");
+        require(n_inputs == 0 || inputs != nullptr, "inputs are null");
+        const size_t count = ir::checked_numel(root.out);
+        write_shape(root.out, out_shape, capacity, out_rank);
+        auto* result = new porch_buffer();
+        if (count == 0) {
+            *out = result;
+            return;
+        }
+        try {
+            const ir::graph compacted = ir::compact(g);
+            bool hit = false;
+            std::shared_ptr<plan::graph_plan> p = plan::lookup(compacted, &hit);
+            std::vector<rt::buffer_state*> buffers;
+            for (int32_t i = 0; i < n_inputs; ++i) {
+                buffers.push_back(
+                    inputs[i] == nullptr
+                        ? nullptr
+                        : hip_jit::buffer_access::state(inputs[i]->handle).get()
+                );
+            }
+            std::shared_ptr<rt::buffer_state> state = plan::run(
+                *p, buffers,
+                [](size_t bytes) -> std::shared_ptr<rt::buffer_state> {
+                    return std::make_shared<hip_jit::device_buffer_state>(bytes);
+                }
+            );
+            result->handle = hip_jit::buffer_access::wrap(
+                std::static_pointer_cast<hip_jit::device_buffer_state>(state)
+            );
+            const double ms = rt::elapsed_ms(start);
+            std::scoped_lock lock{rt::counters_mutex()};
+            if (hit) {
+                rt::counters().plan_hits += 1;
+                rt::counters().last_hit_us = ms * 1000.0;
+            }
+            else {
+                rt::counters().plan_misses += 1;
+                rt::counters().last_miss_ms = ms;
+            }
+        }
+        catch (...) {
+            delete result;
+            throw;
+        }
+        *out = result;
+    });
+}
+
+porch_status porch_plan(const porch_graph* graph, int32_t compile, char* json, size_t capacity) {
+    return guarded([&] {
+        ir::graph g = validated(graph);
+        const ir::graph compacted = ir::compact(g);
+        int cus = 256;
+        if (hip_jit::is_available()) cus = rt::device().compute_units;
+        std::shared_ptr<plan::graph_plan> p = plan::build(compacted, cus);
+        if (compile) plan::compile(*p);
+        copy_text(p->describe(), json, capacity);
+    });
+}
+
+porch_status porch_plan_source(const porch_graph* graph, int32_t index, char* source,
+                               size_t capacity, size_t* length) {
+    return guarded([&] {
+        ir::graph g = validated(graph);
+        const ir::graph compacted = ir::compact(g);
+        std::shared_ptr<plan::graph_plan> p = plan::build(compacted, 256);
+        if (index < 0 || static_cast<size_t>(index) >= p->steps.size())
+            throw std::out_of_range("plan has no kernel with that index");
+        const std::string& text = p->steps[static_cast<size_t>(index)].code.source;
+        if (length) *length = text.size();
+        copy_text(text, source, capacity);
+    });
+}
+
+porch_status porch_get_jit_stats(porch_jit_stats* stats) {
+    return guarded([&] {
+        require(stats != nullptr, "stats is null");
+        std::scoped_lock lock{rt::counters_mutex()};
+        const rt::jit_counters& c = rt::counters();
+        stats->plan_hits = c.plan_hits;
+        stats->plan_misses = c.plan_misses;
+        stats->compiles = c.compiles;
+        stats->launches = c.launches;
+        stats->codegen_ms = c.codegen_ms;
+        stats->compile_ms = c.compile_ms;
+        stats->module_load_ms = c.module_load_ms;
+        stats->last_miss_ms = c.last_miss_ms;
+        stats->last_hit_us = c.last_hit_us;
+    });
+}
+
+porch_status porch_reset_jit_cache(void) {
+    return guarded([] {
+        plan::clear_cache();
+        rt::clear_caches();
+    });
+}
+
+porch_status porch_event_create(porch_event** out) {
+    return guarded([&] {
+        require(out != nullptr, "output pointer is null");
+        auto* e = new porch_event();
+        hip::error_t rc = hip::runtime().event_create_with_flags(&e->event, hip::event_default);
+        if (rc != hip::success) {
+            delete e;
+            hip::check(rc, "hipEventCreateWithFlags");
+        }
+        *out = e;
+    });
+}
+
+porch_status porch_event_record(porch_event* event) {
+    return guarded([&] {
+        require(event != nullptr, "event is null");
+        hip::check(
+            hip::runtime().event_record(event->event, rt::current_stream()->handle()),
+            "hipEventRecord"
+        );
+    });
+}
+
+porch_status porch_event_synchronize(porch_event* event) {
+    return guarded([&] {
+        require(event != nullptr, "event is null");
+        hip::check(hip::runtime().event_synchronize(event->event), "hipEventSynchronize");
+    });
+}
+
+porch_status porch_event_elapsed_ms(const porch_event* start, const porch_event* stop,
+                                    float* ms) {
+    return guarded([&] {
+        require(start != nullptr && stop != nullptr && ms != nullptr, "argument is null");
+        hip::check(hip::runtime().event_elapsed_time(ms, start->event, stop->event),
+                   "hipEventElapsedTime");
+    });
+}
+
+void porch_event_release(porch_event* event) {
+    if (event == nullptr) return;
+    try {
+        (void)hip::runtime().event_destroy(event->event);
+    }
+    catch (...) {
+    }
+    delete event;
+}
+
+porch_status porch_flush_caches(size_t bytes) {
+    return guarded([&] { rt::flush_caches(bytes); });
+}
+
+} // extern "C"

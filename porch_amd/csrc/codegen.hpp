@@ -1,0 +1,113 @@
+#pragma once
+
+// Emitters of gfx950 HIP source for fused regions.  Each emitter takes a
+// lowered kernel expression (lower.hpp) and produces one kernel with its
+// launch geometry.  Kernel classes:
+//
+//   pointwise.flat   wave64 grid loop, 4 outputs per lane with 128-bit loads
+//                    and stores wherever every leaf is unit-stride (or
+//                    invariant) along the innermost output dimension;
+//   pointwise.tiled  64x64 output tiles whose transposed leaves are read with
+//                    lanes along the leaf's contiguous dimension, staged in
+//                    LDS (padded rows, conflict-free) and written with lanes
+//                    along the output's contiguous dimension;
+//   pointwise.scalar one output per lane, any index map (div/mod allowed);
+//   row              one wave (or workgroup) per row: the row's leaves are
+//                    read once into registers, each row reduction is a
+//                    register fold plus a wave butterfly, and the outputs (or
+//                    the row's reduction) are written in the same pass;
+//   reduce.column    one lane per output, sequential fold over a non-last
+//                    axis with lanes along the contiguous output dimension;
+//   gemm             LDS-tiled v_mfma_f32_32x32x2f32 with the elementwise
+//                    epilogue applied to the accumulators before the store.
+
+#include "lower.hpp"
+
+#include <string>
+#include <vector>
+
+namespace porch::cg {
+
+    struct kernel_code {
+        std::string kind;
+        std::string name;
+        std::string source;
+        unsigned grid_x = 1;
+        unsigned grid_y = 1;
+        unsigned grid_z = 1;
+        unsigned block = 256;
+        int n_slots = 0; // kernel takes slot 0..n_slots-1, then `out`
+    };
+
+    // Largest element count of any tensor the kernel touches; decides
+    // between 32- and 64-bit index arithmetic.
+    struct index_width {
+        bool wide = false;
+        [[nodiscard]] const char* type() const {
+            return wide ? "long long" : "int";
+        }
+    };
+
+    struct pointwise_request {
+        const kexpr* expr = nullptr;
+        int root = -1;
+        std::vector<int64_t> shape; // output shape (kernel coordinates)
+        int n_slots = 0;
+        index_width width;
+    };
+
+    kernel_code emit_pointwise(const pointwise_request& request);
+
+    // Row programs: reductions over the last axis of `shape` consumed
+    // through broadcasts, then either an elementwise output over `shape`
+    // or a final reduction per row.
+    struct row_reduction {
+        bool is_max = false; // sum otherwise
+        int producer = -1;   // kexpr root of the reduced values
+    };
+    struct row_request {
+        const kexpr* expr = nullptr;
+        std::vector<int64_t> shape; // row space [rows..., L]
+        std::vector<row_reduction> reductions; // in dependency order
+        bool reduce_output = false; // output is one value per row
+        bool output_is_max = false;
+        int output = -1;            // kexpr root of the output values
+        int n_slots = 0;
+        index_width width;
+        int compute_units = 256;
+    };
+
+    kernel_code emit_row(const row_request& request);
+
+    struct column_reduce_request {
+        const kexpr* expr = nullptr;
+        int producer = -1;
+        std::vector<int64_t> shape; // producer shape
+        size_t axis = 0;            // reduced axis (not the last)
+        bool is_max = false;
+        int n_slots = 0;
+        index_width width;
+    };
+
+    kernel_code emit_column_reduce(const column_reduce_request& request);
+
+    // C = epilogue(A @ B) with A [M,K], B [K,N] given by element strides.
+    struct gemm_operand {
+        int slot = -1;
+        int64_t offset = 0;
+        int64_t stride_row = 0; // A: per m, B: per k
+        int64_t stride_col = 0; // A: per k, B: per n
+    };
+    struct gemm_request {
+        const kexpr* expr = nullptr;
+        int64_t m = 0, n = 0, k = 0;
+        gemm_operand a, b;
+        int epilogue = -1;        // kexpr over (m, n); row_value 0 = acc
+        int n_slots = 0;
+        index_width width;
+        int compute_units = 256;
+    };
+
+    kernel_code emit_gemm(const gemm_request& request);
+
+} // namespace porch::cg

@@ -1,0 +1,64 @@
+#pragma once
+
+// Emission of a kernel expression as straight-line HIP with common
+// subexpressions shared, `width` lanes of values per node (1 or 4), and
+// select nodes emitted as real branches so a branch's loads only run when
+// it is taken.  Arithmetic is IEEE binary32 exactly as written (kernels are
+// compiled with -ffp-contract=off); maximum/minimum keep the reference's
+// ternary NaN behaviour (reference src/tensor.cpp:677-682).
+
+#include "lower.hpp"
+
+#include <functional>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace porch::cg {
+
+    struct emitter {
+        const kexpr& k;
+        std::string& code;
+        std::string indent = "    ";
+        int width = 1;
+
+        // Values of a load node, one expression per lane (may emit
+        // statements first).
+        std::function<std::vector<std::string>(int id)> load;
+        // Optional override for any node (e.g. LDS-staged subtrees);
+        // returns an empty vector to fall through.
+        std::function<std::vector<std::string>(int id)> override_node;
+        // The value of row reduction `row` (uniform across lanes).
+        std::function<std::string(int row)> row_value;
+        // Condition text of a select (evaluated once; uniform across lanes).
+        std::function<std::string(const kcond& c)> condition;
+
+        emitter(const kexpr& expr, std::string& target, int lanes);
+
+        std::vector<std::string> emit(int id);
+        std::string fresh(const char* prefix);
+        void line(const std::string& text);
+
+      private:
+        std::vector<std::map<int, std::vector<std::string>>> frames_;
+        int counter_ = 0;
+        const std::vector<std::string>* find(int id) const;
+    };
+
+    // Index text of an affine/generic ival with coordinate q_d renamed
+    // through `names` (names[d] is the C expression for coordinate d).
+    std::string index_text(const ival& v, const std::vector<std::string>& names);
+
+    // Declarations `const T q{d} = ...;` decomposing a flat index over
+    // `shape` (only coordinates in `needed` are declared).
+    std::string decompose(const std::string& flat, const std::vector<int64_t>& shape,
+                          const std::vector<bool>& needed, const char* type,
+                          const std::string& indent);
+
+    // Which kernel coordinates any index or condition under `root` uses.
+    std::vector<bool> used_coordinates(const kexpr& k, int root, size_t rank);
+
+    std::string kernel_prologue(int n_slots, const char* index_type);
+    std::string kernel_params(int n_slots);
+
+} // namespace porch::cg

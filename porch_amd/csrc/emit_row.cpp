@@ -1,0 +1,409 @@
+// Row programs.  The reference materialises every nested reduction as its
+// own kernel (reference src/tensor.cpp:970-989) and reduces each output with
+// a 256-thread block and a shared-memory tree (896-962): softmax becomes
+// four launches and about four reads of the input.  A row program runs the
+// whole row-space graph in one kernel: one wave64 per row (a workgroup per
+// row for rows longer than 4096), the row's leaves read once into
+// registers, each reduction folded in registers and finished with a wave
+// butterfly (plus LDS across waves in workgroup mode), and the outputs - or
+// the row's final reduction - written in the same pass.
+
+#include "codegen.hpp"
+#include "emit_expr.hpp"
+
+#include <algorithm>
+#include <functional>
+#include <memory>
+#include <set>
+#include <stdexcept>
+
+namespace porch::cg {
+    namespace {
+
+        std::vector<std::string> coordinate_names(size_t rank) {
+            std::vector<std::string> names;
+            for (size_t d = 0; d < rank; ++d) names.push_back("q" + std::to_string(d));
+            return names;
+        }
+
+        bool depends_on_column(const kexpr& k, int root, size_t col) {
+            for (const int id : k.postorder(root)) {
+                const knode& n = k.at(id);
+                if (n.op == kop::load) {
+                    if (!n.index.is_affine) return true;
+                    if (n.index.w[col] != 0) return true;
+                }
+                if (n.op == kop::select) {
+                    if (!n.cond.lhs.is_affine || n.cond.lhs.w[col] != 0) return true;
+                }
+            }
+            return false;
+        }
+
+        bool row_invariant(const ival& x, size_t rank) {
+            if (!x.is_affine) return false;
+            for (size_t d = 0; d + 1 < rank; ++d) {
+                if (x.w[d] != 0) return false;
+            }
+            return true;
+        }
+
+        // Nodes under a select (either branch) from `root`.
+        void mark_under_select(const kexpr& k, int root, std::vector<char>& under) {
+            std::function<void(int, bool)> walk = [&](int id, bool inside) {
+                if (id < 0) return;
+                if (inside) {
+                    if (under[id]) return;
+                    under[id] = 1;
+                }
+                const knode& n = k.at(id);
+                const bool child_inside = inside || n.op == kop::select;
+                walk(n.a, child_inside);
+                walk(n.b, child_inside);
+            };
+            walk(root, false);
+        }
+
+    } // namespace
+
+    kernel_code emit_row(const row_request& r) {
+        const kexpr& k = *r.expr;
+        const size_t rank = r.shape.size();
+        const size_t col = rank - 1;
+        const int64_t length = r.shape[col];
+        std::vector<int64_t> row_shape(r.shape.begin(), r.shape.end() - 1);
+        const int64_t rows = ir::numel(row_shape);
+        const bool block_mode = length > 4096;
+        const int lanes = block_mode ? 256 : 64;
+
+        // Pass roots: each reduction's producer, then the output.
+        std::vector<int> pass_roots;
+        for (const row_reduction& red : r.reductions) pass_roots.push_back(red.producer);
+        pass_roots.push_back(r.output);
+        const size_t n_pass = pass_roots.size();
+
+        bool all_affine = true;
+        bool uniform_selects = true;
+        for (const int root : pass_roots) {
+            for (const int id : k.postorder(root)) {
+                const knode& n = k.at(id);
+                if (n.op == kop::load && !n.index.is_affine) all_affine = false;
+                if (n.op == kop::select &&
+                    (!n.cond.lhs.is_affine || n.cond.lhs.w[col] != 0))
+                    uniform_selects = false;
+            }
+        }
+        const int width = (all_affine && uniform_selects && length % 4 == 0) ? 4 : 1;
+        const int64_t per_chunk = static_cast<int64_t>(lanes) * width;
+        const int64_t chunks = (length + per_chunk - 1) / per_chunk;
+        const bool ragged = length % per_chunk != 0;
+
+        // Nodes under a select are never cached (their values exist only on
+        // the taken branch).
+        std::vector<char> under(k.nodes.size(), 0);
+        for (size_t p = 0; p < n_pass; ++p) mark_under_select(k, pass_roots[p], under);
+
+        // Row-invariant, column-varying loads are hoisted out of the row loop.
+        std::vector<int> hoisted;
+        const int64_t per_value = chunks * width;
+        const int64_t budget = 128; // cached floats per lane
+        if (rows > 1) {
+            std::set<int> seen;
+            for (const int root : pass_roots) {
+                for (const int id : k.postorder(root)) {
+                    const knode& n = k.at(id);
+                    if (n.op != kop::load || under[id] || seen.count(id)) continue;
+                    if (row_invariant(n.index, rank) && depends_on_column(k, id, col)) {
+                        hoisted.push_back(id);
+                        seen.insert(id);
+                    }
+                }
+            }
+            if (static_cast<int64_t>(hoisted.size()) * per_value > budget / 2) hoisted.clear();
+        }
+        auto is_hoisted = [&](int id) {
+            return std::find(hoisted.begin(), hoisted.end(), id) != hoisted.end();
+        };
+
+        // Register caches across passes.  Pass p walks its root; a
+        // column-varying node already computed by an earlier pass is read
+        // from its cache (and not descended into), so a value and its
+        // operands are never both kept.  `allow` limits what may be cached.
+        std::vector<int> cached;
+        std::vector<size_t> first_pass(k.nodes.size(), 0);
+        std::vector<size_t> last_pass(k.nodes.size(), 0);
+        auto plan_caches = [&](bool loads_only) {
+            cached.clear();
+            std::vector<int> computed(k.nodes.size(), -1);
+            std::vector<char> is_cached(k.nodes.size(), 0);
+            for (size_t p = 0; p < n_pass; ++p) {
+                std::vector<char> visited(k.nodes.size(), 0);
+                std::function<void(int)> walk = [&](int id) {
+                    if (id < 0 || visited[id]) return;
+                    visited[id] = 1;
+                    const knode& n = k.at(id);
+                    const bool cacheable =
+                        !under[id] && !is_hoisted(id) && n.op != kop::constant &&
+                        n.op != kop::row_value && depends_on_column(k, id, col) &&
+                        (!loads_only || n.op == kop::load);
+                    if (cacheable && computed[id] >= 0 && static_cast<size_t>(computed[id]) < p) {
+                        if (!is_cached[id]) {
+                            is_cached[id] = 1;
+                            cached.push_back(id);
+                            first_pass[id] = static_cast<size_t>(computed[id]);
+                        }
+                        last_pass[id] = p;
+                        return;
+                    }
+                    if (computed[id] < 0) computed[id] = static_cast<int>(p);
+                    walk(n.a);
+                    walk(n.b);
+                };
+                walk(pass_roots[p]);
+            }
+            // Peak number of cached values alive across a pass boundary.
+            int64_t peak = 0;
+            for (size_t b = 0; b + 1 < n_pass; ++b) {
+                int64_t live = 0;
+                for (const int id : cached)
+                    if (first_pass[id] <= b && last_pass[id] > b) ++live;
+                peak = std::max(peak, live);
+            }
+            return (peak + static_cast<int64_t>(hoisted.size())) * per_value <= budget;
+        };
+        if (!plan_caches(false) && !plan_caches(true)) cached.clear();
+
+        const int64_t rows_per_group = block_mode ? 1 : 4;
+        int64_t rows_per_wave = 1;
+        if (!hoisted.empty()) {
+            const int64_t target = static_cast<int64_t>(r.compute_units) * 8 * rows_per_group;
+            rows_per_wave = std::max<int64_t>(1, rows / std::max<int64_t>(target, 1));
+        }
+        const int64_t groups =
+            std::max<int64_t>(1, (rows + rows_per_group * rows_per_wave - 1) /
+                                     (rows_per_group * rows_per_wave));
+
+        kernel_code kc;
+        kc.kind = "row";
+        kc.name = "porch_row";
+        kc.n_slots = r.n_slots;
+        kc.block = 256;
+        kc.grid_x = static_cast<unsigned>(std::min<int64_t>(groups, int64_t{1} << 22));
+        const char* T = r.width.type();
+        const std::vector<std::string> names = coordinate_names(rank);
+        const std::string qc = "q" + std::to_string(col);
+
+        std::string& s = kc.source;
+        s = kernel_prologue(r.n_slots, T);
+        s += "__device__ __forceinline__ float porch_max(float a, float b) { return a > b ? a : b; }\n";
+        s += "extern \"C\" __global__ void __launch_bounds__(256) porch_row(" +
+             kernel_params(r.n_slots) + ") {\n";
+        s += "    const int lane = threadIdx.x & 63;\n";
+        s += "    const int wave = threadIdx.x >> 6;\n";
+        if (block_mode) {
+            s += "    __shared__ float red[4];\n";
+            s += "    const int tl = threadIdx.x;\n";
+        }
+        else {
+            s += "    const int tl = lane;\n";
+        }
+        const std::string W = std::to_string(width);
+        const std::string NC = std::to_string(chunks);
+        for (const int id : cached) {
+            s += "    float c" + std::to_string(id) + "[" + NC + "][" + W + "];\n";
+        }
+
+        auto chunk_open = [&](std::string& code, const std::string& indent) {
+            code += indent + "#pragma unroll\n";
+            code += indent + "for (int j = 0; j < " + NC + "; ++j) {\n";
+            code += indent + "    const " + T + " " + qc + " = (" + T + ")(j * " +
+                    std::to_string(lanes) + " + tl) * " + W + ";\n";
+            if (ragged) code += indent + "    if (" + qc + " < " + std::to_string(length) + ") {\n";
+        };
+        auto chunk_close = [&](std::string& code, const std::string& indent) {
+            if (ragged) code += indent + "    }\n";
+            code += indent + "}\n";
+        };
+
+        auto load_text = [&](emitter& em, int id) {
+            const knode& n = k.at(id);
+            const std::string base = "a" + std::to_string(n.slot);
+            std::vector<std::string> out(static_cast<size_t>(width));
+            if (width == 1) {
+                out[0] = base + "[" + index_text(n.index, names) + "]";
+                return out;
+            }
+            const int64_t step = n.index.w[col];
+            const std::string idx = index_text(n.index, names);
+            if (step == 0) {
+                const std::string v = em.fresh("u");
+                em.line("const float " + v + " = " + base + "[" + idx + "];");
+                for (auto& lane_value : out) lane_value = v;
+                return out;
+            }
+            bool aligned = step == 1 && n.index.c0 % 4 == 0;
+            for (size_t d = 0; d + 1 < rank && aligned; ++d) {
+                if (n.index.w[d] % 4 != 0) aligned = false;
+            }
+            if (aligned) {
+                const std::string v = em.fresh("w");
+                em.line("const float4 " + v + " = *reinterpret_cast<const float4*>(" + base +
+                        " + " + idx + ");");
+                return std::vector<std::string>{v + ".x", v + ".y", v + ".z", v + ".w"};
+            }
+            const std::string p = em.fresh("p");
+            em.line("const float* " + p + " = " + base + " + " + idx + ";");
+            for (int e = 0; e < width; ++e) out[e] = p + "[" + std::to_string(step * e) + "]";
+            return out;
+        };
+
+        // Hoisted row-invariant loads.
+        for (const int id : hoisted) {
+            s += "    float h" + std::to_string(id) + "[" + NC + "][" + W + "];\n";
+        }
+        if (!hoisted.empty()) {
+            std::string code;
+            chunk_open(code, "    ");
+            std::string body;
+            emitter em(k, body, width);
+            em.indent = "        ";
+            for (const int id : hoisted) {
+                const std::vector<std::string> v = load_text(em, id);
+                for (int e = 0; e < width; ++e)
+                    em.line("h" + std::to_string(id) + "[j][" + std::to_string(e) +
+                            "] = " + v[e] + ";");
+            }
+            code += body;
+            chunk_close(code, "    ");
+            s += code;
+        }
+
+        const std::string row_step = std::to_string(rows_per_group);
+        if (block_mode) {
+            s += "    for (idx_t row = blockIdx.x; row < " + std::to_string(rows) +
+                 "; row += gridDim.x) {\n";
+        }
+        else {
+            s += "    for (idx_t row = (idx_t)blockIdx.x * 4 + wave; row < " +
+                 std::to_string(rows) + "; row += (idx_t)gridDim.x * 4) {\n";
+        }
+        {
+            std::vector<bool> needed(row_shape.size(), true);
+            s += decompose("row", row_shape, needed, T, "        ");
+        }
+
+        auto reduce_lanes = [&](const std::string& acc, bool is_max) {
+            std::string code;
+            const std::string op = is_max ? "porch_max(" + acc + ", __shfl_xor(" + acc + ", m, 64))"
+                                          : acc + " + __shfl_xor(" + acc + ", m, 64)";
+            code += "        #pragma unroll\n";
+            code += "        for (int m = 32; m >= 1; m >>= 1) " + acc + " = " + op + ";\n";
+            if (block_mode) {
+                code += "        if (lane == 0) red[wave] = " + acc + ";\n";
+                code += "        __syncthreads();\n";
+                if (is_max)
+                    code += "        " + acc + " = porch_max(porch_max(red[0], red[1]), porch_max(red[2], red[3]));\n";
+                else
+                    code += "        " + acc + " = (red[0] + red[1]) + (red[2] + red[3]);\n";
+                code += "        __syncthreads();\n";
+            }
+            return code;
+        };
+
+        auto make_emitter = [&](std::string& body, size_t pass) {
+            auto em = std::make_unique<emitter>(k, body, width);
+            em->indent = ragged ? "                " : "            ";
+            emitter* self = em.get();
+            em->load = [&, self](int id) {
+                for (const int h : hoisted) {
+                    if (h == id) {
+                        std::vector<std::string> out;
+                        for (int e = 0; e < width; ++e)
+                            out.push_back("h" + std::to_string(id) + "[j][" + std::to_string(e) + "]");
+                        return out;
+                    }
+                }
+                return load_text(*self, id);
+            };
+            em->override_node = [&, pass](int id) -> std::vector<std::string> {
+                for (const int c : cached) {
+                    if (c == id && first_pass[id] < pass) {
+                        std::vector<std::string> out;
+                        for (int e = 0; e < width; ++e)
+                            out.push_back("c" + std::to_string(id) + "[j][" + std::to_string(e) + "]");
+                        return out;
+                    }
+                }
+                return {};
+            };
+            em->row_value = [](int row) { return "rv" + std::to_string(row); };
+            em->condition = [&](const kcond& c) {
+                return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
+            };
+            return em;
+        };
+
+        auto store_caches = [&](emitter& em, size_t pass, int root) {
+            for (const int c : cached) {
+                if (first_pass[c] != pass) continue;
+                bool reached = false;
+                for (const int id : k.postorder(root)) reached = reached || id == c;
+                if (!reached) continue;
+                const std::vector<std::string> v = em.emit(c);
+                for (int e = 0; e < width; ++e)
+                    em.line("c" + std::to_string(c) + "[j][" + std::to_string(e) + "] = " + v[e] + ";");
+            }
+        };
+
+        auto fold_pass = [&](size_t pass, int root, bool is_max, const std::string& acc) {
+            std::string code;
+            code += "        float " + acc + " = " + (is_max ? "-PORCH_FLT_MAX" : "0.0f") + ";\n";
+            chunk_open(code, "        ");
+            std::string body;
+            auto em = make_emitter(body, pass);
+            const std::vector<std::string> v = em->emit(root);
+            store_caches(*em, pass, root);
+            for (int e = 0; e < width; ++e) {
+                if (is_max) em->line(acc + " = porch_max(" + acc + ", " + v[e] + ");");
+                else em->line(acc + " += " + v[e] + ";");
+            }
+            code += body;
+            chunk_close(code, "        ");
+            code += reduce_lanes(acc, is_max);
+            return code;
+        };
+
+        for (size_t i = 0; i < r.reductions.size(); ++i) {
+            const std::string acc = "acc" + std::to_string(i);
+            s += fold_pass(i, r.reductions[i].producer, r.reductions[i].is_max, acc);
+            s += "        const float rv" + std::to_string(i) + " = " + acc + ";\n";
+        }
+        const size_t out_pass = n_pass - 1;
+        if (r.reduce_output) {
+            s += fold_pass(out_pass, r.output, r.output_is_max, "acc_out");
+            if (block_mode) s += "        if (threadIdx.x == 0) out[row] = acc_out;\n";
+            else s += "        if (lane == 0) out[row] = acc_out;\n";
+        }
+        else {
+            std::string code;
+            chunk_open(code, "        ");
+            std::string body;
+            auto em = make_emitter(body, out_pass);
+            const std::vector<std::string> v = em->emit(r.output);
+            const std::string base = "row * " + std::to_string(length) + " + " + qc;
+            if (width == 4) {
+                em->line("*reinterpret_cast<float4*>(out + " + base + ") = make_float4(" + v[0] +
+                         ", " + v[1] + ", " + v[2] + ", " + v[3] + ");");
+            }
+            else {
+                em->line("out[" + base + "] = " + v[0] + ";");
+            }
+            code += body;
+            chunk_close(code, "        ");
+            s += code;
+        }
+        s += "    }\n}\n";
+        return kc;
+    }
+
+} // namespace porch::cg

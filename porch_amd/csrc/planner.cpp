@@ -1,0 +1,562 @@
+#include "planner.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <functional>
+#include <map>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+#include <unordered_map>
+
+namespace porch::plan {
+    namespace {
+
+        bool is_elementwise(ir::op kind) {
+            return ir::is_elementwise_binary(kind) || kind == ir::op::exp ||
+                   kind == ir::op::reciprocal;
+        }
+
+        bool is_boundary(ir::op kind) {
+            return ir::is_reduction(kind) || kind == ir::op::matmul;
+        }
+
+        struct builder {
+            const ir::graph& g;
+            graph_plan& plan;
+            int compute_units;
+            std::map<int, int> temp_of;
+            cg::index_width width;
+
+            builder(const ir::graph& graph, graph_plan& target, int cus)
+                : g(graph), plan(target), compute_units(cus) {
+                int64_t largest = 0;
+                for (const ir::node& n : g.nodes) {
+                    largest = std::max(largest, ir::numel(n.out));
+                    if (n.kind == ir::op::input)
+                        largest = std::max(largest, ir::numel(n.shape));
+                    if (n.kind == ir::op::slice) {
+                        int64_t last = n.offset;
+                        for (size_t d = 0; d < n.shape.size(); ++d)
+                            last += std::max<int64_t>(n.shape[d] - 1, 0) * n.strides[d];
+                        largest = std::max(largest, last + 1);
+                    }
+                }
+                width.wide = largest >= (int64_t{1} << 30);
+            }
+
+            [[nodiscard]] int n_slots() const {
+                return g.n_inputs + static_cast<int>(plan.temp_elems.size());
+            }
+
+            void bind_inputs(cg::lowering& low) const {
+                for (int i = 0; i < g.n_inputs; ++i) low.input_slot[static_cast<size_t>(i)] = i;
+                for (const auto& [node, temp] : temp_of) {
+                    cg::binding b;
+                    b.what = cg::binding::kind::slot;
+                    b.slot = g.n_inputs + temp;
+                    low.bound[node] = b;
+                }
+            }
+
+            // Matmul / reduction nodes reachable from `id` through pointwise
+            // and view nodes, excluding `skip` and materialised nodes.
+            void boundaries(int id, std::set<int>& found, const std::set<int>& skip,
+                            bool is_root) {
+                std::set<int> seen;
+                std::function<void(int, bool)> walk = [&](int x, bool root) {
+                    if (x < 0 || seen.count(x)) return;
+                    seen.insert(x);
+                    if (temp_of.count(x)) return;
+                    if (skip.count(x)) return;
+                    const ir::node& n = g.at(x);
+                    if (!root && is_boundary(n.kind)) {
+                        found.insert(x);
+                        return;
+                    }
+                    walk(n.lhs, false);
+                    walk(n.rhs, false);
+                };
+                walk(id, is_root);
+            }
+
+            arg_ref ensure_temp(int id) {
+                auto found = temp_of.find(id);
+                if (found != temp_of.end()) return {arg_ref::kind::temp, found->second};
+                const int t = static_cast<int>(plan.temp_elems.size());
+                plan.temp_elems.push_back(ir::numel(g.at(id).out));
+                arg_ref dest{arg_ref::kind::temp, t};
+                emit(id, dest);
+                temp_of[id] = t;
+                return dest;
+            }
+
+            void add_step(cg::kernel_code code, arg_ref dest) {
+                step s;
+                s.code = std::move(code);
+                s.dest = dest;
+                plan.steps.push_back(std::move(s));
+            }
+
+            // ---------------------------------------------------------
+            // gemm
+            // ---------------------------------------------------------
+            int epilogue_matmul(int id) {
+                // The single matmul reached from `id` through elementwise
+                // nodes only (so the epilogue runs at the matmul's (m, n)).
+                std::set<int> found;
+                std::set<int> seen;
+                std::function<void(int)> walk = [&](int x) {
+                    if (x < 0 || seen.count(x) || temp_of.count(x)) return;
+                    seen.insert(x);
+                    const ir::node& n = g.at(x);
+                    if (n.kind == ir::op::matmul) {
+                        found.insert(x);
+                        return;
+                    }
+                    if (!is_elementwise(n.kind)) return;
+                    walk(n.lhs);
+                    walk(n.rhs);
+                };
+                walk(id);
+                if (found.size() != 1) return -1;
+                const int mm = *found.begin();
+                if (g.at(mm).out != g.at(id).out) return -1;
+                // Every path to the matmul must be elementwise: a view in
+                // between would read the accumulator at other coordinates.
+                std::set<std::pair<int, bool>> visited;
+                bool via_view = false;
+                std::function<void(int, bool)> check = [&](int x, bool view) {
+                    if (x < 0 || temp_of.count(x) || via_view) return;
+                    if (x == mm) {
+                        if (view) via_view = true;
+                        return;
+                    }
+                    const ir::node& n = g.at(x);
+                    if (is_boundary(n.kind)) return;
+                    const bool next = view || !is_elementwise(n.kind);
+                    if (!visited.insert({x, view}).second) return;
+                    check(n.lhs, next);
+                    check(n.rhs, next);
+                };
+                check(id, false);
+                if (via_view) return -1;
+                return mm;
+            }
+
+            bool pure_view_of_input(int id) {
+                const ir::node& n = g.at(id);
+                if (temp_of.count(id)) return true;
+                if (n.kind == ir::op::input) return true;
+                if (n.kind == ir::op::slice || n.kind == ir::op::reshape ||
+                    n.kind == ir::op::unsqueeze || n.kind == ir::op::transpose ||
+                    n.kind == ir::op::broadcast)
+                    return pure_view_of_input(n.lhs);
+                return false;
+            }
+
+            cg::gemm_operand operand(int id, int64_t rows, int64_t cols) {
+                if (pure_view_of_input(id)) {
+                    cg::kexpr k;
+                    cg::lowering low(g, k, {rows, cols});
+                    bind_inputs(low);
+                    const int root = low.at(id, low.identity());
+                    const cg::knode& n = k.at(root);
+                    if (n.op == cg::kop::load && n.index.is_affine) {
+                        cg::gemm_operand op;
+                        op.slot = n.slot;
+                        op.offset = n.index.c0;
+                        op.stride_row = n.index.w[0];
+                        op.stride_col = n.index.w[1];
+                        return op;
+                    }
+                }
+                const arg_ref t = ensure_temp(id);
+                cg::gemm_operand op;
+                op.slot = g.n_inputs + t.index;
+                op.offset = 0;
+                op.stride_row = cols;
+                op.stride_col = 1;
+                return op;
+            }
+
+            bool try_gemm(int id, arg_ref dest) {
+                const int mm = epilogue_matmul(id);
+                if (mm < 0) return false;
+                const ir::node& m = g.at(mm);
+                const int64_t M = g.at(m.lhs).out[0];
+                const int64_t K = g.at(m.lhs).out[1];
+                const int64_t N = g.at(m.rhs).out[1];
+                cg::gemm_request r;
+                r.m = M;
+                r.n = N;
+                r.k = K;
+                r.a = operand(m.lhs, M, K);
+                r.b = operand(m.rhs, K, N);
+                // Other boundaries in the epilogue region.
+                std::set<int> others;
+                boundaries(id, others, {mm}, true);
+                for (const int b : others) ensure_temp(b);
+                cg::kexpr k;
+                cg::lowering low(g, k, {M, N});
+                bind_inputs(low);
+                cg::binding acc;
+                acc.what = cg::binding::kind::row_value;
+                acc.row = 0;
+                low.bound[mm] = acc;
+                r.epilogue = low.at(id, low.identity());
+                r.expr = &k;
+                r.n_slots = n_slots();
+                r.width = width;
+                r.compute_units = compute_units;
+                add_step(cg::emit_gemm(r), dest);
+                return true;
+            }
+
+            // ---------------------------------------------------------
+            // row programs
+            // ---------------------------------------------------------
+            // Collects the row reductions under `id` (through elementwise
+            // and view nodes).  Every reduction must reduce the last axis of
+            // `row_shape` with keepdim and be consumed directly by a
+            // broadcast back to `row_shape` that sits on an elementwise-only
+            // path from a row-space root.  Returns false if the region does
+            // not have that form.
+            bool collect_row(int id, const std::vector<int64_t>& row_shape,
+                             std::set<int>& reductions,
+                             std::set<std::pair<int, bool>>& seen,
+                             bool elementwise_path) {
+                if (id < 0 || temp_of.count(id)) return true;
+                // A node is checked once per kind of path that reaches it:
+                // a reduction reached through a view must not be bound to
+                // the row value.
+                if (!seen.insert({id, elementwise_path}).second) return true;
+                const ir::node& n = g.at(id);
+                if (n.kind == ir::op::matmul) return true; // materialised
+                if (ir::is_reduction(n.kind)) return false; // not via broadcast
+                if (n.kind == ir::op::broadcast && elementwise_path &&
+                    n.out == row_shape) {
+                    const ir::node& child = g.at(n.lhs);
+                    if (ir::is_reduction(child.kind) && !temp_of.count(n.lhs)) {
+                        const ir::node& src = g.at(child.lhs);
+                        const size_t last = row_shape.size() - 1;
+                        if (!child.keepdim || src.out != row_shape ||
+                            static_cast<size_t>(child.axis) != last)
+                            return false;
+                        if (!reductions.count(n.lhs)) {
+                            reductions.insert(n.lhs);
+                            std::set<std::pair<int, bool>> inner_seen;
+                            if (!collect_row(child.lhs, row_shape, reductions,
+                                             inner_seen, true))
+                                return false;
+                        }
+                        return true;
+                    }
+                }
+                const bool keeps = is_elementwise(n.kind);
+                if (n.lhs >= 0 &&
+                    !collect_row(n.lhs, row_shape, reductions, seen,
+                                 elementwise_path && keeps))
+                    return false;
+                if (n.rhs >= 0 &&
+                    !collect_row(n.rhs, row_shape, reductions, seen,
+                                 elementwise_path && keeps))
+                    return false;
+                return true;
+            }
+
+            bool try_row(int id, arg_ref dest) {
+                const ir::node& n = g.at(id);
+                const bool reduce_output = ir::is_reduction(n.kind);
+                const int producer = reduce_output ? n.lhs : id;
+                const std::vector<int64_t> row_shape = g.at(producer).out;
+                if (row_shape.empty()) return false;
+                if (reduce_output &&
+                    static_cast<size_t>(n.axis) != row_shape.size() - 1)
+                    return false;
+                std::set<int> reductions;
+                std::set<std::pair<int, bool>> seen;
+                if (!collect_row(producer, row_shape, reductions, seen, true)) return false;
+                if (reductions.empty() && !reduce_output) return false;
+                // Matmuls inside become temporaries first.
+                std::set<int> mms;
+                {
+                    std::set<int> all;
+                    boundaries(producer, all, {}, false);
+                    for (const int r : reductions) boundaries(g.at(r).lhs, all, {}, false);
+                    for (const int b : all) {
+                        if (g.at(b).kind == ir::op::matmul) mms.insert(b);
+                        else if (!reductions.count(b)) return false;
+                    }
+                }
+                for (const int mm : mms) ensure_temp(mm);
+
+                cg::kexpr k;
+                cg::lowering low(g, k, row_shape);
+                bind_inputs(low);
+                std::vector<int> order(reductions.begin(), reductions.end());
+                std::sort(order.begin(), order.end());
+                for (size_t i = 0; i < order.size(); ++i) {
+                    cg::binding b;
+                    b.what = cg::binding::kind::row_value;
+                    b.row = static_cast<int>(i);
+                    low.bound[order[i]] = b;
+                }
+                cg::row_request r;
+                r.expr = &k;
+                r.shape = row_shape;
+                for (const int red : order) {
+                    cg::row_reduction rr;
+                    rr.is_max = g.at(red).kind == ir::op::max;
+                    // Lower the producer without the reduction's own binding
+                    // in scope for itself (bindings only replace the
+                    // reduction node, not its operand).
+                    rr.producer = low.at(g.at(red).lhs, low.identity());
+                    r.reductions.push_back(rr);
+                }
+                r.reduce_output = reduce_output;
+                r.output_is_max = reduce_output && n.kind == ir::op::max;
+                r.output = low.at(producer, low.identity());
+                r.n_slots = n_slots();
+                r.width = width;
+                r.compute_units = compute_units;
+                add_step(cg::emit_row(r), dest);
+                return true;
+            }
+
+            // ---------------------------------------------------------
+            // other reductions, pointwise
+            // ---------------------------------------------------------
+            void emit_reduction(int id, arg_ref dest) {
+                const ir::node& n = g.at(id);
+                std::set<int> inner;
+                boundaries(n.lhs, inner, {}, false);
+                for (const int b : inner) ensure_temp(b);
+                const std::vector<int64_t>& shape = g.at(n.lhs).out;
+                cg::kexpr k;
+                cg::lowering low(g, k, shape);
+                bind_inputs(low);
+                const int producer = low.at(n.lhs, low.identity());
+                if (static_cast<size_t>(n.axis) == shape.size() - 1) {
+                    cg::row_request r;
+                    r.expr = &k;
+                    r.shape = shape;
+                    r.reduce_output = true;
+                    r.output_is_max = n.kind == ir::op::max;
+                    r.output = producer;
+                    r.n_slots = n_slots();
+                    r.width = width;
+                    r.compute_units = compute_units;
+                    add_step(cg::emit_row(r), dest);
+                    return;
+                }
+                cg::column_reduce_request r;
+                r.expr = &k;
+                r.producer = producer;
+                r.shape = shape;
+                r.axis = static_cast<size_t>(n.axis);
+                r.is_max = n.kind == ir::op::max;
+                r.n_slots = n_slots();
+                r.width = width;
+                add_step(cg::emit_column_reduce(r), dest);
+            }
+
+            void emit_pointwise(int id, arg_ref dest) {
+                std::set<int> inner;
+                boundaries(id, inner, {}, true);
+                for (const int b : inner) ensure_temp(b);
+                const std::vector<int64_t>& shape = g.at(id).out;
+                cg::kexpr k;
+                cg::lowering low(g, k, shape);
+                bind_inputs(low);
+                cg::pointwise_request r;
+                r.expr = &k;
+                r.root = low.at(id, low.identity());
+                r.shape = shape;
+                r.n_slots = n_slots();
+                r.width = width;
+                add_step(cg::emit_pointwise(r), dest);
+            }
+
+            void emit(int id, arg_ref dest) {
+                const ir::node& n = g.at(id);
+                if (ir::numel(n.out) == 0) return;
+                if (try_gemm(id, dest)) return;
+                if (try_row(id, dest)) return;
+                if (ir::is_reduction(n.kind)) {
+                    emit_reduction(id, dest);
+                    return;
+                }
+                emit_pointwise(id, dest);
+            }
+        };
+
+        struct plan_cache {
+            std::mutex mutex;
+            std::unordered_map<std::string, std::shared_ptr<graph_plan>> entries;
+        };
+        plan_cache& cache() {
+            static plan_cache* instance = new plan_cache();
+            return *instance;
+        }
+
+        int planning_compute_units() {
+            try {
+                return rt::device().compute_units;
+            }
+            catch (...) {
+                return 256; // MI355X
+            }
+        }
+
+    } // namespace
+
+    std::string graph_plan::describe() const {
+        std::ostringstream os;
+        os << "{\"out_shape\":[";
+        for (size_t i = 0; i < out_shape.size(); ++i) os << (i ? "," : "") << out_shape[i];
+        os << "],\"temps\":[";
+        for (size_t i = 0; i < temp_elems.size(); ++i) os << (i ? "," : "") << temp_elems[i];
+        os << "],\"kernels\":[";
+        for (size_t i = 0; i < steps.size(); ++i) {
+            const step& s = steps[i];
+            os << (i ? "," : "") << "{\"kind\":\"" << s.code.kind << "\",\"name\":\""
+               << s.code.name << "\",\"grid\":[" << s.code.grid_x << ","
+               << s.code.grid_y << "," << s.code.grid_z << "],\"block\":" << s.code.block
+               << ",\"slots\":" << s.code.n_slots << ",\"dest\":\""
+               << (s.dest.what == arg_ref::kind::output
+                       ? std::string("output")
+                       : "temp" + std::to_string(s.dest.index))
+               << "\",\"source_bytes\":" << s.code.source.size()
+               << ",\"code_bytes\":" << (s.object ? s.object->bytes.size() : 0) << "}";
+        }
+        os << "],\"codegen_ms\":" << codegen_ms << ",\"compile_ms\":" << compile_ms << "}";
+        return os.str();
+    }
+
+    std::shared_ptr<graph_plan> build(const ir::graph& g, int compute_units) {
+        const auto start = std::chrono::steady_clock::now();
+        auto plan = std::make_shared<graph_plan>();
+        const ir::node& root = g.at(g.root());
+        plan->out_shape = root.out;
+        plan->n_inputs = g.n_inputs;
+        plan->input_elems.assign(static_cast<size_t>(g.n_inputs), 0);
+        for (const ir::node& n : g.nodes) {
+            if (n.kind == ir::op::input) {
+                int64_t& need = plan->input_elems[static_cast<size_t>(n.input)];
+                need = std::max(need, ir::numel(n.shape));
+            }
+        }
+        builder b(g, *plan, compute_units);
+        if (ir::numel(root.out) > 0) b.emit(g.root(), {arg_ref::kind::output, 0});
+        plan->codegen_ms = rt::elapsed_ms(start);
+        return plan;
+    }
+
+    void compile(graph_plan& plan) {
+        const auto start = std::chrono::steady_clock::now();
+        for (step& s : plan.steps) {
+            if (!s.object) s.object = rt::compile(s.code.source, {});
+        }
+        plan.compile_ms = rt::elapsed_ms(start);
+    }
+
+    std::shared_ptr<graph_plan> lookup(const ir::graph& g, bool* hit) {
+        const std::string key = ir::canonical_key(g);
+        {
+            std::scoped_lock lock{cache().mutex};
+            auto found = cache().entries.find(key);
+            if (found != cache().entries.end()) {
+                if (hit) *hit = true;
+                return found->second;
+            }
+        }
+        if (hit) *hit = false;
+        std::shared_ptr<graph_plan> plan = build(g, planning_compute_units());
+        compile(*plan);
+        {
+            std::scoped_lock lock{rt::counters_mutex()};
+            rt::counters().codegen_ms += plan->codegen_ms;
+        }
+        std::scoped_lock lock{cache().mutex};
+        auto [it, inserted] = cache().entries.emplace(key, plan);
+        return it->second;
+    }
+
+    void clear_cache() {
+        std::scoped_lock lock{cache().mutex};
+        cache().entries.clear();
+    }
+
+    std::shared_ptr<rt::buffer_state> run(
+        graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
+        const std::function<std::shared_ptr<rt::buffer_state>(size_t)>& allocate
+    ) {
+        if (static_cast<int>(inputs.size()) < plan.n_inputs) {
+            throw std::invalid_argument("graph needs more input buffers");
+        }
+        for (int i = 0; i < plan.n_inputs; ++i) {
+            const int64_t need = plan.input_elems[static_cast<size_t>(i)];
+            const rt::buffer_state* in = inputs[static_cast<size_t>(i)];
+            const size_t have = in == nullptr ? 0 : in->bytes;
+            if (need > 0 && have < static_cast<size_t>(need) * sizeof(float)) {
+                throw std::invalid_argument(
+                    have == 0 ? "GPU kernel input is empty"
+                              : "input device buffer is too small"
+                );
+            }
+        }
+        const size_t out_bytes =
+            static_cast<size_t>(ir::numel(plan.out_shape)) * sizeof(float);
+        if (out_bytes == 0) return allocate(0);
+
+        std::shared_ptr<rt::stream> s = rt::current_stream();
+        {
+            std::scoped_lock lock{plan.load_mutex};
+            if (!plan.loaded) {
+                for (step& st : plan.steps)
+                    st.kernel = rt::load_kernel(st.object, st.code.name);
+                plan.loaded = true;
+            }
+        }
+        for (int i = 0; i < plan.n_inputs; ++i) {
+            rt::buffer_state* in = inputs[static_cast<size_t>(i)];
+            if (in != nullptr && in->bytes > 0) in->before_read(s);
+        }
+        std::shared_ptr<rt::buffer_state> out = allocate(out_bytes);
+        std::vector<std::shared_ptr<rt::buffer_state>> temps;
+        temps.reserve(plan.temp_elems.size());
+        for (const int64_t elems : plan.temp_elems) {
+            temps.push_back(std::make_shared<rt::buffer_state>(
+                static_cast<size_t>(std::max<int64_t>(elems, 1)) * sizeof(float)
+            ));
+        }
+        std::vector<void*> pointers;
+        std::vector<void*> params;
+        for (const step& st : plan.steps) {
+            const int slots = st.code.n_slots;
+            pointers.assign(static_cast<size_t>(slots) + 1, nullptr);
+            for (int i = 0; i < slots; ++i) {
+                if (i < plan.n_inputs) {
+                    rt::buffer_state* in = inputs[static_cast<size_t>(i)];
+                    pointers[i] = in == nullptr ? nullptr : in->ptr;
+                }
+                else {
+                    const size_t t = static_cast<size_t>(i - plan.n_inputs);
+                    pointers[i] = t < temps.size() ? temps[t]->ptr : nullptr;
+                }
+            }
+            pointers[slots] = st.dest.what == arg_ref::kind::output
+                                  ? out->ptr
+                                  : temps[static_cast<size_t>(st.dest.index)]->ptr;
+            params.assign(pointers.size(), nullptr);
+            for (size_t i = 0; i < pointers.size(); ++i) params[i] = &pointers[i];
+            rt::launch(st.kernel, st.code.grid_x, st.code.grid_y, st.code.grid_z,
+                       st.code.block, 0, params.data(), *s);
+        }
+        out->after_write(s);
+        // Temporaries are freed stream-ordered after the launches above.
+        return out;
+    }
+
+} // namespace porch::plan

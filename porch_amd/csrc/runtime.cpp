@@ -1,0 +1,425 @@
+#include "runtime.hpp"
+
+#include "porch/hip_jit.hpp"
+
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <stdexcept>
+#include <unordered_map>
+
+namespace porch::rt {
+    namespace {
+
+        struct device_state {
+            device_info info;
+        };
+
+        device_state* init_device() {
+            const hip::api& h = hip::runtime();
+            hip::check(h.init(0), "hipInit");
+            int count = 0;
+            hip::check(h.get_device_count(&count), "hipGetDeviceCount");
+            if (count < 1) {
+                throw std::runtime_error(
+                    "porch GPU execution requires a HIP device"
+                );
+            }
+            auto* state = new device_state();
+            device_info& info = state->info;
+            info.ordinal = 0;
+            hip::check(h.set_device(0), "hipSetDevice");
+            hip::check(
+                h.device_get_attribute(
+                    &info.compute_units, hip::attr_multiprocessor_count, 0
+                ),
+                "hipDeviceGetAttribute"
+            );
+            hip::check(
+                h.device_get_attribute(&info.clock_khz, hip::attr_clock_rate, 0),
+                "hipDeviceGetAttribute"
+            );
+            (void)h.device_get_attribute(
+                &info.l2_bytes, hip::attr_l2_cache_size, 0
+            );
+            std::vector<char> props(hip::device_prop_size + 1024, 0);
+            if (h.get_device_properties(props.data(), 0) == hip::success) {
+                const char* name = props.data() + hip::device_prop_arch_offset;
+                info.arch.assign(name, strnlen(name, 256));
+            }
+            // Keep freed blocks in the pool: stream-ordered reuse without
+            // returning memory to the driver at every synchronisation.
+            hip::mem_pool_t pool = nullptr;
+            if (h.device_get_default_mem_pool(&pool, 0) == hip::success &&
+                pool != nullptr) {
+                uint64_t threshold = std::numeric_limits<uint64_t>::max();
+                (void)h.mem_pool_set_attribute(
+                    pool, hip::mem_pool_attr_release_threshold, &threshold
+                );
+            }
+            return state;
+        }
+
+        device_state& device_singleton() {
+            static device_state* instance = init_device();
+            return *instance;
+        }
+
+        struct rtc_program {
+            hip::rtc_program_t program = nullptr;
+            ~rtc_program() {
+                if (program != nullptr)
+                    (void)hip::compiler().rtc_destroy_program(&program);
+            }
+        };
+
+        std::string program_log(hip::rtc_program_t program) {
+            const hip::api& c = hip::compiler();
+            size_t size = 0;
+            hip::check_rtc(
+                c.rtc_get_program_log_size(program, &size),
+                "hiprtcGetProgramLogSize"
+            );
+            if (size == 0) return {};
+            std::string log(size, '\0');
+            hip::check_rtc(
+                c.rtc_get_program_log(program, log.data()),
+                "hiprtcGetProgramLog"
+            );
+            while (!log.empty() && log.back() == '\0') log.pop_back();
+            return log;
+        }
+
+        struct code_cache {
+            std::mutex mutex;
+            std::unordered_map<std::string, std::shared_ptr<const code_object>>
+                entries;
+        };
+        code_cache& codes() {
+            static code_cache* cache = new code_cache();
+            return *cache;
+        }
+
+        struct loaded_module {
+            hip::module_t module = nullptr;
+            std::unordered_map<std::string, kernel_handle> kernels;
+        };
+        struct module_cache {
+            std::mutex mutex;
+            // keyed by the code object's bytes
+            std::unordered_map<std::string, loaded_module> entries;
+        };
+        module_cache& modules() {
+            static module_cache* cache = new module_cache();
+            return *cache;
+        }
+
+        std::string cache_key(
+            std::string_view source, const std::vector<std::string>& options
+        ) {
+            std::string key;
+            key.reserve(source.size() + 64);
+            key += std::to_string(source.size());
+            key += ':';
+            key += source;
+            for (const std::string& option : options) {
+                key += '\0';
+                key += std::to_string(option.size());
+                key += ':';
+                key += option;
+            }
+            return key;
+        }
+
+    } // namespace
+
+    const device_info& device() { return device_singleton().info; }
+
+    stream::stream() {
+        const hip::api& h = hip::runtime();
+        (void)device();
+        hip::check(h.set_device(0), "hipSetDevice");
+        hip::check(
+            h.stream_create_with_flags(&handle_, hip::stream_non_blocking),
+            "hipStreamCreateWithFlags"
+        );
+    }
+
+    stream::~stream() {
+        if (handle_ == nullptr) return;
+        try {
+            const hip::api& h = hip::runtime();
+            (void)h.stream_synchronize(handle_);
+            (void)h.stream_destroy(handle_);
+        }
+        catch (...) {
+        }
+    }
+
+    void stream::synchronize() const {
+        hip::check(
+            hip::runtime().stream_synchronize(handle_), "hipStreamSynchronize"
+        );
+    }
+
+    std::shared_ptr<stream> current_stream() {
+        thread_local std::shared_ptr<stream> mine = std::make_shared<stream>();
+        return mine;
+    }
+
+    void order_after(const stream& consumer, const stream& producer) {
+        if (&consumer == &producer) return;
+        const hip::api& h = hip::runtime();
+        hip::event_t event = nullptr;
+        hip::check(
+            h.event_create_with_flags(&event, hip::event_disable_timing),
+            "hipEventCreateWithFlags"
+        );
+        hip::error_t recorded = h.event_record(event, producer.handle());
+        hip::error_t waited =
+            recorded == hip::success
+                ? h.stream_wait_event(consumer.handle(), event, 0)
+                : recorded;
+        (void)h.event_destroy(event);
+        hip::check(recorded, "hipEventRecord");
+        hip::check(waited, "hipStreamWaitEvent");
+    }
+
+    buffer_state::buffer_state(size_t requested_bytes)
+        : bytes(requested_bytes) {
+        if (bytes == 0) return;
+        std::shared_ptr<stream> s = current_stream();
+        hip::check(
+            hip::runtime().malloc_async(&ptr, bytes, s->handle()),
+            "hipMallocAsync"
+        );
+        producer_ = std::move(s);
+    }
+
+    buffer_state::~buffer_state() {
+        if (ptr == nullptr) return;
+        try {
+            std::shared_ptr<stream> owner =
+                producer_ != nullptr ? producer_ : current_stream();
+            for (const std::shared_ptr<stream>& reader : readers_) {
+                if (reader != owner) order_after(*owner, *reader);
+            }
+            (void)hip::runtime().free_async(ptr, owner->handle());
+        }
+        catch (...) {
+        }
+    }
+
+    void buffer_state::before_read(const std::shared_ptr<stream>& s) {
+        std::scoped_lock lock{mutex_};
+        if (producer_ == nullptr || producer_ == s) return;
+        order_after(*s, *producer_);
+        for (const std::shared_ptr<stream>& reader : readers_) {
+            if (reader == s) return;
+        }
+        readers_.push_back(s);
+    }
+
+    void buffer_state::before_write(const std::shared_ptr<stream>& s) {
+        std::scoped_lock lock{mutex_};
+        if (producer_ != nullptr && producer_ != s) order_after(*s, *producer_);
+        for (const std::shared_ptr<stream>& reader : readers_) {
+            if (reader != s) order_after(*s, *reader);
+        }
+        readers_.clear();
+    }
+
+    void buffer_state::after_write(const std::shared_ptr<stream>& s) {
+        std::scoped_lock lock{mutex_};
+        producer_ = s;
+    }
+
+    std::shared_ptr<stream> buffer_state::producer_stream() const {
+        std::scoped_lock lock{mutex_};
+        return producer_;
+    }
+
+    std::string target_arch() {
+        if (const char* arch = std::getenv("PORCH_HIP_ARCH")) return arch;
+        return "gfx950";
+    }
+
+    std::vector<std::string> default_options() {
+        return {
+            "--offload-arch=" + target_arch(),
+            "-O3",
+            "-std=c++17",
+            "-ffp-contract=off",
+            // Packed FP32 (v_pk_*_f32) stays off in every kernel.
+            "-Xclang",
+            "-target-feature",
+            "-Xclang",
+            "-packed-fp32-ops",
+        };
+    }
+
+    std::shared_ptr<const code_object> compile(
+        std::string_view source, const std::vector<std::string>& extra_options
+    ) {
+        std::vector<std::string> options = default_options();
+        options.insert(
+            options.end(), extra_options.begin(), extra_options.end()
+        );
+        const std::string key = cache_key(source, options);
+        {
+            std::scoped_lock lock{codes().mutex};
+            auto found = codes().entries.find(key);
+            if (found != codes().entries.end()) return found->second;
+        }
+
+        const hip::api& c = hip::compiler();
+        const auto start = std::chrono::steady_clock::now();
+        rtc_program program;
+        const std::string text{source};
+        hip::check_rtc(
+            c.rtc_create_program(
+                &program.program, text.c_str(), "porch_kernel.hip", 0, nullptr,
+                nullptr
+            ),
+            "hiprtcCreateProgram"
+        );
+        std::vector<const char*> option_ptrs;
+        option_ptrs.reserve(options.size());
+        for (const std::string& option : options)
+            option_ptrs.push_back(option.c_str());
+        const hip::rtc_result_t result = c.rtc_compile_program(
+            program.program, static_cast<int>(option_ptrs.size()),
+            option_ptrs.data()
+        );
+        if (result != hip::rtc_success) {
+            std::string log = program_log(program.program);
+            if (log.empty()) {
+                const char* text_error = c.rtc_get_error_string(result);
+                log = text_error != nullptr ? text_error : "hiprtc failed";
+            }
+            throw hip_jit::compilation_error(std::move(log));
+        }
+        size_t size = 0;
+        hip::check_rtc(
+            c.rtc_get_code_size(program.program, &size), "hiprtcGetCodeSize"
+        );
+        auto object = std::make_shared<code_object>();
+        object->bytes.assign(size, '\0');
+        hip::check_rtc(
+            c.rtc_get_code(program.program, object->bytes.data()),
+            "hiprtcGetCode"
+        );
+        object->compile_ms = elapsed_ms(start);
+        {
+            std::scoped_lock lock{counters_mutex()};
+            counters().compiles += 1;
+            counters().compile_ms += object->compile_ms;
+        }
+        std::scoped_lock lock{codes().mutex};
+        auto [it, inserted] = codes().entries.emplace(key, object);
+        return it->second;
+    }
+
+    kernel_handle load_kernel(
+        const std::shared_ptr<const code_object>& code, std::string_view name
+    ) {
+        const hip::api& h = hip::runtime();
+        (void)device();
+        std::scoped_lock lock{modules().mutex};
+        loaded_module& entry = modules().entries[code->bytes];
+        if (entry.module == nullptr) {
+            const auto start = std::chrono::steady_clock::now();
+            hip::check(
+                h.module_load_data(&entry.module, code->bytes.data()),
+                "hipModuleLoadData"
+            );
+            std::scoped_lock counters_lock{counters_mutex()};
+            counters().module_load_ms += elapsed_ms(start);
+        }
+        const std::string function_name{name};
+        auto found = entry.kernels.find(function_name);
+        if (found != entry.kernels.end()) return found->second;
+        kernel_handle kernel;
+        hip::check(
+            h.module_get_function(
+                &kernel.function, entry.module, function_name.c_str()
+            ),
+            "hipModuleGetFunction"
+        );
+        (void)h.func_get_attribute(
+            &kernel.registers, hip::func_attr_num_regs, kernel.function
+        );
+        (void)h.func_get_attribute(
+            &kernel.lds_bytes, hip::func_attr_shared_size_bytes, kernel.function
+        );
+        (void)h.func_get_attribute(
+            &kernel.scratch_bytes, hip::func_attr_local_size_bytes,
+            kernel.function
+        );
+        entry.kernels.emplace(function_name, kernel);
+        return kernel;
+    }
+
+    void launch(
+        const kernel_handle& kernel, unsigned grid_x, unsigned grid_y,
+        unsigned grid_z, unsigned block_x, unsigned shared_bytes,
+        void** params, const stream& s
+    ) {
+        hip::check(
+            hip::runtime().module_launch_kernel(
+                kernel.function, grid_x, grid_y, grid_z, block_x, 1, 1,
+                shared_bytes, s.handle(), params, nullptr
+            ),
+            "hipModuleLaunchKernel"
+        );
+        std::scoped_lock lock{counters_mutex()};
+        counters().launches += 1;
+    }
+
+    void clear_caches() {
+        {
+            std::scoped_lock lock{codes().mutex};
+            codes().entries.clear();
+        }
+        // Modules stay loaded: kernels of cached plans may still be queued.
+        // A cleared code cache forces recompilation; a recompiled code
+        // object that is byte-identical reuses its module.
+    }
+
+    jit_counters& counters() {
+        static jit_counters* instance = new jit_counters();
+        return *instance;
+    }
+
+    std::mutex& counters_mutex() {
+        static std::mutex* instance = new std::mutex();
+        return *instance;
+    }
+
+    void flush_caches(size_t bytes) {
+        static std::mutex mutex;
+        static void* scratch = nullptr;
+        static size_t scratch_bytes = 0;
+        std::scoped_lock lock{mutex};
+        std::shared_ptr<stream> s = current_stream();
+        const hip::api& h = hip::runtime();
+        bytes = (bytes + 3) & ~size_t{3};
+        if (scratch_bytes < bytes) {
+            if (scratch != nullptr) {
+                hip::check(h.free_async(scratch, s->handle()), "hipFreeAsync");
+            }
+            scratch = nullptr;
+            hip::check(
+                h.malloc_async(&scratch, bytes, s->handle()), "hipMallocAsync"
+            );
+            scratch_bytes = bytes;
+        }
+        static int pattern = 0;
+        pattern += 1;
+        hip::check(
+            h.memset_d32_async(scratch, pattern, bytes / 4, s->handle()),
+            "hipMemsetD32Async"
+        );
+    }
+
+} // namespace porch::rt

@@ -1,0 +1,100 @@
+"""The five benchmark graphs of the MI355X fused-graph path, at any size.
+
+Each is porch source over seeded synthetic inputs (splitmix64, see
+porch_amd.synth):
+  c1  (a + b) * 2 - 1                     a, b ~ U[-1,1] length 2^20
+  c2  concat(transpose(x[0::2,1::2]), transpose(x[1::2,0::2]), 0) + 1
+                                          x ~ N(0,1) [4096,4096]
+  c3  softmax(x, 1)                       x ~ N(0,3) [8192,4096], 1% set to +20
+  c4  sum(logistic(relu(x*w + bias)), 1)  x ~ N(0,1) [16384,2048], w ~ U(.5,1.5),
+                                          bias ~ N(0,.1) [1,2048]
+  c5  relu(A @ B + bias) - 0.5            A, B ~ U(-1,1)/64 [4096,4096],
+                                          bias ~ N(0,.01) [1,4096]
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+import porch_amd as porch
+from porch_amd import synth
+
+# -----------------------------------------------------------------------------
+
+def config_inputs(name: str, size: dict | None = None) -> list[np.ndarray]:
+    s = dict(CONFIG_SIZES[name])
+    s.update(size or {})
+    if name == "c1":
+        n = s["n"]
+        return [synth.uniform(n, 101, -1.0, 1.0), synth.uniform(n, 102, -1.0, 1.0)]
+    if name == "c2":
+        n = s["n"]
+        return [synth.normal(n * n, 201, 0.0, 1.0)]
+    if name == "c3":
+        rows, cols = s["rows"], s["cols"]
+        x = synth.normal(rows * cols, 301, 0.0, 3.0)
+        synth.replace(x, 302, 0.01, 20.0)
+        return [x]
+    if name == "c4":
+        rows, cols = s["rows"], s["cols"]
+        return [synth.normal(rows * cols, 401, 0.0, 1.0), synth.uniform(cols, 402, 0.5, 1.5),
+                synth.normal(cols, 403, 0.0, 0.1)]
+    if name == "c5":
+        m, k, n = s["m"], s["k"], s["n"]
+        return [synth.uniform(m * k, 501, -1.0, 1.0) / np.float32(64.0),
+                synth.uniform(k * n, 502, -1.0, 1.0) / np.float32(64.0),
+                synth.normal(n, 503, 0.0, 0.01)]
+    raise ValueError(name)
+
+
+CONFIG_SIZES = {
+    "c1": {"n": 1 << 20},
+    "c2": {"n": 4096},
+    "c3": {"rows": 8192, "cols": 4096},
+    "c4": {"rows": 16384, "cols": 2048},
+    "c5": {"m": 4096, "k": 4096, "n": 4096},
+}
+
+
+def config_shapes(name: str, size: dict | None = None) -> list[list[int]]:
+    s = dict(CONFIG_SIZES[name])
+    s.update(size or {})
+    if name == "c1":
+        return [[s["n"]], [s["n"]]]
+    if name == "c2":
+        return [[s["n"], s["n"]]]
+    if name == "c3":
+        return [[s["rows"], s["cols"]]]
+    if name == "c4":
+        return [[s["rows"], s["cols"]], [1, s["cols"]], [1, s["cols"]]]
+    if name == "c5":
+        return [[s["m"], s["k"]], [s["k"], s["n"]], [1, s["n"]]]
+    raise ValueError(name)
+
+
+def config_graph(name: str, tensors, size: dict | None = None):
+    """The benchmark graph of config `name` over `tensors` (porch source)."""
+    s = dict(CONFIG_SIZES[name])
+    s.update(size or {})
+    if name == "c1":
+        a, b = tensors
+        return (a + b) * 2.0 - 1.0
+    if name == "c2":
+        (x,) = tensors
+        n = s["n"]
+        return porch.concat(
+            porch.transpose(x[porch.slice(0, n, 2), porch.slice(1, n, 2)]),
+            porch.transpose(x[porch.slice(1, n, 2), porch.slice(0, n, 2)]), 0) + 1.0
+    if name == "c3":
+        (x,) = tensors
+        return porch.softmax(x, 1)
+    if name == "c4":
+        x, w, b = tensors
+        shape = [s["rows"], s["cols"]]
+        return porch.sum(porch.logistic(porch.relu(
+            x * porch.broadcast_to(w, shape) + porch.broadcast_to(b, shape))), 1)
+    if name == "c5":
+        a, b, bias = tensors
+        shape = [s["m"], s["n"]]
+        return porch.relu(porch.matmul(a, b) + porch.broadcast_to(bias, shape)) - 0.5
+    raise ValueError(name)

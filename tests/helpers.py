@@ -1,0 +1,103 @@
+"""Shared test helpers: the KAT expression notation, host-only placeholder
+tensors (graphs for the oracle and the planner without a GPU), and the five
+benchmark graphs at any size."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+
+import porch_amd as porch
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def placeholder(shape, values=None) -> porch.tensor:
+    """A tensor with host values and no device buffer (CPU-only graphs)."""
+    t = porch.tensor.__new__(porch.tensor)
+    t._state = porch._State(list(shape), porch.device())
+    host = None
+    if values is not None:
+        host = np.ascontiguousarray(np.asarray(values, dtype=np.float32).reshape(-1))
+    t._state.storage = porch._Storage(None, host)
+    return t
+
+
+def kat_cases():
+    with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
+        data = json.load(f)
+    return data["cases"], data["errors"]
+
+
+def kat_input_values(spec) -> np.ndarray:
+    count = int(np.prod(spec["shape"]))
+    if "values" in spec:
+        values = np.asarray(spec["values"], dtype=np.float32)
+    else:
+        values = np.arange(spec["iota_from"], spec["iota_from"] + count, dtype=np.float32)
+    for position, value in spec.get("set", []):
+        values[position] = value
+    return values
+
+
+_BINARY = {"add": "__add__", "sub": "__sub__", "mul": "__mul__", "div": "__truediv__"}
+
+
+def build(expr, inputs):
+    """porch expression from the prefix notation over `inputs` (tensors)."""
+    if isinstance(expr, (int, float)):
+        return porch.tensor_expr(float(expr))
+    op, *args = expr
+    if op == "in":
+        return porch.tensor_expr(inputs[args[0]])
+    if op == "idx":
+        items = []
+        for item in args[1]:
+            if item == "all":
+                items.append(porch.all)
+            elif isinstance(item, list):
+                items.append(porch.slice(*item))
+            else:
+                items.append(item)
+        return inputs[args[0]][tuple(items)]
+    if op in _BINARY:
+        lhs = build(args[0], inputs)
+        rhs = build(args[1], inputs)
+        return getattr(porch.tensor_expr(lhs), _BINARY[op])(rhs)
+    if op in ("matmul", "maximum", "minimum"):
+        return getattr(porch, op)(build(args[0], inputs), build(args[1], inputs))
+    if op in ("exp", "reciprocal", "transpose", "relu", "logistic"):
+        return getattr(porch, op)(build(args[0], inputs))
+    if op == "reshape":
+        return porch.reshape(build(args[0], inputs), args[1])
+    if op == "broadcast":
+        return porch.broadcast_to(build(args[0], inputs), args[1])
+    if op == "unsqueeze":
+        return porch.unsqueeze(build(args[0], inputs), args[1])
+    if op == "concat":
+        return porch.concat(build(args[0], inputs), build(args[1], inputs), args[2])
+    if op in ("sum", "max"):
+        return getattr(porch, op)(build(args[0], inputs), args[1], args[2])
+    if op == "softmax":
+        return porch.softmax(build(args[0], inputs), args[1])
+    raise ValueError(f"unknown op {op}")
+
+
+def check_kat(case, values: np.ndarray) -> None:
+    values = np.asarray(values, dtype=np.float32).reshape(-1)
+    if "exact" in case:
+        expected = np.asarray(case["exact"], dtype=np.float32)
+        assert values.shape == expected.shape, (values, expected)
+        assert np.array_equal(values.view(np.uint32), expected.view(np.uint32)), (values, expected)
+    for i, interval in enumerate(case.get("open", [])):
+        if interval is None:
+            continue
+        lo, hi = interval
+        assert lo < values[i] < hi, (case["name"], i, values[i])
+    for position, value in case.get("eq", []):
+        assert values[position] == np.float32(value), (case["name"], position, values[position])
+
+
+from porch_amd.workloads import CONFIG_SIZES, config_graph, config_inputs, config_shapes  # noqa: E402,F401

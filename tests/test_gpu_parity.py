@@ -1,0 +1,253 @@
+"""GPU results against the host evaluator on the same seeded inputs.
+
+Bars (stated per test): bit-exact for view/index/concat/+-*/ graphs (kernels
+are built with -ffp-contract=off, correctly rounded division); exp-based
+graphs within 2 ulp or 1e-6 relative; reductions 1e-5 and matmul 1e-4
+relative (their summation order is free).  Full-size configs are checked
+against the oracle (on a row sample for the matmul) and through properties
+that do not depend on size.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import host
+from tests.helpers import CONFIG_SIZES, config_graph, config_inputs, config_shapes
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_and_oracle(porch, name, size=None, inputs=None):
+    shapes = config_shapes(name, size)
+    inputs = inputs if inputs is not None else config_inputs(name, size)
+    tensors = [porch.tensor(s, v) for s, v in zip(shapes, inputs)]
+    expr = config_graph(name, tensors, size)
+    out = porch.materialize(expr).cpu().reshape(expr.shape())
+    return out, host.evaluate(expr), inputs
+
+
+def assert_bits_equal(a, b):
+    assert a.shape == b.shape
+    diff = np.flatnonzero(a.reshape(-1).view(np.uint32) != b.reshape(-1).view(np.uint32))
+    assert diff.size == 0, (diff[:8], a.reshape(-1)[diff[:8]], b.reshape(-1)[diff[:8]])
+
+
+def ulp_distance(a, b):
+    ai = a.reshape(-1).view(np.int32).astype(np.int64)
+    bi = b.reshape(-1).view(np.int32).astype(np.int64)
+    ai = np.where(ai < 0, -(ai & 0x7FFFFFFF), ai)
+    bi = np.where(bi < 0, -(bi & 0x7FFFFFFF), bi)
+    return np.abs(ai - bi)
+
+
+def assert_close(gpu_out, ref, rel):
+    assert gpu_out.shape == ref.shape
+    err = np.abs(gpu_out.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), 1e-30)
+    assert err.max() <= rel, (err.max(), np.unravel_index(err.argmax(), err.shape))
+
+
+# -- config 1: elementwise chain, bit-exact ----------------------------------
+
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1000, 4099, 1 << 20])
+def test_c1_elementwise_bit_exact(gpu, n):
+    out, ref, _ = gpu_and_oracle(gpu, "c1", {"n": n})
+    assert_bits_equal(out, ref)
+
+
+# -- config 2: strided slice + transpose + concat, bit-exact ------------------
+
+@pytest.mark.parametrize("n", [2, 6, 62, 64, 130, 4096])
+def test_c2_view_chain_bit_exact(gpu, n):
+    out, ref, (x,) = gpu_and_oracle(gpu, "c2", {"n": n})
+    assert_bits_equal(out, ref)
+    # size-independent closed form y[i, j] = x[2j, 2i+1] + 1 (top half)
+    xm = x.reshape(n, n)
+    assert np.array_equal(out[: n // 2], xm[0::2, 1::2].T + np.float32(1.0))
+
+
+# -- config 3: softmax, 1e-6 relative ----------------------------------------
+
+@pytest.mark.parametrize("size", [{"rows": 3, "cols": 7}, {"rows": 17, "cols": 256},
+                                  {"rows": 64, "cols": 4100}, {"rows": 8, "cols": 12288},
+                                  {"rows": 8192, "cols": 4096}])
+def test_c3_softmax_within_1e6(gpu, size):
+    out, ref, _ = gpu_and_oracle(gpu, "c3", size)
+    assert_close(out, ref, 1e-6)
+    assert np.allclose(out.sum(axis=1), 1.0, atol=2e-5)
+
+
+# -- config 4: broadcast + logistic + row sum, 1e-5 relative -----------------
+
+@pytest.mark.parametrize("size", [{"rows": 5, "cols": 9}, {"rows": 33, "cols": 2048},
+                                  {"rows": 16384, "cols": 2048}, {"rows": 4, "cols": 10000}])
+def test_c4_row_reduction_within_1e5(gpu, size):
+    out, ref, _ = gpu_and_oracle(gpu, "c4", size)
+    assert_close(out, ref, 1e-5)
+
+
+# -- config 5: matmul + epilogue, 1e-4 relative ------------------------------
+
+@pytest.mark.parametrize("size", [{"m": 2, "k": 3, "n": 5}, {"m": 67, "k": 129, "n": 33},
+                                  {"m": 256, "k": 4096, "n": 128}])
+def test_c5_matmul_epilogue_within_1e4(gpu, size):
+    out, ref, _ = gpu_and_oracle(gpu, "c5", size)
+    assert_close(out, ref, 1e-4)
+
+
+def test_c5_full_size_on_a_row_sample(gpu):
+    porch = gpu
+    size = CONFIG_SIZES["c5"]
+    a, b, bias = config_inputs("c5")
+    m, k, n = size["m"], size["k"], size["n"]
+    ta, tb, tbias = porch.tensor([m, k], a), porch.tensor([k, n], b), porch.tensor([1, n], bias)
+    out = porch.materialize(config_graph("c5", [ta, tb, tbias])).cpu().reshape(m, n)
+    rows = np.array([0, 1, 2, 777, 2048, 4000, 4095])
+    sample = porch.tensor([rows.size, k], a.reshape(m, k)[rows])
+    ref = host.evaluate(porch.relu(porch.matmul(sample, tb) + porch.broadcast_to(tbias, [rows.size, n])) - 0.5)
+    assert_close(out[rows], ref, 1e-4)
+    exact = np.maximum(a.reshape(m, k)[rows].astype(np.float64) @ b.reshape(k, n) + bias, 0.0) - 0.5
+    assert np.abs(out[rows] - exact).max() < 5e-6
+
+
+# -- edge cases the reference's tests touch: empty, ragged, rank-3 ----------
+
+def test_empty_results_and_empty_operands(gpu):
+    porch = gpu
+    x = porch.tensor([0, 4], [])
+    assert porch.materialize(x + 1.0).numel() == 0
+    y = porch.tensor([2, 4], np.arange(8, dtype=np.float32))
+    # concat with an empty operand (the reference launches with an empty input
+    # buffer and throws; porch_amd never reads it)
+    out = porch.materialize(porch.concat(x, y, 0))
+    assert np.array_equal(out.cpu(), np.arange(8, dtype=np.float32))
+    assert porch.materialize(porch.sum(porch.tensor([3, 0], []), 1)).cpu().tolist() == [0, 0, 0]
+
+
+def test_rank3_views_bit_exact(gpu):
+    porch = gpu
+    x = (np.arange(5 * 6 * 7, dtype=np.float32) * 0.37).reshape(5, 6, 7)
+    t = porch.tensor([5, 6, 7], x)
+    cases = [
+        porch.tensor(t[porch.slice(1, 5, 2), porch.all, porch.slice(1, 7, 3)]) * 2.0,
+        porch.reshape(porch.transpose(porch.reshape(t, [30, 7])), [7, 5, 6]) - 1.0,
+        porch.concat(t, porch.tensor(t[porch.all, porch.slice(0, 2)]), 1) + 0.5,
+        porch.broadcast_to(porch.unsqueeze(porch.tensor(t[2]), 0), [3, 6, 7]) / 4.0,
+        porch.maximum(t, porch.minimum(t * 2.0, 3.0)),
+    ]
+    for expr in cases:
+        assert_bits_equal(porch.materialize(expr).cpu().reshape(expr.shape()), host.evaluate(expr))
+
+
+def test_reductions_over_every_axis(gpu):
+    porch = gpu
+    rng = np.random.default_rng(11)
+    x = rng.integers(-50, 50, size=(6, 70, 9)).astype(np.float32)
+    t = porch.tensor([6, 70, 9], x)
+    for axis in range(3):
+        for keep in (False, True):
+            for op in (porch.sum, porch.max):
+                expr = op(t, axis, keep)
+                assert_bits_equal(porch.materialize(expr).cpu().reshape(expr.shape()),
+                                  host.evaluate(expr))
+
+
+def test_max_semantics_match_reference(gpu):
+    porch = gpu
+    t = porch.tensor([2, 5], [-np.inf] * 5 + [1, 2, 3, 4, 5])
+    out = porch.materialize(porch.max(t, 1)).cpu()
+    assert out[0] == np.float32(-3.4028234663852886e38) and out[1] == 5.0
+    a = porch.tensor([3], [np.nan, 1.0, -0.0])
+    b = porch.tensor([3], [2.0, np.nan, 0.0])
+    hi = porch.materialize(porch.maximum(a, b)).cpu()
+    assert hi[0] == 2.0 and np.isnan(hi[1]) and hi[2] == 0.0 and not np.signbit(hi[2])
+
+
+def test_exp_within_2_ulp_of_host(gpu):
+    porch = gpu
+    xs = np.concatenate([np.linspace(-87.0, 88.0, 200003), [-104.0, -100.0, -90.0, 0.0, -0.0,
+                                                            89.0, np.inf, -np.inf, np.nan]])
+    xs = xs.astype(np.float32)
+    t = porch.tensor([xs.size], xs)
+    out = porch.materialize(porch.exp(t)).cpu()
+    ref = host.evaluate(porch.exp(t))
+    finite = np.isfinite(ref)
+    assert ulp_distance(out[finite], ref[finite]).max() <= 2
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    assert np.array_equal(out[np.isinf(ref)], ref[np.isinf(ref)])
+
+
+def test_logistic_and_reciprocal(gpu):
+    porch = gpu
+    xs = np.linspace(-30, 30, 100001).astype(np.float32)
+    t = porch.tensor([xs.size], xs)
+    out = porch.materialize(porch.logistic(t)).cpu()
+    ref = host.evaluate(porch.logistic(t))
+    assert ulp_distance(out, ref).max() <= 2
+    r = porch.materialize(porch.reciprocal(t)).cpu()
+    assert_bits_equal(r, host.evaluate(porch.reciprocal(t)))
+
+
+# -- seeded random graphs: views and elementwise arithmetic, bit-exact -------
+
+def random_graph(porch, rng, inputs):
+    def fresh(shape):
+        values = rng.integers(-8, 9, size=int(np.prod(shape))).astype(np.float32) * np.float32(0.5)
+        t = porch.tensor(list(shape), values)
+        inputs.append(t)
+        return porch.tensor_expr(t)
+
+    rank = int(rng.integers(1, 4))
+    shape = [int(rng.integers(1, 9)) for _ in range(rank)]
+    expr = fresh(shape)
+    for _ in range(int(rng.integers(2, 7))):
+        shape = expr.shape()
+        choice = int(rng.integers(0, 10))
+        if choice == 0:
+            expr = expr * float(rng.choice([2.0, 0.5, -1.0])) + float(rng.integers(-3, 4))
+        elif choice == 1:
+            expr = porch.maximum(expr, fresh(shape)) - porch.minimum(expr, 0.5)
+        elif choice == 2 and len(shape) == 2:
+            expr = porch.transpose(expr)
+        elif choice == 3:
+            lazy = porch.tensor(expr)  # slicing an expression goes through a pending tensor
+            items = []
+            for extent in shape:
+                start = int(rng.integers(0, extent))
+                step = int(rng.integers(1, 3))
+                items.append(porch.slice(start, extent, step))
+            expr = lazy[tuple(items)]
+        elif choice == 4:
+            n = int(np.prod(shape))
+            factors = [f for f in range(1, n + 1) if n % f == 0]
+            f = int(rng.choice(factors))
+            expr = porch.reshape(expr, [f, n // f])
+        elif choice == 5:
+            expr = porch.unsqueeze(expr, int(rng.integers(0, len(shape) + 1)))
+        elif choice == 6:
+            target = [int(rng.integers(1, 4))] + [e if e != 1 else int(rng.integers(1, 4)) for e in shape]
+            expr = porch.broadcast_to(expr, target)
+        elif choice == 7:
+            axis = int(rng.integers(0, len(shape)))
+            other = list(shape)
+            other[axis] = int(rng.integers(1, 5))
+            expr = porch.concat(expr, fresh(other), axis) if rng.integers(0, 2) else \
+                porch.concat(fresh(other), expr, axis)
+        elif choice == 8:
+            expr = expr + fresh(shape) * 2.0
+        else:
+            expr = expr / 4.0
+        if int(np.prod(expr.shape())) > 4096:
+            break
+    return expr
+
+
+def test_random_view_graphs_bit_exact(gpu):
+    porch = gpu
+    rng = np.random.default_rng(20261201)
+    for trial in range(150):
+        inputs = []
+        expr = random_graph(porch, rng, inputs)
+        out = porch.materialize(expr).cpu().reshape(expr.shape())
+        ref = host.evaluate(expr)
+        assert out.shape == ref.shape, trial
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, porch.plan(expr))

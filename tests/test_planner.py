@@ -1,0 +1,103 @@
+"""The planner's kernel choices and offline hiprtc compilation (no GPU)."""
+
+import pytest
+
+import porch_amd as porch
+from tests.helpers import config_graph, config_shapes, placeholder
+
+EXPECTED_KIND = {
+    "c1": "pointwise.flat",
+    "c2": "pointwise.tiled",
+    "c3": "row",
+    "c4": "row",
+    "c5": "gemm",
+}
+
+
+@pytest.mark.parametrize("name", sorted(EXPECTED_KIND))
+def test_each_benchmark_graph_is_one_fused_kernel(name):
+    tensors = [placeholder(s) for s in config_shapes(name)]
+    plan = porch.plan(config_graph(name, tensors), compile=True)
+    assert len(plan["kernels"]) == 1, plan
+    assert plan["temps"] == []
+    kernel = plan["kernels"][0]
+    assert kernel["kind"].startswith(EXPECTED_KIND[name]), kernel
+    assert kernel["code_bytes"] > 0 and kernel["dest"] == "output"
+
+
+def test_softmax_reads_the_row_once():
+    x = placeholder([8192, 4096])
+    source = porch.kernel_source(porch.softmax(x, 1))
+    # one 128-bit load per column chunk, in the first pass only
+    assert source.count("reinterpret_cast<const float4*>(a0") == 1
+    assert source.count("expf(") == 4  # one pass, four lanes
+
+
+def test_shared_reductions_are_materialised_once():
+    """softmax over a non-last axis cannot be one row program; its max is
+    still computed once (the reference computes it twice)."""
+    x = placeholder([64, 32])
+    plan = porch.plan(porch.softmax(x, 0))
+    kinds = [k["kind"] for k in plan["kernels"]]
+    assert kinds.count("reduce.column") == 2, kinds  # max and sum, once each
+    assert len(plan["temps"]) == 2
+
+
+def test_nested_reduction_feeds_elementwise_kernel():
+    x = placeholder([1, 513])
+    plan = porch.plan(porch.sum(x, 1) * 2.0 + 1.0)
+    assert [k["kind"] for k in plan["kernels"]] == ["row", "pointwise.scalar"]
+
+
+def test_matmul_operand_expressions_are_materialised():
+    a = placeholder([2, 3])
+    b = placeholder([3, 2])
+    plan = porch.plan(porch.matmul(a + a, b))
+    kinds = [k["kind"] for k in plan["kernels"]]
+    assert kinds[-1].startswith("gemm") and len(kinds) == 2
+
+
+def test_matmul_read_through_a_view_is_not_fused_as_epilogue():
+    a = placeholder([4, 4])
+    m = porch.matmul(a, a)
+    plan = porch.plan(m + porch.transpose(m))
+    kinds = [k["kind"] for k in plan["kernels"]]
+    assert kinds[0].startswith("gemm") and kinds[-1].startswith("pointwise")
+    assert len(plan["temps"]) == 1
+
+
+def test_transposed_operand_feeds_gemm_without_copy():
+    a = placeholder([64, 32])
+    b = placeholder([64, 48])
+    plan = porch.plan(porch.matmul(porch.transpose(a), b))
+    assert len(plan["kernels"]) == 1 and plan["kernels"][0]["kind"].startswith("gemm")
+
+
+@pytest.mark.parametrize("expr_fn", [
+    lambda x: porch.transpose(x) + 1.0,
+    lambda x: porch.concat(x, x, 1) * 2.0,
+    lambda x: porch.reshape(porch.transpose(x), [6, 4]) - 1.0,
+    lambda x: porch.broadcast_to(porch.sum(x, 1, True), [4, 6]) / x,
+    lambda x: porch.max(porch.exp(x), 0, True),
+    lambda x: porch.relu(porch.matmul(x, porch.transpose(x))) - 0.5,
+])
+def test_small_graphs_compile_offline(expr_fn):
+    x = placeholder([4, 6])
+    plan = porch.plan(expr_fn(x), compile=True)
+    assert all(k["code_bytes"] > 0 for k in plan["kernels"])
+
+
+def test_large_tensors_use_64_bit_indices():
+    x = placeholder([1 << 16, 1 << 15])  # 2^31 elements
+    assert "typedef long long idx_t" in porch.kernel_source(x + 1.0)
+    y = placeholder([1024, 1024])
+    assert "typedef int idx_t" in porch.kernel_source(y + 1.0)
+
+
+def test_scalars_are_emitted_exactly():
+    x = placeholder([8])
+    for value in (0.1, 1e-45, 3.4028234663852886e38, -0.0):
+        source = porch.kernel_source(x * value)
+        assert "f" in source
+    inf_source = porch.kernel_source(x * float("inf"))
+    assert "__uint_as_float(0x7f800000u)" in inf_source
