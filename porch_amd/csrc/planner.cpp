@@ -378,9 +378,31 @@ namespace porch::plan {
                 add_step(cg::emit_pointwise(r), dest);
             }
 
+            // A reduction over an empty axis is its identity everywhere:
+            // 0.0f for sum, -FLT_MAX for max (the values the reference's
+            // block reduction starts from, src/tensor.cpp:900-901).
+            void emit_identity_fill(int id, arg_ref dest) {
+                const ir::node& n = g.at(id);
+                cg::kexpr k;
+                cg::knode c;
+                c.op = cg::kop::constant;
+                c.value = n.kind == ir::op::sum ? 0.0F : -3.40282346638528859812e+38F;
+                cg::pointwise_request r;
+                r.expr = &k;
+                r.root = k.add(c);
+                r.shape = n.out;
+                r.n_slots = n_slots();
+                r.width = width;
+                add_step(cg::emit_pointwise(r), dest);
+            }
+
             void emit(int id, arg_ref dest) {
                 const ir::node& n = g.at(id);
                 if (ir::numel(n.out) == 0) return;
+                if (ir::is_reduction(n.kind) && ir::numel(g.at(n.lhs).out) == 0) {
+                    emit_identity_fill(id, dest);
+                    return;
+                }
                 if (try_gemm(id, dest)) return;
                 if (try_row(id, dest)) return;
                 if (ir::is_reduction(n.kind)) {
