@@ -193,6 +193,19 @@ porch_status porch_materialize(const porch_graph* graph,
                                int64_t* out_shape, int32_t capacity,
                                int32_t* out_rank);
 
+/* porch_materialize with HIP events attached to the first and the last
+ * kernel launch (hipExtModuleLaunchKernel), so elapsed time between them is
+ * the kernels' own execution on the calling thread's stream.  Events come
+ * from porch_event_create (declared below).
+ * No reference counterpart: measurement support for the same path. */
+typedef struct porch_event porch_event;
+porch_status porch_materialize_timed(const porch_graph* graph,
+                                     const porch_buffer* const* inputs,
+                                     int32_t n_inputs, porch_buffer** out,
+                                     int64_t* out_shape, int32_t capacity,
+                                     int32_t* out_rank, porch_event* start,
+                                     porch_event* stop);
+
 /* Plans and compiles the graph without a device and without launching
  * (hiprtc runs on the host).  Writes a JSON description of the plan
  * (kernel classes, launch geometry, temporaries) into json[capacity].
@@ -228,7 +241,6 @@ porch_status porch_reset_jit_cache(void);
 /* Timing support (HIP events on the calling thread's current stream)   */
 /* ------------------------------------------------------------------ */
 
-typedef struct porch_event porch_event;
 porch_status porch_event_create(porch_event** out);
 porch_status porch_event_record(porch_event* event);
 porch_status porch_event_synchronize(porch_event* event);

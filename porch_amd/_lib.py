@@ -118,6 +118,10 @@ _SIGNATURES = {
                                            ctypes.c_int32, ctypes.POINTER(_P),
                                            ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
                                            ctypes.POINTER(ctypes.c_int32)]),
+    "porch_materialize_timed": (ctypes.c_int32, [ctypes.POINTER(Graph), ctypes.POINTER(_P),
+                                                 ctypes.c_int32, ctypes.POINTER(_P),
+                                                 ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
+                                                 ctypes.POINTER(ctypes.c_int32), _P, _P]),
     "porch_plan": (ctypes.c_int32, [ctypes.POINTER(Graph), ctypes.c_int32, ctypes.c_char_p,
                                     ctypes.c_size_t]),
     "porch_plan_source": (ctypes.c_int32, [ctypes.POINTER(Graph), ctypes.c_int32,

@@ -243,64 +243,83 @@ porch_status porch_infer_shape(const porch_graph* graph, int64_t* shape, int32_t
     });
 }
 
+namespace {
+    porch_status materialize_impl(const porch_graph* graph, const porch_buffer* const* inputs,
+                                  int32_t n_inputs, porch_buffer** out, int64_t* out_shape,
+                                  int32_t capacity, int32_t* out_rank, porch_event* start,
+                                  porch_event* stop) {
+        return guarded([&] {
+            const auto begin = std::chrono::steady_clock::now();
+            require(out != nullptr, "output pointer is null");
+            *out = nullptr;
+            ir::graph g = validated(graph);
+            const ir::node& root = g.at(g.root());
+            if (root.is_scalar)
+                throw std::invalid_argument("scalar expression cannot materialize to a tensor");
+            require(n_inputs >= g.n_inputs, "graph needs more input buffers");
+            require(n_inputs == 0 || inputs != nullptr, "inputs are null");
+            const size_t count = ir::checked_numel(root.out);
+            write_shape(root.out, out_shape, capacity, out_rank);
+            auto* result = new porch_buffer();
+            if (count == 0) {
+                *out = result;
+                return;
+            }
+            try {
+                const ir::graph compacted = ir::compact(g);
+                bool hit = false;
+                std::shared_ptr<plan::graph_plan> p = plan::lookup(compacted, &hit);
+                std::vector<rt::buffer_state*> buffers;
+                for (int32_t i = 0; i < n_inputs; ++i) {
+                    buffers.push_back(
+                        inputs[i] == nullptr
+                            ? nullptr
+                            : hip_jit::buffer_access::state(inputs[i]->handle).get()
+                    );
+                }
+                std::shared_ptr<rt::buffer_state> state = plan::run(
+                    *p, buffers,
+                    [](size_t bytes) -> std::shared_ptr<rt::buffer_state> {
+                        return std::make_shared<hip_jit::device_buffer_state>(bytes);
+                    },
+                    start ? start->event : nullptr, stop ? stop->event : nullptr
+                );
+                result->handle = hip_jit::buffer_access::wrap(
+                    std::static_pointer_cast<hip_jit::device_buffer_state>(state)
+                );
+                const double ms = rt::elapsed_ms(begin);
+                std::scoped_lock lock{rt::counters_mutex()};
+                if (hit) {
+                    rt::counters().plan_hits += 1;
+                    rt::counters().last_hit_us = ms * 1000.0;
+                }
+                else {
+                    rt::counters().plan_misses += 1;
+                    rt::counters().last_miss_ms = ms;
+                }
+            }
+            catch (...) {
+                delete result;
+                throw;
+            }
+            *out = result;
+        });
+    }
+} // namespace
+
 porch_status porch_materialize(const porch_graph* graph, const porch_buffer* const* inputs,
                                int32_t n_inputs, porch_buffer** out, int64_t* out_shape,
                                int32_t capacity, int32_t* out_rank) {
-    return guarded([&] {
-        const auto start = std::chrono::steady_clock::now();
-        require(out != nullptr, "output pointer is null");
-        *out = nullptr;
-        ir::graph g = validated(graph);
-        const ir::node& root = g.at(g.root());
-        if (root.is_scalar)
-            throw std::invalid_argument("scalar expression cannot materialize to a tensor");
-        require(n_inputs >= g.n_inputs, "graph needs more input buffers");
-        require(n_inputs == 0 || inputs != nullptr, "inputs are null");
-        const size_t count = ir::checked_numel(root.out);
-        write_shape(root.out, out_shape, capacity, out_rank);
-        auto* result = new porch_buffer();
-        if (count == 0) {
-            *out = result;
-            return;
-        }
-        try {
-            const ir::graph compacted = ir::compact(g);
-            bool hit = false;
-            std::shared_ptr<plan::graph_plan> p = plan::lookup(compacted, &hit);
-            std::vector<rt::buffer_state*> buffers;
-            for (int32_t i = 0; i < n_inputs; ++i) {
-                buffers.push_back(
-                    inputs[i] == nullptr
-                        ? nullptr
-                        : hip_jit::buffer_access::state(inputs[i]->handle).get()
-                );
-            }
-            std::shared_ptr<rt::buffer_state> state = plan::run(
-                *p, buffers,
-                [](size_t bytes) -> std::shared_ptr<rt::buffer_state> {
-                    return std::make_shared<hip_jit::device_buffer_state>(bytes);
-                }
-            );
-            result->handle = hip_jit::buffer_access::wrap(
-                std::static_pointer_cast<hip_jit::device_buffer_state>(state)
-            );
-            const double ms = rt::elapsed_ms(start);
-            std::scoped_lock lock{rt::counters_mutex()};
-            if (hit) {
-                rt::counters().plan_hits += 1;
-                rt::counters().last_hit_us = ms * 1000.0;
-            }
-            else {
-                rt::counters().plan_misses += 1;
-                rt::counters().last_miss_ms = ms;
-            }
-        }
-        catch (...) {
-            delete result;
-            throw;
-        }
-        *out = result;
-    });
+    return materialize_impl(graph, inputs, n_inputs, out, out_shape, capacity, out_rank,
+                            nullptr, nullptr);
+}
+
+porch_status porch_materialize_timed(const porch_graph* graph, const porch_buffer* const* inputs,
+                                     int32_t n_inputs, porch_buffer** out, int64_t* out_shape,
+                                     int32_t capacity, int32_t* out_rank, porch_event* start,
+                                     porch_event* stop) {
+    return materialize_impl(graph, inputs, n_inputs, out, out_shape, capacity, out_rank,
+                            start, stop);
 }
 
 porch_status porch_plan(const porch_graph* graph, int32_t compile, char* json, size_t capacity) {

@@ -75,10 +75,220 @@ namespace porch::cg {
             return kc;
         }
 
+        // ----------------------------------------------------------------
+        // LDS-tiled fp32 MFMA: 128x128 tile per 256-thread workgroup, each
+        // wave a 64x64 quadrant as 2x2 v_mfma_f32_32x32x2f32 blocks, K in
+        // steps of 16 through double-buffered LDS (one barrier per step).
+        // Operand lane layout (checked on gfx950): A[i = l%32][k = l/32],
+        // B[k = l/32][j = l%32]; accumulator register v of lane l holds
+        // C[8*(v/4) + 4*(l/32) + v%4][l%32].
+        // ----------------------------------------------------------------
+        constexpr int BM = 128;
+        constexpr int BN = 128;
+        constexpr int BK = 16;
+
+        struct operand_layout {
+            bool k_major;      // contiguous along k (A row-major, B col-major)
+            bool vector;       // 128-bit global loads are aligned and in bounds
+            int pitch;         // LDS row pitch (floats) of the k-major tile
+        };
+
+        // Loads of one operand tile into registers r{X}[8] and their stores
+        // to LDS (tile stored k-major: T[k][i], i = m for A, n for B).
+        void operand_code(std::string& load, std::string& store, const char* X,
+                          const gemm_operand& op, bool is_a, int64_t rows_ext,
+                          int64_t k_ext, const operand_layout& lay) {
+            // i: the m (A) or n (B) coordinate; stride_i / stride_k in memory
+            const int64_t stride_i = is_a ? op.stride_row : op.stride_col;
+            const int64_t stride_k = is_a ? op.stride_col : op.stride_row;
+            const std::string base = std::string(is_a ? "A" : "B");
+            const std::string i0 = is_a ? "m0" : "n0";
+            const std::string x{X};
+            if (lay.k_major) {
+                // chunk c: i = c >> 2, k = (c & 3) * 4 .. +3
+                load += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                load += "        const int c = tid + i * 256;\n";
+                load += "        const int ii = c >> 2;\n        const int kq = (c & 3) * 4;\n";
+                load += "        const idx_t gi = " + i0 + " + ii;\n";
+                load += "        const idx_t gk = k0 + kq;\n";
+                if (lay.vector) {
+                    load += "        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);\n";
+                    load += "        if (gi < " + std::to_string(rows_ext) + " && gk < " +
+                            std::to_string(k_ext) + ") v = *reinterpret_cast<const float4*>(" +
+                            base + " + gi * " + std::to_string(stride_i) + " + gk);\n";
+                    load += "        r" + x + "[i * 4 + 0] = v.x; r" + x + "[i * 4 + 1] = v.y; r" +
+                            x + "[i * 4 + 2] = v.z; r" + x + "[i * 4 + 3] = v.w;\n";
+                }
+                else {
+                    load += "        #pragma unroll\n        for (int e = 0; e < 4; ++e)\n";
+                    load += "            r" + x + "[i * 4 + e] = (gi < " + std::to_string(rows_ext) +
+                            " && gk + e < " + std::to_string(k_ext) + ") ? " + base + "[gi * " +
+                            std::to_string(stride_i) + " + (gk + e) * " +
+                            std::to_string(stride_k) + "] : 0.0f;\n";
+                }
+                load += "    }\n";
+                store += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                store += "        const int c = tid + i * 256;\n";
+                store += "        const int ii = c >> 2;\n        const int kq = (c & 3) * 4;\n";
+                store += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) " + x +
+                         "s[nb][kq + e][ii] = r" + x + "[i * 4 + e];\n";
+                store += "    }\n";
+            }
+            else {
+                // contiguous along i: chunk c: k = c >> 5, i = (c & 31) * 4 .. +3
+                load += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                load += "        const int c = tid + i * 256;\n";
+                load += "        const int kk = c >> 5;\n        const int iq = (c & 31) * 4;\n";
+                load += "        const idx_t gi = " + i0 + " + iq;\n";
+                load += "        const idx_t gk = k0 + kk;\n";
+                if (lay.vector) {
+                    load += "        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);\n";
+                    load += "        if (gi < " + std::to_string(rows_ext) + " && gk < " +
+                            std::to_string(k_ext) + ") v = *reinterpret_cast<const float4*>(" +
+                            base + " + gk * " + std::to_string(stride_k) + " + gi);\n";
+                    load += "        r" + x + "[i * 4 + 0] = v.x; r" + x + "[i * 4 + 1] = v.y; r" +
+                            x + "[i * 4 + 2] = v.z; r" + x + "[i * 4 + 3] = v.w;\n";
+                }
+                else {
+                    load += "        #pragma unroll\n        for (int e = 0; e < 4; ++e)\n";
+                    load += "            r" + x + "[i * 4 + e] = (gi + e < " + std::to_string(rows_ext) +
+                            " && gk < " + std::to_string(k_ext) + ") ? " + base + "[(gi + e) * " +
+                            std::to_string(stride_i) + " + gk * " + std::to_string(stride_k) +
+                            "] : 0.0f;\n";
+                }
+                load += "    }\n";
+                store += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                store += "        const int c = tid + i * 256;\n";
+                store += "        const int kk = c >> 5;\n        const int iq = (c & 31) * 4;\n";
+                store += "        *reinterpret_cast<float4*>(&" + x + "s[nb][kk][iq]) = make_float4(r" +
+                         x + "[i * 4 + 0], r" + x + "[i * 4 + 1], r" + x + "[i * 4 + 2], r" + x +
+                         "[i * 4 + 3]);\n";
+                store += "    }\n";
+            }
+        }
+
+        operand_layout layout_of(const gemm_operand& op, bool is_a, int64_t rows_ext,
+                                 int64_t k_ext) {
+            const int64_t stride_i = is_a ? op.stride_row : op.stride_col;
+            const int64_t stride_k = is_a ? op.stride_col : op.stride_row;
+            operand_layout lay;
+            lay.k_major = stride_k == 1 && !(stride_i == 1 && stride_k != 1);
+            if (stride_k != 1 && stride_i != 1) lay.k_major = true; // strided: scalar path
+            if (lay.k_major) {
+                lay.vector = stride_k == 1 && op.offset % 4 == 0 && stride_i % 4 == 0 &&
+                             k_ext % 4 == 0;
+                lay.pitch = BM + 2; // scalar LDS writes: conflict-free with pitch = 2 mod 8
+            }
+            else {
+                lay.vector = op.offset % 4 == 0 && stride_k % 4 == 0 && rows_ext % 4 == 0;
+                lay.pitch = BM + 4; // 128-bit LDS writes need 16-byte rows
+            }
+            return lay;
+        }
+
+        kernel_code emit_gemm_mfma(const gemm_request& r) {
+            const int64_t tiles_m = (r.m + BM - 1) / BM;
+            const int64_t tiles_n = (r.n + BN - 1) / BN;
+            const int64_t tiles = tiles_m * tiles_n;
+            const int64_t steps = (r.k + BK - 1) / BK;
+            const operand_layout la = layout_of(r.a, true, r.m, r.k);
+            const operand_layout lb = layout_of(r.b, false, r.n, r.k);
+            kernel_code kc;
+            kc.kind = "gemm.mfma";
+            kc.name = "porch_gemm";
+            kc.n_slots = r.n_slots;
+            kc.block = 256;
+            kc.grid_x = static_cast<unsigned>(tiles);
+            const char* T = r.width.type();
+            std::string& s = kc.source;
+            s = kernel_prologue(r.n_slots, T);
+            s += "typedef float floatx16 __attribute__((ext_vector_type(16)));\n";
+            s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" +
+                 kernel_params(r.n_slots) + ") {\n";
+            s += "    __shared__ __attribute__((aligned(16))) float As[2][" + std::to_string(BK) + "][" + std::to_string(la.pitch) + "];\n";
+            s += "    __shared__ __attribute__((aligned(16))) float Bs[2][" + std::to_string(BK) + "][" + std::to_string(lb.pitch) + "];\n";
+            s += "    const int tid = threadIdx.x;\n";
+            s += "    const int lane = tid & 63;\n";
+            s += "    const int wave = tid >> 6;\n";
+            s += "    const int wm = wave >> 1;\n    const int wn = wave & 1;\n";
+            // Workgroups are dispatched round-robin over the 8 XCDs; give
+            // each XCD a contiguous band of tile rows so its L2 holds them.
+            if (tiles % 8 == 0) {
+                s += "    const int tile = (blockIdx.x % 8) * " + std::to_string(tiles / 8) +
+                     " + blockIdx.x / 8;\n";
+            }
+            else {
+                s += "    const int tile = blockIdx.x;\n";
+            }
+            s += "    const idx_t m0 = (idx_t)(tile / " + std::to_string(tiles_n) + ") * " +
+                 std::to_string(BM) + ";\n";
+            s += "    const idx_t n0 = (idx_t)(tile % " + std::to_string(tiles_n) + ") * " +
+                 std::to_string(BN) + ";\n";
+            s += "    const float* __restrict__ A = a" + std::to_string(r.a.slot) + " + " +
+                 std::to_string(r.a.offset) + ";\n";
+            s += "    const float* __restrict__ B = a" + std::to_string(r.b.slot) + " + " +
+                 std::to_string(r.b.offset) + ";\n";
+            s += "    float rA[8];\n    float rB[8];\n";
+            s += "    floatx16 acc[2][2];\n";
+            s += "    #pragma unroll\n    for (int i = 0; i < 2; ++i)\n";
+            s += "        #pragma unroll\n        for (int j = 0; j < 2; ++j)\n";
+            s += "            #pragma unroll\n            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;\n";
+            std::string load_a, store_a, load_b, store_b;
+            operand_code(load_a, store_a, "A", r.a, true, r.m, r.k, la);
+            operand_code(load_b, store_b, "B", r.b, false, r.n, r.k, lb);
+            // prologue: tile 0
+            s += "    {\n        const idx_t k0 = 0;\n        const int nb = 0;\n";
+            s += load_a + load_b + store_a + store_b;
+            s += "    }\n    __syncthreads();\n";
+            s += "    for (int t = 0; t < " + std::to_string(steps) + "; ++t) {\n";
+            s += "        const int cb = t & 1;\n";
+            s += "        const int nb = cb ^ 1;\n";
+            s += "        const idx_t k0 = (idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
+            s += "        const bool more = t + 1 < " + std::to_string(steps) + ";\n";
+            s += "        if (more) {\n" + load_a + load_b + "        }\n";
+            s += "        #pragma unroll\n";
+            s += "        for (int kk = 0; kk < " + std::to_string(BK) + "; kk += 2) {\n";
+            s += "            const int kr = kk + (lane >> 5);\n";
+            s += "            const float a0 = As[cb][kr][wm * 64 + (lane & 31)];\n";
+            s += "            const float a1 = As[cb][kr][wm * 64 + 32 + (lane & 31)];\n";
+            s += "            const float b0 = Bs[cb][kr][wn * 64 + (lane & 31)];\n";
+            s += "            const float b1 = Bs[cb][kr][wn * 64 + 32 + (lane & 31)];\n";
+            s += "            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);\n";
+            s += "            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);\n";
+            s += "            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);\n";
+            s += "            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);\n";
+            s += "        }\n";
+            s += "        if (more) {\n" + store_a + store_b + "        }\n";
+            s += "        __syncthreads();\n";
+            s += "    }\n";
+            // epilogue
+            s += "    #pragma unroll\n    for (int bi = 0; bi < 2; ++bi)\n";
+            s += "    #pragma unroll\n    for (int bj = 0; bj < 2; ++bj)\n";
+            s += "    #pragma unroll\n    for (int v = 0; v < 16; ++v) {\n";
+            s += "        const idx_t q0 = m0 + wm * 64 + bi * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);\n";
+            s += "        const idx_t q1 = n0 + wn * 64 + bj * 32 + (lane & 31);\n";
+            s += "        if (q0 < " + std::to_string(r.m) + " && q1 < " + std::to_string(r.n) + ") {\n";
+            s += "            const float acc_v = acc[bi][bj][v];\n";
+            std::string body;
+            emitter em(*r.expr, body, 1);
+            em.indent = "            ";
+            const std::vector<std::string> names{"q0", "q1"};
+            epilogue_emitter(em, r, names, "acc_v");
+            const std::string v = em.emit(r.epilogue)[0];
+            s += body;
+            s += "            out[q0 * " + std::to_string(r.n) + " + q1] = " + v + ";\n";
+            s += "        }\n    }\n}\n";
+            return kc;
+        }
+
     } // namespace
 
     kernel_code emit_gemm(const gemm_request& r) {
-        return emit_gemm_scalar(r);
+        // Small products keep the reference's sequential K loop (their
+        // launch is latency-bound anyway); large ones use MFMA.
+        if (r.m * r.n * r.k < (int64_t{1} << 18) || r.m < 32 || r.n < 32)
+            return emit_gemm_scalar(r);
+        return emit_gemm_mfma(r);
     }
 
 } // namespace porch::cg

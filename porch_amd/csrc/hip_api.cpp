@@ -104,6 +104,10 @@ namespace porch::hip {
                     hip_library, t.module_launch_kernel, "hipModuleLaunchKernel"
                 );
                 ok &= bind(
+                    hip_library, t.ext_module_launch_kernel,
+                    "hipExtModuleLaunchKernel"
+                );
+                ok &= bind(
                     hip_library, t.func_get_attribute, "hipFuncGetAttribute"
                 );
                 ok &= bind(hip_library, t.get_error_name, "hipGetErrorName");

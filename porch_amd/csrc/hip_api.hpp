@@ -80,6 +80,10 @@ namespace porch::hip {
             function_t, unsigned, unsigned, unsigned, unsigned, unsigned,
             unsigned, unsigned, stream_t, void**, void**
         );
+        error_t (*ext_module_launch_kernel)(
+            function_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,
+            size_t, stream_t, void**, void**, event_t, event_t, uint32_t
+        );
         error_t (*func_get_attribute)(int*, int, function_t);
         const char* (*get_error_name)(error_t);
         const char* (*get_error_string)(error_t);

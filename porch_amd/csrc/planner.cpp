@@ -512,7 +512,8 @@ namespace porch::plan {
 
     std::shared_ptr<rt::buffer_state> run(
         graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
-        const std::function<std::shared_ptr<rt::buffer_state>(size_t)>& allocate
+        const std::function<std::shared_ptr<rt::buffer_state>(size_t)>& allocate,
+        hip::event_t start, hip::event_t stop
     ) {
         if (static_cast<int>(inputs.size()) < plan.n_inputs) {
             throw std::invalid_argument("graph needs more input buffers");
@@ -555,7 +556,8 @@ namespace porch::plan {
         }
         std::vector<void*> pointers;
         std::vector<void*> params;
-        for (const step& st : plan.steps) {
+        for (size_t index = 0; index < plan.steps.size(); ++index) {
+            const step& st = plan.steps[index];
             const int slots = st.code.n_slots;
             pointers.assign(static_cast<size_t>(slots) + 1, nullptr);
             for (int i = 0; i < slots; ++i) {
@@ -574,7 +576,9 @@ namespace porch::plan {
             params.assign(pointers.size(), nullptr);
             for (size_t i = 0; i < pointers.size(); ++i) params[i] = &pointers[i];
             rt::launch(st.kernel, st.code.grid_x, st.code.grid_y, st.code.grid_z,
-                       st.code.block, 0, params.data(), *s);
+                       st.code.block, 0, params.data(), *s,
+                       index == 0 ? start : nullptr,
+                       index + 1 == plan.steps.size() ? stop : nullptr);
         }
         out->after_write(s);
         // Temporaries are freed stream-ordered after the launches above.

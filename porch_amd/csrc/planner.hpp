@@ -73,9 +73,12 @@ namespace porch::plan {
     // Launches the plan on the calling thread's stream.  `inputs[i]` backs
     // input slot i.  Returns the output buffer (no allocation when the
     // output is empty).
+    // `start` / `stop` (optional) are attached to the first and the last
+    // kernel launch.
     std::shared_ptr<rt::buffer_state> run(
         graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
-        const std::function<std::shared_ptr<rt::buffer_state>(size_t)>& allocate
+        const std::function<std::shared_ptr<rt::buffer_state>(size_t)>& allocate,
+        hip::event_t start = nullptr, hip::event_t stop = nullptr
     );
 
 } // namespace porch::plan

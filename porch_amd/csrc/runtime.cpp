@@ -2,6 +2,9 @@
 
 #include "porch/hip_jit.hpp"
 
+#include <sys/syscall.h>
+#include <unistd.h>
+
 #include <cstdlib>
 #include <cstring>
 #include <limits>
@@ -162,9 +165,24 @@ namespace porch::rt {
         );
     }
 
+    namespace {
+        // The calling thread's stream.  A worker thread's stream is
+        // released when the thread exits (buffers it produced keep it
+        // alive).  The process's initial thread only exits inside exit(),
+        // where thread-local destructors run before the HIP runtime and any
+        // attached tool have shut down: that stream is left to the OS.
+        struct thread_stream {
+            std::shared_ptr<stream> s = std::make_shared<stream>();
+            ~thread_stream() {
+                if (static_cast<pid_t>(syscall(SYS_gettid)) == getpid())
+                    new std::shared_ptr<stream>(std::move(s)); // never freed
+            }
+        };
+    } // namespace
+
     std::shared_ptr<stream> current_stream() {
-        thread_local std::shared_ptr<stream> mine = std::make_shared<stream>();
-        return mine;
+        thread_local thread_stream mine;
+        return mine.s;
     }
 
     void order_after(const stream& consumer, const stream& producer) {
@@ -363,15 +381,31 @@ namespace porch::rt {
     void launch(
         const kernel_handle& kernel, unsigned grid_x, unsigned grid_y,
         unsigned grid_z, unsigned block_x, unsigned shared_bytes,
-        void** params, const stream& s
+        void** params, const stream& s, hip::event_t start, hip::event_t stop
     ) {
-        hip::check(
-            hip::runtime().module_launch_kernel(
-                kernel.function, grid_x, grid_y, grid_z, block_x, 1, 1,
-                shared_bytes, s.handle(), params, nullptr
-            ),
-            "hipModuleLaunchKernel"
-        );
+        const hip::api& h = hip::runtime();
+        if (start == nullptr && stop == nullptr) {
+            hip::check(
+                h.module_launch_kernel(
+                    kernel.function, grid_x, grid_y, grid_z, block_x, 1, 1,
+                    shared_bytes, s.handle(), params, nullptr
+                ),
+                "hipModuleLaunchKernel"
+            );
+        }
+        else {
+            const uint64_t threads = static_cast<uint64_t>(grid_x) * block_x;
+            if (threads > 0xffffffffULL || grid_y != 1 || grid_z != 1)
+                throw std::invalid_argument("timed launch grid is too large");
+            hip::check(
+                h.ext_module_launch_kernel(
+                    kernel.function, static_cast<uint32_t>(threads), 1, 1,
+                    block_x, 1, 1, shared_bytes, s.handle(), params, nullptr,
+                    start, stop, 0
+                ),
+                "hipExtModuleLaunchKernel"
+            );
+        }
         std::scoped_lock lock{counters_mutex()};
         counters().launches += 1;
     }

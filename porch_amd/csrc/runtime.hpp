@@ -105,10 +105,14 @@ namespace porch::rt {
         const std::shared_ptr<const code_object>& code, std::string_view name
     );
 
+    // Launches on stream `s`.  With `start`/`stop` the launch goes through
+    // hipExtModuleLaunchKernel, whose events are timestamped by the
+    // dispatch itself (no extra barrier packets between them).
     void launch(
         const kernel_handle& kernel, unsigned grid_x, unsigned grid_y,
         unsigned grid_z, unsigned block_x, unsigned shared_bytes,
-        void** params, const stream& s
+        void** params, const stream& s, hip::event_t start = nullptr,
+        hip::event_t stop = nullptr
     );
 
     void clear_caches();

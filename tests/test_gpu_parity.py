@@ -254,3 +254,56 @@ def test_random_view_graphs_bit_exact(gpu):
         ref = host.evaluate(expr)
         assert out.shape == ref.shape, trial
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, porch.plan(expr))
+
+
+# -- the MFMA GEMM: tile edges, K tails, operand layouts ---------------------
+
+def gemm_bound(a64, b64):
+    """Scale of fp32 accumulation error: sum_k |a_ik| |b_kj|."""
+    return np.abs(a64) @ np.abs(b64)
+
+
+@pytest.mark.parametrize("m,k,n", [(200, 1000, 130), (128, 16, 128), (257, 33, 64),
+                                   (1024, 4096, 96), (64, 2049, 300)])
+def test_mfma_gemm_edges_and_tails(gpu, m, k, n):
+    porch = gpu
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, size=(k, n)).astype(np.float32)
+    expr = porch.matmul(porch.tensor([m, k], a), porch.tensor([k, n], b))
+    assert porch.plan(expr)["kernels"][-1]["kind"] == "gemm.mfma"
+    out = porch.materialize(expr).cpu().reshape(m, n)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert (np.abs(out - ref) <= 1e-5 * gemm_bound(a.astype(np.float64), b.astype(np.float64)) + 1e-30).all()
+
+
+@pytest.mark.parametrize("layout", ["at", "bt", "both", "offset"])
+def test_mfma_gemm_operand_layouts(gpu, layout):
+    porch = gpu
+    m, k, n = 192, 260, 136
+    rng = np.random.default_rng(5)
+    a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, size=(k, n)).astype(np.float32)
+    if layout == "at":
+        lhs = porch.transpose(porch.tensor([k, m], np.ascontiguousarray(a.T)))
+        rhs = porch.tensor([k, n], b)
+    elif layout == "bt":
+        lhs = porch.tensor([m, k], a)
+        rhs = porch.transpose(porch.tensor([n, k], np.ascontiguousarray(b.T)))
+    elif layout == "both":
+        lhs = porch.transpose(porch.tensor([k, m], np.ascontiguousarray(a.T)))
+        rhs = porch.transpose(porch.tensor([n, k], np.ascontiguousarray(b.T)))
+    else:
+        # operands as strided sub-views with odd offsets: scalar loads path
+        big_a = np.zeros((m + 1, k + 3), dtype=np.float32)
+        big_a[1:, 3:] = a
+        lhs = porch.tensor([m + 1, k + 3], big_a)[porch.slice(1, m + 1), porch.slice(3, k + 3)]
+        rhs = porch.tensor([k, n], b)
+    expr = porch.relu(porch.matmul(lhs, rhs)) - 0.25
+    out = porch.materialize(expr).cpu().reshape(m, n)
+    ref = np.maximum(a.astype(np.float64) @ b.astype(np.float64), 0.0) - 0.25
+    bound = gemm_bound(a.astype(np.float64), b.astype(np.float64))
+    assert (np.abs(out - ref) <= 1e-5 * bound + 1e-7).all()
+    # against the oracle (sequential fp32 sum): both within the bound, and
+    # the epilogue's -0.25 cancels, so the comparison is absolute
+    assert (np.abs(out - host.evaluate(expr)) <= 2e-5 * bound + 1e-7).all()
