@@ -42,6 +42,7 @@ WORK = {
     "c3": ("hbm", 2 * 8192 * 4096 * 4),
     "c4": ("hbm", 16384 * 2048 * 4 + 2 * 2048 * 4 + 16384 * 4),
     "c5": ("mfma", 2 * 4096 ** 3),
+    "copy": ("hbm", 2 * 8192 * 8192 * 4),
 }
 DESCRIPTION = {
     "c1": "(a + b) * 2 - 1, a, b fp32 [1048576]",
@@ -49,9 +50,10 @@ DESCRIPTION = {
     "c3": "softmax(x, 1), x fp32 [8192,4096]",
     "c4": "sum(logistic(relu(x*bcast(w) + bcast(bias))), 1), x fp32 [16384,2048]",
     "c5": "relu(A @ B + bcast(bias)) - 0.5, A, B fp32 [4096,4096]",
+    "copy": "reshape(x) copy, x fp32 [8192,8192] (byte-counter calibration)",
 }
 # Input copies rotated through so that a step never re-reads cached data.
-ROTATION = {"c1": 48, "c2": 8, "c3": 4, "c4": 6, "c5": 1}
+ROTATION = {"c1": 48, "c2": 8, "c3": 4, "c4": 6, "c5": 1, "copy": 2}
 
 
 def log(message: str) -> None:

@@ -10,6 +10,8 @@ porch_amd.synth):
                                           bias ~ N(0,.1) [1,2048]
   c5  relu(A @ B + bias) - 0.5            A, B ~ U(-1,1)/64 [4096,4096],
                                           bias ~ N(0,.01) [1,4096]
+and `copy`, reshape(x) over x [8192,8192]: a plain copy of known size used to
+calibrate hardware byte counters.
 """
 
 from __future__ import annotations
@@ -39,6 +41,8 @@ def config_inputs(name: str, size: dict | None = None) -> list[np.ndarray]:
         rows, cols = s["rows"], s["cols"]
         return [synth.normal(rows * cols, 401, 0.0, 1.0), synth.uniform(cols, 402, 0.5, 1.5),
                 synth.normal(cols, 403, 0.0, 0.1)]
+    if name == "copy":
+        return [synth.uniform(s["n"] * s["n"], 601, -1.0, 1.0)]
     if name == "c5":
         m, k, n = s["m"], s["k"], s["n"]
         return [synth.uniform(m * k, 501, -1.0, 1.0) / np.float32(64.0),
@@ -53,6 +57,7 @@ CONFIG_SIZES = {
     "c3": {"rows": 8192, "cols": 4096},
     "c4": {"rows": 16384, "cols": 2048},
     "c5": {"m": 4096, "k": 4096, "n": 4096},
+    "copy": {"n": 8192},
 }
 
 
@@ -69,6 +74,8 @@ def config_shapes(name: str, size: dict | None = None) -> list[list[int]]:
         return [[s["rows"], s["cols"]], [1, s["cols"]], [1, s["cols"]]]
     if name == "c5":
         return [[s["m"], s["k"]], [s["k"], s["n"]], [1, s["n"]]]
+    if name == "copy":
+        return [[s["n"], s["n"]]]
     raise ValueError(name)
 
 
@@ -97,4 +104,7 @@ def config_graph(name: str, tensors, size: dict | None = None):
         a, b, bias = tensors
         shape = [s["m"], s["n"]]
         return porch.relu(porch.matmul(a, b) + porch.broadcast_to(bias, shape)) - 0.5
+    if name == "copy":
+        (x,) = tensors
+        return porch.reshape(x, [s["n"] * s["n"]])
     raise ValueError(name)
