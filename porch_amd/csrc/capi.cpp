@@ -7,6 +7,8 @@
 
 #include <chrono>
 #include <cstring>
+#include <mutex>
+#include <unordered_map>
 #include <stdexcept>
 #include <string>
 
@@ -244,6 +246,36 @@ porch_status porch_infer_shape(const porch_graph* graph, int64_t* shape, int32_t
 }
 
 namespace {
+    // Graphs already validated and planned, keyed by the exact bytes of the
+    // node table and dims: a repeated table skips validation, shape
+    // inference, compaction and key building.
+    struct table_entry {
+        std::shared_ptr<plan::graph_plan> plan;
+        std::vector<int64_t> out_shape;
+        int n_inputs = 0;
+    };
+    struct table_cache {
+        std::mutex mutex;
+        std::unordered_map<std::string, table_entry> entries;
+    };
+    table_cache& tables() {
+        static table_cache* instance = new table_cache();
+        return *instance;
+    }
+
+    std::string table_key(const porch_graph* graph) {
+        std::string key;
+        if (graph == nullptr || graph->nodes == nullptr || graph->n_nodes <= 0 ||
+            graph->n_dims < 0 || (graph->n_dims > 0 && graph->dims == nullptr))
+            return key;
+        const size_t node_bytes = static_cast<size_t>(graph->n_nodes) * sizeof(porch_node);
+        const size_t dim_bytes = static_cast<size_t>(graph->n_dims) * sizeof(int64_t);
+        key.resize(node_bytes + dim_bytes);
+        std::memcpy(key.data(), graph->nodes, node_bytes);
+        if (dim_bytes) std::memcpy(key.data() + node_bytes, graph->dims, dim_bytes);
+        return key;
+    }
+
     porch_status materialize_impl(const porch_graph* graph, const porch_buffer* const* inputs,
                                   int32_t n_inputs, porch_buffer** out, int64_t* out_shape,
                                   int32_t capacity, int32_t* out_rank, porch_event* start,
@@ -252,33 +284,53 @@ namespace {
             const auto begin = std::chrono::steady_clock::now();
             require(out != nullptr, "output pointer is null");
             *out = nullptr;
-            ir::graph g = validated(graph);
-            const ir::node& root = g.at(g.root());
-            if (root.is_scalar)
-                throw std::invalid_argument("scalar expression cannot materialize to a tensor");
-            require(n_inputs >= g.n_inputs, "graph needs more input buffers");
+            const std::string key = table_key(graph);
+            table_entry entry;
+            bool hit = false;
+            if (!key.empty()) {
+                std::scoped_lock lock{tables().mutex};
+                auto found = tables().entries.find(key);
+                if (found != tables().entries.end()) {
+                    entry = found->second;
+                    hit = true;
+                }
+            }
+            if (!hit) {
+                ir::graph g = validated(graph);
+                const ir::node& root = g.at(g.root());
+                if (root.is_scalar)
+                    throw std::invalid_argument(
+                        "scalar expression cannot materialize to a tensor");
+                entry.out_shape = root.out;
+                entry.n_inputs = g.n_inputs;
+                if (ir::checked_numel(root.out) > 0) {
+                    bool plan_hit = false;
+                    entry.plan = plan::lookup(ir::compact(g), &plan_hit);
+                    hit = plan_hit;
+                    if (!key.empty()) {
+                        std::scoped_lock lock{tables().mutex};
+                        tables().entries.emplace(key, entry);
+                    }
+                }
+            }
+            require(n_inputs >= entry.n_inputs, "graph needs more input buffers");
             require(n_inputs == 0 || inputs != nullptr, "inputs are null");
-            const size_t count = ir::checked_numel(root.out);
-            write_shape(root.out, out_shape, capacity, out_rank);
+            write_shape(entry.out_shape, out_shape, capacity, out_rank);
             auto* result = new porch_buffer();
-            if (count == 0) {
+            if (entry.plan == nullptr) { // empty result
                 *out = result;
                 return;
             }
             try {
-                const ir::graph compacted = ir::compact(g);
-                bool hit = false;
-                std::shared_ptr<plan::graph_plan> p = plan::lookup(compacted, &hit);
-                std::vector<rt::buffer_state*> buffers;
+                std::vector<rt::buffer_state*> buffers(static_cast<size_t>(n_inputs));
                 for (int32_t i = 0; i < n_inputs; ++i) {
-                    buffers.push_back(
+                    buffers[static_cast<size_t>(i)] =
                         inputs[i] == nullptr
                             ? nullptr
-                            : hip_jit::buffer_access::state(inputs[i]->handle).get()
-                    );
+                            : hip_jit::buffer_access::state(inputs[i]->handle).get();
                 }
                 std::shared_ptr<rt::buffer_state> state = plan::run(
-                    *p, buffers,
+                    *entry.plan, buffers,
                     [](size_t bytes) -> std::shared_ptr<rt::buffer_state> {
                         return std::make_shared<hip_jit::device_buffer_state>(bytes);
                     },
@@ -367,6 +419,10 @@ porch_status porch_get_jit_stats(porch_jit_stats* stats) {
 
 porch_status porch_reset_jit_cache(void) {
     return guarded([] {
+        {
+            std::scoped_lock lock{tables().mutex};
+            tables().entries.clear();
+        }
         plan::clear_cache();
         rt::clear_caches();
     });

@@ -8,6 +8,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <limits>
+#include <map>
 #include <stdexcept>
 #include <unordered_map>
 
@@ -151,6 +152,7 @@ namespace porch::rt {
     stream::~stream() {
         if (handle_ == nullptr) return;
         try {
+            release_stream_blocks(*this);
             const hip::api& h = hip::runtime();
             (void)h.stream_synchronize(handle_);
             (void)h.stream_destroy(handle_);
@@ -203,14 +205,120 @@ namespace porch::rt {
         hip::check(waited, "hipStreamWaitEvent");
     }
 
+    namespace {
+        struct block_cache {
+            std::mutex mutex;
+            std::unordered_map<const stream*, std::multimap<size_t, void*>> free;
+            size_t cached = 0;
+        };
+        block_cache& blocks() {
+            static block_cache* instance = new block_cache();
+            return *instance;
+        }
+        // Cached bytes kept across all streams (of 288 GB of HBM3E).
+        constexpr size_t block_cache_limit = size_t{32} << 30;
+        constexpr hip::error_t error_out_of_memory = 2;
+
+        size_t block_size(size_t bytes) {
+            constexpr size_t small = size_t{1} << 20;
+            if (bytes <= small) return (bytes + 511) & ~size_t{511};
+            return (bytes + small - 1) & ~(small - 1);
+        }
+
+        // Frees every cached block (all streams); caller holds the mutex.
+        void drain(block_cache& c) {
+            const hip::api& h = hip::runtime();
+            for (auto& [owner, list] : c.free) {
+                for (auto& [size, ptr] : list) {
+                    (void)h.free_async(ptr, owner->handle());
+                    c.cached -= size;
+                }
+                list.clear();
+            }
+        }
+    } // namespace
+
+    void* allocate_block(size_t bytes, const stream& s, size_t* capacity) {
+        const size_t want = block_size(bytes);
+        block_cache& c = blocks();
+        {
+            std::scoped_lock lock{c.mutex};
+            auto list = c.free.find(&s);
+            if (list != c.free.end()) {
+                auto fit = list->second.lower_bound(want);
+                if (fit != list->second.end() && fit->first <= want + want / 4) {
+                    void* ptr = fit->second;
+                    *capacity = fit->first;
+                    c.cached -= fit->first;
+                    list->second.erase(fit);
+                    return ptr;
+                }
+            }
+        }
+        const hip::api& h = hip::runtime();
+        void* ptr = nullptr;
+        hip::error_t rc = h.malloc_async(&ptr, want, s.handle());
+        if (rc == error_out_of_memory) {
+            {
+                std::scoped_lock lock{c.mutex};
+                drain(c);
+            }
+            rc = h.malloc_async(&ptr, want, s.handle());
+        }
+        hip::check(rc, "hipMallocAsync");
+        *capacity = want;
+        return ptr;
+    }
+
+    void release_block(void* ptr, size_t capacity, const stream& s) {
+        block_cache& c = blocks();
+        std::scoped_lock lock{c.mutex};
+        c.free[&s].emplace(capacity, ptr);
+        c.cached += capacity;
+        if (c.cached <= block_cache_limit) return;
+        const hip::api& h = hip::runtime();
+        // Over the limit: return the largest cached blocks to the pool.
+        while (c.cached > block_cache_limit / 2) {
+            const stream* owner = nullptr;
+            std::multimap<size_t, void*>::iterator largest;
+            for (auto& [st, list] : c.free) {
+                if (list.empty()) continue;
+                auto last = std::prev(list.end());
+                if (owner == nullptr || last->first > largest->first) {
+                    owner = st;
+                    largest = last;
+                }
+            }
+            if (owner == nullptr) break;
+            (void)h.free_async(largest->second, owner->handle());
+            c.cached -= largest->first;
+            c.free[owner].erase(largest);
+        }
+    }
+
+    void release_stream_blocks(const stream& s) {
+        block_cache& c = blocks();
+        std::scoped_lock lock{c.mutex};
+        auto list = c.free.find(&s);
+        if (list == c.free.end()) return;
+        const hip::api& h = hip::runtime();
+        for (auto& [size, ptr] : list->second) {
+            (void)h.free_async(ptr, s.handle());
+            c.cached -= size;
+        }
+        c.free.erase(list);
+    }
+
+    size_t cached_block_bytes() {
+        std::scoped_lock lock{blocks().mutex};
+        return blocks().cached;
+    }
+
     buffer_state::buffer_state(size_t requested_bytes)
         : bytes(requested_bytes) {
         if (bytes == 0) return;
         std::shared_ptr<stream> s = current_stream();
-        hip::check(
-            hip::runtime().malloc_async(&ptr, bytes, s->handle()),
-            "hipMallocAsync"
-        );
+        ptr = allocate_block(bytes, *s, &capacity);
         producer_ = std::move(s);
     }
 
@@ -222,7 +330,7 @@ namespace porch::rt {
             for (const std::shared_ptr<stream>& reader : readers_) {
                 if (reader != owner) order_after(*owner, *reader);
             }
-            (void)hip::runtime().free_async(ptr, owner->handle());
+            release_block(ptr, capacity, *owner);
         }
         catch (...) {
         }

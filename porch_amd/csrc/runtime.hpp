@@ -55,6 +55,17 @@ namespace porch::rt {
     // The calling thread's stream (created on first use).
     std::shared_ptr<stream> current_stream();
 
+    // Device blocks come from hipMallocAsync on a stream; a released block
+    // goes to that stream's free list and is handed to the next allocation
+    // of a fitting size on the same stream with no HIP call (stream order
+    // already puts the new user after the old one).  Cached blocks beyond
+    // a limit, and all of a stream's blocks when the stream is destroyed,
+    // go back through hipFreeAsync.
+    void* allocate_block(size_t bytes, const stream& s, size_t* capacity);
+    void release_block(void* ptr, size_t capacity, const stream& s);
+    void release_stream_blocks(const stream& s);
+    size_t cached_block_bytes();
+
     // Makes `consumer` wait for all work queued so far on `producer`.
     void order_after(const stream& consumer, const stream& producer);
 
@@ -66,6 +77,7 @@ namespace porch::rt {
 
         void* ptr = nullptr;
         size_t bytes = 0;
+        size_t capacity = 0; // size of the block behind ptr (>= bytes)
 
         // Orders stream `s` after the last write (and, for writes, after
         // readers on other streams) and records the access.
