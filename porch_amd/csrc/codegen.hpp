@@ -53,6 +53,7 @@ namespace porch::cg {
         int root = -1;
         std::vector<int64_t> shape; // output shape (kernel coordinates)
         int n_slots = 0;
+        std::vector<int64_t> slot_elems; // floats each slot's buffer holds
         index_width width;
     };
 

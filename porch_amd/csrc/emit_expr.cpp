@@ -98,6 +98,11 @@ namespace porch::cg {
                 break;
             }
             case kop::select: {
+                const int forced = forced_branch ? forced_branch(id) : -1;
+                if (forced >= 0) {
+                    result = emit(forced == 0 ? n.a : n.b);
+                    break;
+                }
                 std::vector<std::string> names(static_cast<size_t>(width));
                 std::string decl = "float ";
                 for (int e = 0; e < width; ++e) {

@@ -32,6 +32,9 @@ namespace porch::cg {
         std::function<std::string(int row)> row_value;
         // Condition text of a select (evaluated once; uniform across lanes).
         std::function<std::string(const kcond& c)> condition;
+        // Optional: the branch select `id` takes wherever this code runs
+        // (0: first operand, 1: second), or -1 to branch at run time.
+        std::function<int(int id)> forced_branch;
 
         emitter(const kexpr& expr, std::string& target, int lanes);
 

@@ -331,12 +331,87 @@ namespace porch::cg {
             return t;
         }
 
+        // Nodes of the staged subtrees (phase 1) and of the rest (phase 2).
+        std::vector<char> staged_mask(const kexpr& k, const tiling& t) {
+            std::vector<char> in(k.nodes.size(), 0);
+            for (const int root : t.staged)
+                for (const int id : k.postorder(root)) in[id] = 1;
+            return in;
+        }
+
+        // Is select condition `c` the same for the `v` consecutive values
+        // q_d = v*j .. v*j + v-1 of coordinate d, wherever it is evaluated?
+        bool uniform_over(const kcond& c, size_t d, int64_t v) {
+            if (!c.lhs.is_affine) return false;
+            const int64_t w = c.lhs.w[d];
+            if (w == 0 || v == 1) return true;
+            if (w != 1) return false;
+            for (size_t e = 0; e < c.lhs.w.size(); ++e)
+                if (e != d && c.lhs.w[e] % v != 0) return false;
+            return ((c.bound - c.lhs.c0) % v + v) % v == 0;
+        }
+
+        // A load of `v` elements spaced w[d] apart along coordinate d (the
+        // first at a multiple of v) read as one aligned float2/float4.
+        struct vector_load {
+            bool ok = false;
+            int width = 1;   // floats per vector load
+            int64_t m = 0;   // offset of the first element inside the vector
+            int64_t step = 0;
+        };
+
+        vector_load plan_vector_load(const knode& n, size_t d, int64_t v,
+                                     const std::vector<int64_t>& slot_elems) {
+            vector_load out;
+            const ival& x = n.index;
+            if (!x.is_affine || v == 1) return out;
+            const int64_t s = x.w[d];
+            if (s <= 0) return out;
+            const int64_t wv = s * v;
+            if (wv != 2 && wv != 4) return out;
+            for (size_t e = 0; e < x.w.size(); ++e)
+                if (e != d && x.w[e] % wv != 0) return out;
+            const int64_t m = ((x.c0 % wv) + wv) % wv;
+            if (m + s * (v - 1) > wv - 1) return out;
+            // Every vector read stays inside the slot's buffer: evaluate the
+            // index over the load's box with q_d at multiples of v.
+            if (n.slot < 0 || static_cast<size_t>(n.slot) >= slot_elems.size()) return out;
+            int64_t lo = x.c0;
+            int64_t hi = x.c0;
+            for (size_t e = 0; e < x.w.size(); ++e) {
+                int64_t a = n.box[e].first;
+                int64_t b = n.box[e].second - 1;
+                if (e == d) {
+                    a = (a + v - 1) / v * v;
+                    b = b / v * v;
+                }
+                if (b < a) return out;
+                lo += std::min(x.w[e] * a, x.w[e] * b);
+                hi += std::max(x.w[e] * a, x.w[e] * b);
+            }
+            if (lo - m < 0 || hi - m + wv - 1 > slot_elems[static_cast<size_t>(n.slot)] - 1)
+                return out;
+            out.ok = true;
+            out.width = static_cast<int>(wv);
+            out.m = m;
+            out.step = s;
+            return out;
+        }
+
+        const char* lane_name(int64_t i) {
+            static const char* names[] = {".x", ".y", ".z", ".w"};
+            return names[i];
+        }
+
         kernel_code emit_tiled(const pointwise_request& r, const tiling& t) {
+            const kexpr& k = *r.expr;
             const size_t rank = r.shape.size();
             const size_t q = rank - 1;
             const size_t p = static_cast<size_t>(t.p);
-            const int64_t ntq = (r.shape[q] + tile - 1) / tile;
-            const int64_t ntp = (r.shape[p] + tile - 1) / tile;
+            const int64_t extent_p = r.shape[p];
+            const int64_t extent_q = r.shape[q];
+            const int64_t ntq = (extent_q + tile - 1) / tile;
+            const int64_t ntp = (extent_p + tile - 1) / tile;
             std::vector<int64_t> other_shape;
             std::vector<size_t> other_dims;
             for (size_t d = 0; d < rank; ++d) {
@@ -345,6 +420,56 @@ namespace porch::cg {
                 other_dims.push_back(d);
             }
             const int64_t others = ir::numel(other_shape);
+            const size_t n_stage = t.staged.size();
+            const std::vector<char> in_stage = staged_mask(k, t);
+
+            // Phase 1 width: elements per lane along p.
+            int64_t V = 1;
+            for (const int64_t v : {int64_t{4}, int64_t{2}}) {
+                if (extent_p % v != 0) continue;
+                bool uniform = true;
+                bool useful = false;
+                for (size_t id = 0; id < k.nodes.size(); ++id) {
+                    if (!in_stage[id]) continue;
+                    const knode& n = k.at(static_cast<int>(id));
+                    if (n.op == kop::select && !uniform_over(n.cond, p, v)) uniform = false;
+                    if (n.op == kop::load && !n.index.is_affine) uniform = false;
+                    if (n.op == kop::load && plan_vector_load(n, p, v, r.slot_elems).ok)
+                        useful = true;
+                }
+                if (uniform && useful) {
+                    V = v;
+                    break;
+                }
+            }
+            // Phase 2 width: outputs per lane along q (128-bit stores).
+            int64_t W = (extent_q % 4 == 0) ? 4 : 1;
+            {
+                std::vector<char> phase2(k.nodes.size(), 0);
+                std::vector<int> stack{r.root};
+                while (!stack.empty()) {
+                    const int id = stack.back();
+                    stack.pop_back();
+                    if (id < 0 || phase2[id]) continue;
+                    bool staged_root = false;
+                    for (const int sroot : t.staged) staged_root = staged_root || sroot == id;
+                    phase2[id] = 1;
+                    if (staged_root) continue;
+                    const knode& n = k.at(id);
+                    if (n.op == kop::select && !uniform_over(n.cond, q, W)) W = 1;
+                    if (n.op == kop::load && !n.index.is_affine) W = 1;
+                    stack.push_back(n.a);
+                    stack.push_back(n.b);
+                }
+            }
+            // Selects of the staged subtrees decided once per tile (up to 2).
+            std::vector<int> hoisted;
+            for (size_t id = 0; id < k.nodes.size() && hoisted.size() < 2; ++id) {
+                const knode& n = k.at(static_cast<int>(id));
+                if (in_stage[id] && n.op == kop::select && n.cond.lhs.is_affine)
+                    hoisted.push_back(static_cast<int>(id));
+            }
+
             kernel_code kc;
             kc.kind = "pointwise.tiled";
             kc.name = "porch_tiled";
@@ -355,20 +480,21 @@ namespace porch::cg {
             const std::vector<std::string> names = coordinate_names(rank);
             const std::string qs = "q" + std::to_string(q);
             const std::string ps = "q" + std::to_string(p);
-            const size_t n_stage = t.staged.size();
+            const std::string TILE = std::to_string(tile);
 
             std::string& s = kc.source;
             s = kernel_prologue(r.n_slots, T);
             s += "extern \"C\" __global__ void __launch_bounds__(256) porch_tiled(" +
                  kernel_params(r.n_slots) + ") {\n";
-            s += "    __shared__ float stage[" + std::to_string(n_stage) + "][" +
-                 std::to_string(tile) + "][" + std::to_string(tile + 1) + "];\n";
+            s += "    __shared__ float stage[" + std::to_string(n_stage) + "][" + TILE + "][" +
+                 std::to_string(tile + 1) + "];\n";
+            // Consecutive workgroups walk along p: neighbouring tiles read
+            // neighbouring segments of the same source rows.
             s += "    const idx_t tile_id = blockIdx.x;\n";
-            s += "    const idx_t tq = tile_id % " + std::to_string(ntq) + ";\n";
-            s += "    const idx_t tp = (tile_id / " + std::to_string(ntq) + ") % " +
-                 std::to_string(ntp) + ";\n";
+            s += "    const idx_t tp = tile_id % " + std::to_string(ntp) + ";\n";
+            s += "    const idx_t tq = (tile_id / " + std::to_string(ntp) + ") % " +
+                 std::to_string(ntq) + ";\n";
             s += "    const idx_t rest = tile_id / " + std::to_string(ntq * ntp) + ";\n";
-            // Coordinates of the other dimensions, from `rest`.
             {
                 const std::vector<int64_t> ostr = ir::contiguous_strides(other_shape);
                 for (size_t i = 0; i < other_dims.size(); ++i) {
@@ -378,86 +504,233 @@ namespace porch::cg {
                     else
                         value = "(rest / " + std::to_string(ostr[i]) + ") % " +
                                 std::to_string(other_shape[i]);
-                    s += "    const idx_t q" + std::to_string(other_dims[i]) + " = " +
-                         value + ";\n";
+                    s += "    const idx_t q" + std::to_string(other_dims[i]) + " = " + value + ";\n";
                 }
                 if (other_dims.empty()) s += "    (void)rest;\n";
             }
+            s += "    const idx_t pbase = tp * " + TILE + ";\n";
+            s += "    const idx_t qbase = tq * " + TILE + ";\n";
             s += "    const int tid = threadIdx.x;\n";
 
-            auto load_fn = [&](emitter& em) {
-                return [&r, &names, &em](int id) {
-                    (void)em;
-                    const knode& n = r.expr->at(id);
-                    return std::vector<std::string>{
-                        "a" + std::to_string(n.slot) + "[" + index_text(n.index, names) + "]"
-                    };
-                };
-            };
+            // Per-tile decision of the hoisted selects: 1 = first branch on
+            // the whole tile, 2 = second branch, 0 = mixed.
+            for (size_t h = 0; h < hoisted.size(); ++h) {
+                const kcond& c = k.at(hoisted[h]).cond;
+                std::string lo = std::to_string(c.lhs.c0);
+                std::string hi = lo;
+                for (size_t d = 0; d < rank; ++d) {
+                    const int64_t w = c.lhs.w[d];
+                    if (w == 0) continue;
+                    std::string a, b;
+                    if (d == p) {
+                        a = "pbase";
+                        b = "(pbase + " + std::to_string(tile - 1) + " < " + std::to_string(extent_p) +
+                            " ? pbase + " + std::to_string(tile - 1) + " : (idx_t)" +
+                            std::to_string(extent_p - 1) + ")";
+                    }
+                    else if (d == q) {
+                        a = "qbase";
+                        b = "(qbase + " + std::to_string(tile - 1) + " < " + std::to_string(extent_q) +
+                            " ? qbase + " + std::to_string(tile - 1) + " : (idx_t)" +
+                            std::to_string(extent_q - 1) + ")";
+                    }
+                    else {
+                        a = b = "q" + std::to_string(d);
+                    }
+                    const std::string ws = std::to_string(w);
+                    lo += " + " + ws + " * " + (w > 0 ? a : b);
+                    hi += " + " + ws + " * " + (w > 0 ? b : a);
+                }
+                const std::string H = std::to_string(h);
+                s += "    const idx_t lo" + H + " = " + lo + ";\n";
+                s += "    const idx_t hi" + H + " = " + hi + ";\n";
+                s += "    const int mode" + H + " = (hi" + H + " < " + std::to_string(c.bound) +
+                     ") ? 1 : ((lo" + H + " >= " + std::to_string(c.bound) + ") ? 2 : 0);\n";
+            }
+
             auto cond_fn = [&](const kcond& c) {
                 return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
             };
-            auto in_range = ps + " < " + std::to_string(r.shape[p]) + " && " + qs +
-                            " < " + std::to_string(r.shape[q]);
+            const bool full_p = extent_p % tile == 0;
+            const bool full_q = extent_q % tile == 0;
 
-            // Phase 1: lanes along p (the staged leaves' near-contiguous dim).
-            s += "    #pragma unroll 4\n";
-            s += "    for (int it = 0; it < " + std::to_string(tile * tile / block_threads) +
-                 "; ++it) {\n";
-            s += "        const int pl = tid & " + std::to_string(tile - 1) + ";\n";
-            s += "        const int ql = (tid >> 6) + it * " +
-                 std::to_string(block_threads / tile) + ";\n";
-            s += "        const idx_t " + ps + " = tp * " + std::to_string(tile) + " + pl;\n";
-            s += "        const idx_t " + qs + " = tq * " + std::to_string(tile) + " + ql;\n";
-            s += "        if (" + in_range + ") {\n";
-            {
+            // ---- phase 1: lanes along p, V elements per lane ----
+            const int64_t lanes_p = tile / V;
+            const int64_t rows1 = block_threads / lanes_p;
+            const int64_t passes1 = tile / rows1;
+            auto phase1_body = [&](const std::vector<int>& modes) {
+                std::string code;
+                code += "        #pragma unroll\n";
+                code += "        for (int it = 0; it < " + std::to_string(passes1) + "; ++it) {\n";
+                code += "            const int pl = (tid % " + std::to_string(lanes_p) + ") * " +
+                        std::to_string(V) + ";\n";
+                code += "            const int ql = tid / " + std::to_string(lanes_p) + " + it * " +
+                        std::to_string(rows1) + ";\n";
+                code += "            const idx_t " + ps + " = pbase + pl;\n";
+                code += "            const idx_t " + qs + " = qbase + ql;\n";
+                std::string guard;
+                if (!full_p) guard += ps + " < " + std::to_string(extent_p);
+                if (!full_q) guard += std::string(guard.empty() ? "" : " && ") + qs + " < " +
+                                      std::to_string(extent_q);
+                std::string indent = "            ";
+                if (!guard.empty()) {
+                    code += indent + "if (" + guard + ") {\n";
+                    indent += "    ";
+                }
                 std::string body;
-                emitter em(*r.expr, body, 1);
-                em.indent = "            ";
-                em.load = load_fn(em);
+                emitter em(k, body, static_cast<int>(V));
+                em.indent = indent;
                 em.condition = cond_fn;
                 em.row_value = [](int) -> std::string {
                     throw std::logic_error("row value in a pointwise kernel");
                 };
+                em.forced_branch = [&](int id) {
+                    for (size_t h = 0; h < hoisted.size(); ++h) {
+                        if (hoisted[h] == id) return modes[h] == 1 ? 0 : (modes[h] == 2 ? 1 : -1);
+                    }
+                    return -1;
+                };
+                em.load = [&](int id) {
+                    const knode& n = k.at(id);
+                    const std::string base = "a" + std::to_string(n.slot);
+                    const std::string idx = index_text(n.index, names);
+                    std::vector<std::string> lanes(static_cast<size_t>(V));
+                    const int64_t step = n.index.is_affine ? n.index.w[p] : 0;
+                    if (V > 1 && step == 0) {
+                        const std::string u = em.fresh("u");
+                        em.line("const float " + u + " = " + base + "[" + idx + "];");
+                        for (auto& lane : lanes) lane = u;
+                        return lanes;
+                    }
+                    const vector_load vl = plan_vector_load(n, p, V, r.slot_elems);
+                    if (vl.ok) {
+                        const std::string w = em.fresh("w");
+                        const std::string type = vl.width == 4 ? "float4" : "float2";
+                        em.line("const " + type + " " + w + " = *reinterpret_cast<const " + type +
+                                "*>(" + base + " + " + idx + " - " + std::to_string(vl.m) + ");");
+                        for (int64_t e = 0; e < V; ++e) lanes[e] = w + lane_name(vl.m + vl.step * e);
+                        return lanes;
+                    }
+                    if (V == 1) return std::vector<std::string>{base + "[" + idx + "]"};
+                    const std::string ptr = em.fresh("p");
+                    em.line("const float* " + ptr + " = " + base + " + " + idx + ";");
+                    for (int64_t e = 0; e < V; ++e)
+                        lanes[e] = ptr + "[" + std::to_string(step * e) + "]";
+                    return lanes;
+                };
                 for (size_t i = 0; i < n_stage; ++i) {
-                    const std::string v = em.emit(t.staged[i])[0];
-                    em.line("stage[" + std::to_string(i) + "][pl][ql] = " + v + ";");
+                    const std::vector<std::string> v = em.emit(t.staged[i]);
+                    for (int64_t e = 0; e < V; ++e)
+                        em.line("stage[" + std::to_string(i) + "][pl + " + std::to_string(e) +
+                                "][ql] = " + v[e] + ";");
                 }
-                s += body;
+                code += body;
+                if (!guard.empty()) code += "            }\n";
+                code += "        }\n";
+                return code;
+            };
+            // One version of phase 1 per combination of hoisted-select modes.
+            std::vector<std::vector<int>> combos{{}};
+            for (size_t h = 0; h < hoisted.size(); ++h) {
+                std::vector<std::vector<int>> next;
+                for (const auto& c : combos)
+                    for (const int m : {1, 2, 0}) {
+                        auto d = c;
+                        d.push_back(m);
+                        next.push_back(d);
+                    }
+                combos = next;
             }
-            s += "        }\n    }\n";
+            for (size_t c = 0; c < combos.size(); ++c) {
+                std::string test;
+                for (size_t h = 0; h < hoisted.size(); ++h) {
+                    if (!test.empty()) test += " && ";
+                    test += "mode" + std::to_string(h) + " == " + std::to_string(combos[c][h]);
+                }
+                if (combos.size() == 1) s += "    {\n";
+                else if (c == 0) s += "    if (" + test + ") {\n";
+                else if (c + 1 == combos.size()) s += "    } else {\n";
+                else s += "    } else if (" + test + ") {\n";
+                s += phase1_body(combos[c]);
+            }
+            s += "    }\n";
             s += "    __syncthreads();\n";
-            // Phase 2: lanes along q (the output's contiguous dim).
-            s += "    #pragma unroll 4\n";
-            s += "    for (int it = 0; it < " + std::to_string(tile * tile / block_threads) +
-                 "; ++it) {\n";
-            s += "        const int ql = tid & " + std::to_string(tile - 1) + ";\n";
-            s += "        const int pl = (tid >> 6) + it * " +
-                 std::to_string(block_threads / tile) + ";\n";
-            s += "        const idx_t " + ps + " = tp * " + std::to_string(tile) + " + pl;\n";
-            s += "        const idx_t " + qs + " = tq * " + std::to_string(tile) + " + ql;\n";
-            s += "        if (" + in_range + ") {\n";
+
+            // ---- phase 2: lanes along q, W outputs per lane ----
+            const int64_t lanes_q = tile / W;
+            const int64_t rows2 = block_threads / lanes_q;
+            const int64_t passes2 = tile / rows2;
+            s += "    #pragma unroll\n";
+            s += "    for (int it = 0; it < " + std::to_string(passes2) + "; ++it) {\n";
+            s += "        const int ql = (tid % " + std::to_string(lanes_q) + ") * " + std::to_string(W) + ";\n";
+            s += "        const int pl = tid / " + std::to_string(lanes_q) + " + it * " +
+                 std::to_string(rows2) + ";\n";
+            s += "        const idx_t " + ps + " = pbase + pl;\n";
+            s += "        const idx_t " + qs + " = qbase + ql;\n";
+            std::string guard;
+            if (!full_p) guard += ps + " < " + std::to_string(extent_p);
+            if (!full_q) guard += std::string(guard.empty() ? "" : " && ") + qs + " < " +
+                                  std::to_string(extent_q);
+            std::string indent = "        ";
+            if (!guard.empty()) {
+                s += indent + "if (" + guard + ") {\n";
+                indent += "    ";
+            }
             {
                 std::string body;
-                emitter em(*r.expr, body, 1);
-                em.indent = "            ";
-                em.load = load_fn(em);
+                emitter em(k, body, static_cast<int>(W));
+                em.indent = indent;
                 em.condition = cond_fn;
                 em.row_value = [](int) -> std::string {
                     throw std::logic_error("row value in a pointwise kernel");
                 };
                 em.override_node = [&](int id) -> std::vector<std::string> {
                     for (size_t i = 0; i < n_stage; ++i) {
-                        if (t.staged[i] == id)
-                            return {"stage[" + std::to_string(i) + "][pl][ql]"};
+                        if (t.staged[i] != id) continue;
+                        std::vector<std::string> out;
+                        for (int64_t e = 0; e < W; ++e)
+                            out.push_back("stage[" + std::to_string(i) + "][pl][ql + " +
+                                          std::to_string(e) + "]");
+                        return out;
                     }
                     return {};
                 };
-                const std::string v = em.emit(r.root)[0];
+                em.load = [&](int id) {
+                    const knode& n = k.at(id);
+                    const std::string base = "a" + std::to_string(n.slot);
+                    const std::string idx = index_text(n.index, names);
+                    if (W == 1) return std::vector<std::string>{base + "[" + idx + "]"};
+                    std::vector<std::string> lanes(static_cast<size_t>(W));
+                    const int64_t step = n.index.w[q];
+                    if (step == 0) {
+                        const std::string u = em.fresh("u");
+                        em.line("const float " + u + " = " + base + "[" + idx + "];");
+                        for (auto& lane : lanes) lane = u;
+                        return lanes;
+                    }
+                    const vector_load vl = plan_vector_load(n, q, W, r.slot_elems);
+                    if (vl.ok && vl.width == 4 && vl.m == 0 && vl.step == 1) {
+                        const std::string w = em.fresh("w");
+                        em.line("const float4 " + w + " = *reinterpret_cast<const float4*>(" +
+                                base + " + " + idx + ");");
+                        return std::vector<std::string>{w + ".x", w + ".y", w + ".z", w + ".w"};
+                    }
+                    const std::string ptr = em.fresh("p");
+                    em.line("const float* " + ptr + " = " + base + " + " + idx + ";");
+                    for (int64_t e = 0; e < W; ++e)
+                        lanes[e] = ptr + "[" + std::to_string(step * e) + "]";
+                    return lanes;
+                };
+                const std::vector<std::string> v = em.emit(r.root);
                 s += body;
-                s += "            out[" + output_index(r.shape) + "] = " + v + ";\n";
+                if (W == 4)
+                    s += indent + "*reinterpret_cast<float4*>(out + " + output_index(r.shape) +
+                         ") = make_float4(" + v[0] + ", " + v[1] + ", " + v[2] + ", " + v[3] + ");\n";
+                else
+                    s += indent + "out[" + output_index(r.shape) + "] = " + v[0] + ";\n";
             }
-            s += "        }\n    }\n}\n";
+            if (!guard.empty()) s += "        }\n";
+            s += "    }\n}\n";
             return kc;
         }
 

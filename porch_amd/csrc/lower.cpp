@@ -119,7 +119,14 @@ namespace porch::cg {
                 break;
         }
         auto found = interned.find(key);
-        if (found != interned.end()) return found->second;
+        if (found != interned.end()) {
+            knode& known = nodes[static_cast<size_t>(found->second)];
+            for (size_t d = 0; d < known.box.size() && d < n.box.size(); ++d) {
+                known.box[d].first = std::min(known.box[d].first, n.box[d].first);
+                known.box[d].second = std::max(known.box[d].second, n.box[d].second);
+            }
+            return found->second;
+        }
         const int id = static_cast<int>(nodes.size());
         nodes.push_back(std::move(n));
         interned.emplace(std::move(key), id);
@@ -274,6 +281,7 @@ namespace porch::cg {
             load.op = kop::load;
             load.slot = input_slot[static_cast<size_t>(n.input)];
             load.index = lin;
+            load.box = box;
             return out.add(load);
         }
         auto bound_it = bound.find(id);
@@ -283,6 +291,7 @@ namespace porch::cg {
             load.op = kop::load;
             load.slot = bound_it->second.slot;
             load.index = lin;
+            load.box = box;
             return out.add(load);
         }
         if (n.is_scalar) return at(id, {});
@@ -305,6 +314,7 @@ namespace porch::cg {
             load.op = kop::load;
             load.slot = bound_it->second.slot;
             load.index = linearize(coords, n.out);
+            load.box = box;
             return out.add(load);
         }
 
@@ -316,6 +326,7 @@ namespace porch::cg {
                 if (load.slot < 0)
                     throw std::logic_error("input without a kernel slot");
                 load.index = linearize(coords, n.out);
+                load.box = box;
                 return out.add(load);
             }
             case ir::op::scalar: {

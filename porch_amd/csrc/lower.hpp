@@ -66,6 +66,9 @@ namespace porch::cg {
         int b = -1;
         int slot = -1; // load: kernel argument slot
         ival index;    // load
+        // load: ranges [lo, hi) of the kernel coordinates under which the
+        // load executes (the union over the branches that reach it)
+        std::vector<std::pair<int64_t, int64_t>> box;
         float value = 0.0F;
         kcond cond;    // select
         int row = -1;  // row_value

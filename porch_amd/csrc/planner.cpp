@@ -49,6 +49,13 @@ namespace porch::plan {
                 return g.n_inputs + static_cast<int>(plan.temp_elems.size());
             }
 
+            // Floats each kernel slot's buffer is guaranteed to hold.
+            [[nodiscard]] std::vector<int64_t> slot_elems() const {
+                std::vector<int64_t> elems(plan.input_elems.begin(), plan.input_elems.end());
+                elems.insert(elems.end(), plan.temp_elems.begin(), plan.temp_elems.end());
+                return elems;
+            }
+
             void bind_inputs(cg::lowering& low) const {
                 for (int i = 0; i < g.n_inputs; ++i) low.input_slot[static_cast<size_t>(i)] = i;
                 for (const auto& [node, temp] : temp_of) {
@@ -374,6 +381,7 @@ namespace porch::plan {
                 r.root = low.at(id, low.identity());
                 r.shape = shape;
                 r.n_slots = n_slots();
+                r.slot_elems = slot_elems();
                 r.width = width;
                 add_step(cg::emit_pointwise(r), dest);
             }
