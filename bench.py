@@ -11,14 +11,19 @@ back to back, wall clock between synchronisations) and region B (the same K
 steps with a HIP event pair attached to each kernel dispatch; their mean is
 the per-launch duration behind `roofline.achieved`).
 
-The headline line is config c2 (the strided-slice + transpose + concat view
-chain over x fp32 [4096, 4096]): HBM GB/s of algorithmic bytes (all of x
-read, the output written).  The other configs are reported beside it under
+The headline line is the view chain (strided slices + transposes + concat
+over x fp32 [4096, 4096]): HBM GB/s of algorithmic bytes (all of x read, the
+output written).  The other workloads are reported beside it under
 "configs", each with its roofline fraction and JIT latency.  The host
 evaluator (the oracle, OpenMP) is timed on this machine's cores as the CPU
 baseline.
 
-    python bench.py [--steps K] [--warmup W] [--configs c1,c2,...] [--no-cpu]
+`roofline.traffic` is the HBM bytes per launch that rocprofv3's FETCH_SIZE
+and WRITE_SIZE counters read for the same kernel, scaled by what they read
+for a copy kernel of known size; both come from the counter summaries under
+profiles/ (null when a workload has none).
+
+    python bench.py [--steps K] [--warmup W] [--configs view_chain,...] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -43,25 +48,42 @@ FP32_MFMA_PEAK_TFLOPS = 157.3    # 256 CU x 256 flop/clk x 2.4 GHz
 
 METRIC = "fused-graph HBM GB/s (% of peak); fp32 matmul TFLOP/s (% MFMA peak); JIT ms"
 
-# Algorithmic work per step (bytes for HBM-bound graphs, flops for c5).
+# Algorithmic work per step (bytes for HBM-bound graphs, flops for the matmul).
 WORK = {
-    "c1": ("hbm", 3 * 4 * (1 << 20)),
-    "c2": ("hbm", 4096 * 4096 * 4 + 4096 * 2048 * 4),
-    "c3": ("hbm", 2 * 8192 * 4096 * 4),
-    "c4": ("hbm", 16384 * 2048 * 4 + 2 * 2048 * 4 + 16384 * 4),
-    "c5": ("mfma", 2 * 4096 ** 3),
+    "elementwise": ("hbm", 3 * 4 * (1 << 20)),
+    "view_chain": ("hbm", 4096 * 4096 * 4 + 4096 * 2048 * 4),
+    "softmax": ("hbm", 2 * 8192 * 4096 * 4),
+    "logistic_rowsum": ("hbm", 16384 * 2048 * 4 + 2 * 2048 * 4 + 16384 * 4),
+    "matmul_epilogue": ("mfma", 2 * 4096 ** 3),
     "copy": ("hbm", 2 * 8192 * 8192 * 4),
 }
 DESCRIPTION = {
-    "c1": "(a + b) * 2 - 1, a, b fp32 [1048576]",
-    "c2": "concat(transpose(x[0::2,1::2]), transpose(x[1::2,0::2]), 0) + 1, x fp32 [4096,4096]",
-    "c3": "softmax(x, 1), x fp32 [8192,4096]",
-    "c4": "sum(logistic(relu(x*bcast(w) + bcast(bias))), 1), x fp32 [16384,2048]",
-    "c5": "relu(A @ B + bcast(bias)) - 0.5, A, B fp32 [4096,4096]",
+    "elementwise": "(a + b) * 2 - 1, a, b fp32 [1048576]",
+    "view_chain": "concat(transpose(x[0::2,1::2]), transpose(x[1::2,0::2]), 0) + 1, x fp32 [4096,4096]",
+    "softmax": "softmax(x, 1), x fp32 [8192,4096]",
+    "logistic_rowsum": "sum(logistic(relu(x*bcast(w) + bcast(bias))), 1), x fp32 [16384,2048]",
+    "matmul_epilogue": "relu(A @ B + bcast(bias)) - 0.5, A, B fp32 [4096,4096]",
     "copy": "reshape(x) copy, x fp32 [8192,8192] (byte-counter calibration)",
 }
 # Input copies rotated through so that a step never re-reads cached data.
-ROTATION = {"c1": 48, "c2": 8, "c3": 4, "c4": 6, "c5": 1, "copy": 2}
+ROTATION = {"elementwise": 48, "view_chain": 8, "softmax": 4, "logistic_rowsum": 6,
+            "matmul_epilogue": 1, "copy": 2}
+# Counter summaries (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) per workload.
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def profiled_traffic(name: str):
+    """HBM bytes per launch from the workload's committed counter summary."""
+    if not os.path.isdir(PROFILES):
+        return None
+    for entry in sorted(os.listdir(PROFILES)):
+        if not (entry.startswith(name + ".") and entry.endswith(".txt")):
+            continue
+        with open(os.path.join(PROFILES, entry)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    return None
 
 
 def log(message: str) -> None:
@@ -153,7 +175,7 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
         "kernel_ms_mean": float(np.mean(kernel_ms)),
         "kernel_ms_median": float(np.median(kernel_ms)),
         "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
-                     "frac": achieved / peak, "traffic": None},
+                     "frac": achieved / peak, "traffic": profiled_traffic(name)},
         "jit_ms": {"cold": cold_ms, "hit": float(np.median(hit_us)) / 1e3},
         "steps": steps,
     }
@@ -175,7 +197,7 @@ def cpu_baseline(name: str, max_seconds: float = 20.0) -> dict:
         tensors.append(t)
     sample = "full workload"
     scale = 1.0
-    if name == "c5":
+    if name == "matmul_epilogue":
         rows = 256  # 1/16 of the rows of A; time scaled by 16
         a, b, bias = values
         tensors[0]._state = porch._State([rows, 4096], porch.device())
@@ -207,12 +229,12 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    parser.add_argument("--configs", default="elementwise,view_chain,softmax,logistic_rowsum,matmul_epilogue")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: porch's fused-graph path has no multi-GPU "
-              "execution (see DESIGN.md for how it would shard); run with --gpus 1.",
+        print("bench.py measures one GPU: porch's fused-graph path runs every graph on "
+              "one device and has no multi-GPU execution; run with --gpus 1.",
               file=sys.stderr)
         return 2
 
@@ -227,7 +249,7 @@ def main() -> int:
     configs = [c for c in args.configs.split(",") if c]
     results = {}
     for name in configs:
-        # c5 steps are long; keep its timed region short.
+        # Matmul steps are long; keep its timed region short.
         steps = args.steps if WORK[name][0] == "hbm" else max(3, args.steps // 40)
         warmup = args.warmup if WORK[name][0] == "hbm" else max(1, args.warmup // 10)
         log(f"{name}: {DESCRIPTION[name]} ({steps} steps)")
@@ -241,7 +263,7 @@ def main() -> int:
             log(f"{name}: cpu {results[name]['cpu_baseline']['value']:.2f} "
                 f"{results[name]['cpu_baseline']['unit']} on {results[name]['cpu_baseline']['cores']} threads")
 
-    head = "c2" if "c2" in results else configs[0]
+    head = "view_chain" if "view_chain" in results else configs[0]
     h = results[head]
     line = {
         "metric": METRIC,

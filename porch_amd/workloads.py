@@ -2,14 +2,16 @@
 
 Each is porch source over seeded synthetic inputs (splitmix64, see
 porch_amd.synth):
-  c1  (a + b) * 2 - 1                     a, b ~ U[-1,1] length 2^20
-  c2  concat(transpose(x[0::2,1::2]), transpose(x[1::2,0::2]), 0) + 1
-                                          x ~ N(0,1) [4096,4096]
-  c3  softmax(x, 1)                       x ~ N(0,3) [8192,4096], 1% set to +20
-  c4  sum(logistic(relu(x*w + bias)), 1)  x ~ N(0,1) [16384,2048], w ~ U(.5,1.5),
-                                          bias ~ N(0,.1) [1,2048]
-  c5  relu(A @ B + bias) - 0.5            A, B ~ U(-1,1)/64 [4096,4096],
-                                          bias ~ N(0,.01) [1,4096]
+  elementwise      (a + b) * 2 - 1       a, b ~ U[-1,1] length 2^20
+  view_chain       concat(transpose(x[0::2,1::2]), transpose(x[1::2,0::2]), 0) + 1
+                                         x ~ N(0,1) [4096,4096]
+  softmax          softmax(x, 1)         x ~ N(0,3) [8192,4096], 1% set to +20
+  logistic_rowsum  sum(logistic(relu(x*w + bias)), 1)
+                                         x ~ N(0,1) [16384,2048], w ~ U(.5,1.5),
+                                         bias ~ N(0,.1) [1,2048]
+  matmul_epilogue  relu(A @ B + bias) - 0.5
+                                         A, B ~ U(-1,1)/64 [4096,4096],
+                                         bias ~ N(0,.01) [1,4096]
 and `copy`, reshape(x) over x [8192,8192]: a plain copy of known size used to
 calibrate hardware byte counters.
 """
@@ -26,24 +28,24 @@ from porch_amd import synth
 def config_inputs(name: str, size: dict | None = None) -> list[np.ndarray]:
     s = dict(CONFIG_SIZES[name])
     s.update(size or {})
-    if name == "c1":
+    if name == "elementwise":
         n = s["n"]
         return [synth.uniform(n, 101, -1.0, 1.0), synth.uniform(n, 102, -1.0, 1.0)]
-    if name == "c2":
+    if name == "view_chain":
         n = s["n"]
         return [synth.normal(n * n, 201, 0.0, 1.0)]
-    if name == "c3":
+    if name == "softmax":
         rows, cols = s["rows"], s["cols"]
         x = synth.normal(rows * cols, 301, 0.0, 3.0)
         synth.replace(x, 302, 0.01, 20.0)
         return [x]
-    if name == "c4":
+    if name == "logistic_rowsum":
         rows, cols = s["rows"], s["cols"]
         return [synth.normal(rows * cols, 401, 0.0, 1.0), synth.uniform(cols, 402, 0.5, 1.5),
                 synth.normal(cols, 403, 0.0, 0.1)]
     if name == "copy":
         return [synth.uniform(s["n"] * s["n"], 601, -1.0, 1.0)]
-    if name == "c5":
+    if name == "matmul_epilogue":
         m, k, n = s["m"], s["k"], s["n"]
         return [synth.uniform(m * k, 501, -1.0, 1.0) / np.float32(64.0),
                 synth.uniform(k * n, 502, -1.0, 1.0) / np.float32(64.0),
@@ -52,11 +54,11 @@ def config_inputs(name: str, size: dict | None = None) -> list[np.ndarray]:
 
 
 CONFIG_SIZES = {
-    "c1": {"n": 1 << 20},
-    "c2": {"n": 4096},
-    "c3": {"rows": 8192, "cols": 4096},
-    "c4": {"rows": 16384, "cols": 2048},
-    "c5": {"m": 4096, "k": 4096, "n": 4096},
+    "elementwise": {"n": 1 << 20},
+    "view_chain": {"n": 4096},
+    "softmax": {"rows": 8192, "cols": 4096},
+    "logistic_rowsum": {"rows": 16384, "cols": 2048},
+    "matmul_epilogue": {"m": 4096, "k": 4096, "n": 4096},
     "copy": {"n": 8192},
 }
 
@@ -64,15 +66,15 @@ CONFIG_SIZES = {
 def config_shapes(name: str, size: dict | None = None) -> list[list[int]]:
     s = dict(CONFIG_SIZES[name])
     s.update(size or {})
-    if name == "c1":
+    if name == "elementwise":
         return [[s["n"]], [s["n"]]]
-    if name == "c2":
+    if name == "view_chain":
         return [[s["n"], s["n"]]]
-    if name == "c3":
+    if name == "softmax":
         return [[s["rows"], s["cols"]]]
-    if name == "c4":
+    if name == "logistic_rowsum":
         return [[s["rows"], s["cols"]], [1, s["cols"]], [1, s["cols"]]]
-    if name == "c5":
+    if name == "matmul_epilogue":
         return [[s["m"], s["k"]], [s["k"], s["n"]], [1, s["n"]]]
     if name == "copy":
         return [[s["n"], s["n"]]]
@@ -83,24 +85,24 @@ def config_graph(name: str, tensors, size: dict | None = None):
     """The benchmark graph of config `name` over `tensors` (porch source)."""
     s = dict(CONFIG_SIZES[name])
     s.update(size or {})
-    if name == "c1":
+    if name == "elementwise":
         a, b = tensors
         return (a + b) * 2.0 - 1.0
-    if name == "c2":
+    if name == "view_chain":
         (x,) = tensors
         n = s["n"]
         return porch.concat(
             porch.transpose(x[porch.slice(0, n, 2), porch.slice(1, n, 2)]),
             porch.transpose(x[porch.slice(1, n, 2), porch.slice(0, n, 2)]), 0) + 1.0
-    if name == "c3":
+    if name == "softmax":
         (x,) = tensors
         return porch.softmax(x, 1)
-    if name == "c4":
+    if name == "logistic_rowsum":
         x, w, b = tensors
         shape = [s["rows"], s["cols"]]
         return porch.sum(porch.logistic(porch.relu(
             x * porch.broadcast_to(w, shape) + porch.broadcast_to(b, shape))), 1)
-    if name == "c5":
+    if name == "matmul_epilogue":
         a, b, bias = tensors
         shape = [s["m"], s["n"]]
         return porch.relu(porch.matmul(a, b) + porch.broadcast_to(bias, shape)) - 0.5

@@ -49,16 +49,16 @@ def assert_close(gpu_out, ref, rel):
 # -- config 1: elementwise chain, bit-exact ----------------------------------
 
 @pytest.mark.parametrize("n", [1, 3, 4, 5, 1000, 4099, 1 << 20])
-def test_c1_elementwise_bit_exact(gpu, n):
-    out, ref, _ = gpu_and_oracle(gpu, "c1", {"n": n})
+def test_elementwise_bit_exact(gpu, n):
+    out, ref, _ = gpu_and_oracle(gpu, "elementwise", {"n": n})
     assert_bits_equal(out, ref)
 
 
 # -- config 2: strided slice + transpose + concat, bit-exact ------------------
 
 @pytest.mark.parametrize("n", [2, 6, 62, 64, 130, 4096])
-def test_c2_view_chain_bit_exact(gpu, n):
-    out, ref, (x,) = gpu_and_oracle(gpu, "c2", {"n": n})
+def test_view_chain_bit_exact(gpu, n):
+    out, ref, (x,) = gpu_and_oracle(gpu, "view_chain", {"n": n})
     assert_bits_equal(out, ref)
     # size-independent closed form y[i, j] = x[2j, 2i+1] + 1 (top half)
     xm = x.reshape(n, n)
@@ -70,8 +70,8 @@ def test_c2_view_chain_bit_exact(gpu, n):
 @pytest.mark.parametrize("size", [{"rows": 3, "cols": 7}, {"rows": 17, "cols": 256},
                                   {"rows": 64, "cols": 4100}, {"rows": 8, "cols": 12288},
                                   {"rows": 8192, "cols": 4096}])
-def test_c3_softmax_within_1e6(gpu, size):
-    out, ref, _ = gpu_and_oracle(gpu, "c3", size)
+def test_softmax_within_1e6(gpu, size):
+    out, ref, _ = gpu_and_oracle(gpu, "softmax", size)
     assert_close(out, ref, 1e-6)
     assert np.allclose(out.sum(axis=1), 1.0, atol=2e-5)
 
@@ -80,8 +80,8 @@ def test_c3_softmax_within_1e6(gpu, size):
 
 @pytest.mark.parametrize("size", [{"rows": 5, "cols": 9}, {"rows": 33, "cols": 2048},
                                   {"rows": 16384, "cols": 2048}, {"rows": 4, "cols": 10000}])
-def test_c4_row_reduction_within_1e5(gpu, size):
-    out, ref, _ = gpu_and_oracle(gpu, "c4", size)
+def test_logistic_rowsum_within_1e5(gpu, size):
+    out, ref, _ = gpu_and_oracle(gpu, "logistic_rowsum", size)
     assert_close(out, ref, 1e-5)
 
 
@@ -89,18 +89,18 @@ def test_c4_row_reduction_within_1e5(gpu, size):
 
 @pytest.mark.parametrize("size", [{"m": 2, "k": 3, "n": 5}, {"m": 67, "k": 129, "n": 33},
                                   {"m": 256, "k": 4096, "n": 128}])
-def test_c5_matmul_epilogue_within_1e4(gpu, size):
-    out, ref, _ = gpu_and_oracle(gpu, "c5", size)
+def test_matmul_epilogue_within_1e4(gpu, size):
+    out, ref, _ = gpu_and_oracle(gpu, "matmul_epilogue", size)
     assert_close(out, ref, 1e-4)
 
 
-def test_c5_full_size_on_a_row_sample(gpu):
+def test_matmul_epilogue_full_size_on_a_row_sample(gpu):
     porch = gpu
-    size = CONFIG_SIZES["c5"]
-    a, b, bias = config_inputs("c5")
+    size = CONFIG_SIZES["matmul_epilogue"]
+    a, b, bias = config_inputs("matmul_epilogue")
     m, k, n = size["m"], size["k"], size["n"]
     ta, tb, tbias = porch.tensor([m, k], a), porch.tensor([k, n], b), porch.tensor([1, n], bias)
-    out = porch.materialize(config_graph("c5", [ta, tb, tbias])).cpu().reshape(m, n)
+    out = porch.materialize(config_graph("matmul_epilogue", [ta, tb, tbias])).cpu().reshape(m, n)
     rows = np.array([0, 1, 2, 777, 2048, 4000, 4095])
     sample = porch.tensor([rows.size, k], a.reshape(m, k)[rows])
     ref = host.evaluate(porch.relu(porch.matmul(sample, tb) + porch.broadcast_to(tbias, [rows.size, n])) - 0.5)

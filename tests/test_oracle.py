@@ -36,8 +36,8 @@ def oracle_of(name, size, inputs=None):
     return host.evaluate(config_graph(name, tensors, size)), inputs
 
 
-def test_c1_elementwise_chain_is_ieee_binary32():
-    out, (a, b) = oracle_of("c1", {"n": 4099})
+def test_elementwise_chain_is_ieee_binary32():
+    out, (a, b) = oracle_of("elementwise", {"n": 4099})
     expected = (a + b) * np.float32(2.0) - np.float32(1.0)  # numpy binary32, same order
     assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
 
@@ -51,16 +51,16 @@ def c2_closed_form(x, n):
 
 
 @pytest.mark.parametrize("n", [2, 6, 64, 130])
-def test_c2_view_chain_matches_closed_form(n):
-    out, (x,) = oracle_of("c2", {"n": n})
+def test_view_chain_matches_closed_form(n):
+    out, (x,) = oracle_of("view_chain", {"n": n})
     assert out.shape == (n, n // 2)
     assert np.array_equal(out, c2_closed_form(x, n))
 
 
-def test_c2_planted_mistake_is_caught():
+def test_view_chain_planted_mistake_is_caught():
     """Swapping the concat operands must fail the closed-form check."""
     n = 8
-    x = config_inputs("c2", {"n": n})[0]
+    x = config_inputs("view_chain", {"n": n})[0]
     t = placeholder([n, n], x)
     wrong = porch.concat(porch.transpose(t[porch.slice(1, n, 2), porch.slice(0, n, 2)]),
                          porch.transpose(t[porch.slice(0, n, 2), porch.slice(1, n, 2)]), 0) + 1.0
@@ -71,9 +71,9 @@ def test_c2_planted_mistake_is_caught():
     assert not np.array_equal(host.evaluate(transposed_slice), c2_closed_form(x, n))
 
 
-def test_c3_softmax_against_float64():
+def test_softmax_against_float64():
     size = {"rows": 64, "cols": 1000}
-    out, (x,) = oracle_of("c3", size)
+    out, (x,) = oracle_of("softmax", size)
     xm = x.reshape(64, 1000)
     # porch's graph subtracts the row max in binary32 (exact IEEE, so numpy
     # reproduces it); the rest is taken in float64 as the exact value.
@@ -91,10 +91,10 @@ def test_c3_softmax_against_float64():
     assert (x == 20.0).any()
 
 
-def test_c3_planted_mistake_is_caught():
+def test_softmax_planted_mistake_is_caught():
     """Dropping the max shift changes nothing mathematically but a wrong
     axis does: softmax over axis 0 must not pass the axis-1 check."""
-    x = config_inputs("c3", {"rows": 16, "cols": 32})[0]
+    x = config_inputs("softmax", {"rows": 16, "cols": 32})[0]
     t = placeholder([16, 32], x)
     wrong = host.evaluate(porch.softmax(t, 0))
     xm = x.reshape(16, 32).astype(np.float64)
@@ -103,9 +103,9 @@ def test_c3_planted_mistake_is_caught():
     assert np.abs(wrong - truth).max() > 1e-3
 
 
-def test_c4_logistic_row_sums_against_float64():
+def test_logistic_row_sums_against_float64():
     size = {"rows": 40, "cols": 2048}
-    out, (x, w, b) = oracle_of("c4", size)
+    out, (x, w, b) = oracle_of("logistic_rowsum", size)
     z = (x.reshape(40, 2048) * w + b).astype(np.float64)  # binary32 product and sum as in porch
     z = np.maximum(z, 0.0)
     truth = (1.0 / (1.0 + np.exp(-z))).sum(axis=1)
@@ -113,9 +113,9 @@ def test_c4_logistic_row_sums_against_float64():
     assert (np.abs(out - truth) / np.abs(truth)).max() < 1e-5
 
 
-def test_c5_matmul_epilogue_against_float64():
+def test_matmul_epilogue_against_float64():
     size = {"m": 48, "k": 4096, "n": 40}
-    out, (a, b, bias) = oracle_of("c5", size)
+    out, (a, b, bias) = oracle_of("matmul_epilogue", size)
     c = a.reshape(48, 4096).astype(np.float64) @ b.reshape(4096, 40).astype(np.float64)
     truth = np.maximum(c + bias.astype(np.float64), 0.0) - 0.5
     assert (np.abs(out - truth) / np.abs(truth)).max() < 1e-4

@@ -6,11 +6,11 @@ import porch_amd as porch
 from tests.helpers import config_graph, config_shapes, placeholder
 
 EXPECTED_KIND = {
-    "c1": "pointwise.flat",
-    "c2": "pointwise.tiled",
-    "c3": "row",
-    "c4": "row",
-    "c5": "gemm",
+    "elementwise": "pointwise.flat",
+    "view_chain": "pointwise.tiled",
+    "softmax": "row",
+    "logistic_rowsum": "row",
+    "matmul_epilogue": "gemm",
 }
 
 
