@@ -1,5 +1,6 @@
 #include "emit_expr.hpp"
 
+#include <cmath>
 #include <stdexcept>
 
 namespace porch::cg {
@@ -7,6 +8,11 @@ namespace porch::cg {
     emitter::emitter(const kexpr& expr, std::string& target, int lanes)
         : k(expr), code(target), width(lanes) {
         frames_.emplace_back();
+    }
+
+    const vrange& emitter::range_of(int id) {
+        if (ranges_.size() != k.nodes.size()) ranges_ = value_ranges(k, row_value_range, refine_range);
+        return ranges_[static_cast<size_t>(id)];
     }
 
     std::string emitter::fresh(const char* prefix) {
@@ -80,19 +86,36 @@ namespace porch::cg {
                 break;
             }
             case kop::exp: {
-                const std::vector<std::string> a = emit(n.a);
+                // exp(0 - v) is exp(-v): the two arguments differ only in the
+                // sign of zero, and exp(+0) = exp(-0) = 1.  The negation then
+                // folds into the first multiply as a source modifier.
+                const knode& arg = k.at(n.a);
+                const bool negate = arg.op == kop::subtract && k.at(arg.a).op == kop::constant &&
+                                    k.at(arg.a).value == 0.0F && !std::signbit(k.at(arg.a).value);
+                const std::vector<std::string> a = emit(negate ? arg.b : n.a);
+                // Arguments proven <= 88 cannot overflow: porch_exp skips the
+                // overflow handling (and the NaN test when NaN is impossible).
+                const vrange& r = range_of(n.a);
+                const char* fn = "expf";
+                if (!std::isnan(r.hi) && r.hi <= 88.0F) fn = r.nan ? "porch_exp" : "porch_exp_finite";
                 for (int e = 0; e < width; ++e) {
                     const std::string name = fresh("v");
-                    line("const float " + name + " = expf(" + a[e] + ");");
+                    const std::string x = negate ? "-" + a[e] : a[e];
+                    line("const float " + name + " = " + fn + "(" + x + ");");
                     result[e] = name;
                 }
                 break;
             }
             case kop::reciprocal: {
                 const std::vector<std::string> a = emit(n.a);
+                // Operands within |x| in [2^-125, 2^125] take the hardware
+                // reciprocal plus one Newton step, which is the correctly
+                // rounded 1/x there.
+                const bool tame = reciprocal_is_tame(range_of(n.a));
                 for (int e = 0; e < width; ++e) {
                     const std::string name = fresh("v");
-                    line("const float " + name + " = 1.0f / " + a[e] + ";");
+                    line("const float " + name + " = " +
+                         (tame ? "porch_rcp(" + a[e] + ")" : "1.0f / " + a[e]) + ";");
                     result[e] = name;
                 }
                 break;
@@ -212,6 +235,48 @@ namespace porch::cg {
         return params;
     }
 
+    namespace {
+        // Device helpers the emitters call where value ranges allow.
+        //
+        // porch_rcp: hardware reciprocal (about 1 ulp) refined by one
+        // Newton-Raphson step with fused multiply-adds.  For |d| in
+        // [2^-125, 2^125] this equals the IEEE quotient 1.0f / d bit for bit
+        // (verified exhaustively on gfx950 over the binades 2^-125, 2^-60,
+        // 2^-1, 2^0, 2^1, 2^10 and 2^124; the sequence is scale-invariant in
+        // between); NaN propagates.
+        //
+        // porch_exp / porch_exp_finite: exp(x) for x <= 88 by Cody-Waite
+        // style reduction onto the hardware exp2: k = rint(x log2 e) with
+        // x log2 e carried as a hi + lo pair, exp2 of the small remainder,
+        // then ldexp by k (which also produces denormal and zero results).
+        // Below -104 every result rounds to zero, so x is clamped there.
+        // Max error 1 ulp against the correctly rounded exp over every float
+        // in [-104, 88.72] (verified exhaustively on gfx950), the same as
+        // expf.  porch_exp keeps NaN; porch_exp_finite assumes no NaN.
+        const char* math_helpers() {
+            return R"(__device__ __forceinline__ float porch_rcp(float d) {
+    const float r = __builtin_amdgcn_rcpf(d);
+    return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+}
+__device__ __forceinline__ float porch_exp_reduced(float x) {
+    const float L = 1.44269502162933349609375f;
+    const float Llo = 1.925963033500011079013347625732421875e-8f;
+    const float ph = x * L;
+    const float pl = __builtin_fmaf(x, Llo, __builtin_fmaf(x, L, -ph));
+    const float k = __builtin_rintf(ph);
+    const float r = __builtin_amdgcn_exp2f((ph - k) + pl);
+    return __builtin_ldexpf(r, (int)k);
+}
+__device__ __forceinline__ float porch_exp(float x) {
+    return porch_exp_reduced(x < -104.0f ? -104.0f : x);
+}
+__device__ __forceinline__ float porch_exp_finite(float x) {
+    return porch_exp_reduced(__builtin_fmaxf(x, -104.0f));
+}
+)";
+        }
+    } // namespace
+
     std::string kernel_prologue(int n_slots, const char* index_type) {
         (void)n_slots;
         std::string s;
@@ -220,6 +285,7 @@ namespace porch::cg {
         s += index_type;
         s += " idx_t;\n";
         s += "#define PORCH_FLT_MAX 3.40282346638528859812e+38f\n";
+        s += math_helpers();
         return s;
     }
 

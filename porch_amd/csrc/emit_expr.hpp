@@ -8,6 +8,7 @@
 // ternary NaN behaviour (reference src/tensor.cpp:677-682).
 
 #include "lower.hpp"
+#include "range.hpp"
 
 #include <functional>
 #include <map>
@@ -35,6 +36,10 @@ namespace porch::cg {
         // Optional: the branch select `id` takes wherever this code runs
         // (0: first operand, 1: second), or -1 to branch at run time.
         std::function<int(int id)> forced_branch;
+        // Optional inputs of the value-range analysis (range.hpp) that picks
+        // the fast exact reciprocal and the overflow-free exp.
+        std::function<vrange(int row)> row_value_range;
+        std::function<vrange(int id, const vrange& computed)> refine_range;
 
         emitter(const kexpr& expr, std::string& target, int lanes);
 
@@ -42,8 +47,12 @@ namespace porch::cg {
         std::string fresh(const char* prefix);
         void line(const std::string& text);
 
+        // Range of node `id` (computed once, on first use).
+        const vrange& range_of(int id);
+
       private:
         std::vector<std::map<int, std::vector<std::string>>> frames_;
+        std::vector<vrange> ranges_;
         int counter_ = 0;
         const std::vector<std::string>* find(int id) const;
     };

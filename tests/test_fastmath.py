@@ -1,0 +1,152 @@
+"""Range-driven instruction choices for reciprocal and exp.
+
+Where the value-range analysis proves a reciprocal's operand lies in
+[2^-125, 2^125] (in magnitude), kernels use the hardware reciprocal plus one
+Newton step (porch_rcp), which must equal IEEE 1.0f / x bit for bit; where it
+proves an exp argument is <= 88, kernels use porch_exp / porch_exp_finite,
+which must stay within 2 ulp of the host's exp.  The CPU tests pin where the
+analysis allows each form (and where it must not); the GPU tests check the
+results against the oracle, exhaustively over whole binades for the
+reciprocal.
+"""
+
+import re
+
+import numpy as np
+import pytest
+
+import porch_amd as porch
+from oracle import host
+from tests.helpers import placeholder
+
+
+def source_of(expr):
+    return porch.kernel_source(expr, 0)
+
+
+def body(expr):
+    s = source_of(expr)
+    return s[s.index('extern "C"'):]
+
+
+# -- where the fast forms apply (no GPU) ---------------------------------------
+
+def test_logistic_of_relu_takes_both_fast_forms():
+    x = placeholder([64, 128])
+    b = body(porch.logistic(porch.relu(x)))
+    assert "porch_rcp(" in b and "porch_exp_finite(-" in b
+    assert "1.0f /" not in b and "expf(" not in b
+
+
+def test_unknown_operands_keep_ieee_division_and_expf():
+    x = placeholder([64, 128])
+    b = body(porch.reciprocal(x) + porch.exp(x))
+    assert "1.0f / " in b and "expf(" in b and "porch_rcp(" not in b and "porch_exp" not in b
+
+
+@pytest.mark.parametrize("make,fast", [
+    (lambda x: porch.reciprocal(porch.minimum(porch.maximum(x, 1.0), 2.0)), True),
+    (lambda x: porch.reciprocal(porch.maximum(x, 0.0)), False),          # 0 is in range
+    (lambda x: porch.reciprocal(porch.maximum(x, 1e-38)), False),        # below 2^-125
+    (lambda x: porch.reciprocal(porch.maximum(x, 2.0 ** -125)), False),  # unbounded above
+    (lambda x: porch.reciprocal(porch.minimum(porch.maximum(x, 2.0 ** -125), 2.0 ** 125)), True),
+    (lambda x: porch.reciprocal(porch.minimum(porch.maximum(x, -3.0), -0.5)), True),
+    (lambda x: porch.reciprocal(x * x + 1.0), False),  # >= 1, but intervals cannot see a square
+])
+def test_reciprocal_fast_form_only_when_tame(make, fast):
+    b = body(make(placeholder([256])))
+    assert ("porch_rcp(" in b) == fast
+    assert ("1.0f / " in b) == (not fast)
+
+
+@pytest.mark.parametrize("make,fn", [
+    (lambda x: porch.exp(porch.minimum(x, 88.0)), "porch_exp_finite("),  # NaN becomes 88
+    (lambda x: porch.exp(porch.minimum(88.0, x)), "porch_exp("),        # NaN stays NaN
+    (lambda x: porch.exp(porch.minimum(x, 89.0)), "expf("),              # may overflow
+    (lambda x: porch.exp(x), "expf("),
+    (lambda x: porch.exp(0.0 - porch.relu(x)), "porch_exp_finite(-"),
+])
+def test_exp_form_follows_the_argument_range(make, fn):
+    b = body(make(placeholder([256])))
+    called = set(re.findall(r"\b(porch_exp_finite|porch_exp|expf)\(", b))
+    assert called == {fn.split("(")[0]}, called
+    assert fn in b
+
+
+def test_negation_folds_into_exp_only_for_positive_zero():
+    x = placeholder([256])
+    assert "expf(-" in body(porch.exp(0.0 - x))
+    assert "expf(-" not in body(porch.exp(-0.0 - x))
+
+
+# -- results (GPU) ---------------------------------------------------------------
+
+def binade(e):
+    m = np.arange(1 << 23, dtype=np.uint32)
+    return ((np.uint32(e + 127) << np.uint32(23)) | m).view(np.float32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("e,sign", [(0, 1), (-125, 1), (124, 1), (7, 1), (0, -1), (-125, -1), (124, -1)])
+def test_fast_reciprocal_is_ieee_over_a_whole_binade(gpu, e, sign):
+    x = binade(e) * np.float32(sign)
+    lo, hi = sorted([float(sign * 2.0 ** e), float(sign * 2.0 ** (e + 1))])
+    t = gpu.tensor([x.size], x)
+    expr = gpu.reciprocal(gpu.minimum(gpu.maximum(t, lo), hi))
+    assert "porch_rcp(" in gpu.kernel_source(expr, 0)
+    out = gpu.materialize(expr).cpu()
+    ref = (np.float32(1.0) / x).astype(np.float32)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_fast_reciprocal_keeps_nan_and_signs(gpu):
+    x = np.array([1.0, -1.0, 1.5, -1.75, np.nan, 3.0, -2.5], dtype=np.float32)
+    t = gpu.tensor([x.size], x)
+    # constants on the left: a NaN x passes through maximum and minimum
+    expr = gpu.reciprocal(gpu.minimum(4.0, gpu.maximum(1.0, t)))
+    assert "porch_rcp(" in gpu.kernel_source(expr, 0)
+    out = gpu.materialize(expr).cpu()
+    ref = host.evaluate(expr)
+    # NaN where the oracle has NaN (IEEE leaves a NaN result's sign and
+    # payload open), every other value bit for bit.
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    keep = ~np.isnan(ref)
+    assert np.array_equal(out[keep].view(np.uint32), ref[keep].view(np.uint32))
+
+
+def ulp_distance(a, b):
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, np.int64(-(1 << 31)) - ia, ia)
+    ib = np.where(ib < 0, np.int64(-(1 << 31)) - ib, ib)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.gpu
+def test_fast_exp_within_2_ulp(gpu):
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 1 << 32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x) & (np.abs(x) <= 110.0)]
+    x = np.concatenate([x, rng.uniform(-110, 88, size=1 << 20).astype(np.float32),
+                        np.array([-np.inf, -1e30, -104.0, -103.9, -87.4, -87.3, -0.0, 0.0,
+                                  1e-30, 88.0, 87.99], dtype=np.float32)])
+    t = gpu.tensor([x.size], x)
+    for make, fn in [(lambda v: gpu.exp(gpu.minimum(v, 88.0)), "porch_exp_finite("),
+                     (lambda v: gpu.exp(gpu.minimum(88.0, v)), "porch_exp(")]:
+        expr = make(t)
+        assert fn in gpu.kernel_source(expr, 0)
+        out = gpu.materialize(expr).cpu()
+        ref = host.evaluate(expr)
+        assert ulp_distance(out, ref).max() <= 2
+
+
+@pytest.mark.gpu
+def test_fast_exp_propagates_nan(gpu):
+    x = np.array([np.nan, 0.0, -1.0, -np.inf, 88.0], dtype=np.float32)
+    t = gpu.tensor([x.size], x)
+    expr = gpu.exp(gpu.minimum(88.0, t))
+    out = gpu.materialize(expr).cpu()
+    assert np.isnan(out[0]) and out[1] == 1.0 and out[3] == 0.0
+    assert ulp_distance(out[1:], host.evaluate(expr)[1:]).max() <= 2

@@ -1,5 +1,7 @@
 """The planner's kernel choices and offline hiprtc compilation (no GPU)."""
 
+import re
+
 import pytest
 
 import porch_amd as porch
@@ -30,7 +32,7 @@ def test_softmax_reads_the_row_once():
     source = porch.kernel_source(porch.softmax(x, 1))
     # one 128-bit load per column chunk, in the first pass only
     assert source.count("reinterpret_cast<const float4*>(a0") == 1
-    assert source.count("expf(") == 4  # one pass, four lanes
+    assert len(re.findall(r"\bexpf\(", source)) == 4  # one pass, four lanes
 
 
 def test_shared_reductions_are_materialised_once():
