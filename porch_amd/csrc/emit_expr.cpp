@@ -15,6 +15,34 @@ namespace porch::cg {
         return ranges_[static_cast<size_t>(id)];
     }
 
+    void emitter::declare_roots(std::vector<int> ids) {
+        roots_ = std::move(ids);
+        roots_declared_ = true;
+    }
+
+    bool emitter::denormals_absorbed(int id) {
+        if (!roots_declared_) return false;
+        for (const int r : roots_) {
+            if (r == id) return false;
+        }
+        const float tiny = std::ldexp(1.0F, -100);
+        auto big_constant = [&](int c) {
+            const knode& n = k.at(c);
+            return n.op == kop::constant && std::fabs(n.value) >= tiny;
+        };
+        int users = 0;
+        for (size_t u = 0; u < k.nodes.size(); ++u) {
+            const knode& n = k.nodes[u];
+            if (n.a != id && n.b != id) continue;
+            ++users;
+            const bool absorbs = (n.op == kop::add || n.op == kop::subtract) &&
+                                 ((n.a == id && n.b != id && big_constant(n.b)) ||
+                                  (n.b == id && n.a != id && big_constant(n.a)));
+            if (!absorbs) return false;
+        }
+        return users > 0;
+    }
+
     std::string emitter::fresh(const char* prefix) {
         return std::string{prefix} + std::to_string(counter_++);
     }
@@ -97,7 +125,12 @@ namespace porch::cg {
                 // overflow handling (and the NaN test when NaN is impossible).
                 const vrange& r = range_of(n.a);
                 const char* fn = "expf";
-                if (!std::isnan(r.hi) && r.hi <= 88.0F) fn = r.nan ? "porch_exp" : "porch_exp_finite";
+                if (!std::isnan(r.hi) && r.hi <= 88.0F) {
+                    // Where denormal results vanish in the consumer, the
+                    // shorter sequence that flushes them is exact enough.
+                    if (denormals_absorbed(id)) fn = r.nan ? "porch_exp_flush" : "porch_exp_flush_finite";
+                    else fn = r.nan ? "porch_exp" : "porch_exp_finite";
+                }
                 for (int e = 0; e < width; ++e) {
                     const std::string name = fresh("v");
                     const std::string x = negate ? "-" + a[e] : a[e];
@@ -253,6 +286,13 @@ namespace porch::cg {
         // Max error 1 ulp against the correctly rounded exp over every float
         // in [-104, 88.72] (verified exhaustively on gfx950), the same as
         // expf.  porch_exp keeps NaN; porch_exp_finite assumes no NaN.
+        //
+        // porch_exp_flush / porch_exp_flush_finite: exp(x) for x <= 88 as
+        // exp2(p) (1 + u) with p = RN(x log2 e) and u = x - p ln 2 (ln 2 as a
+        // hi + lo pair), one fused multiply-add.  Max error 1 ulp for normal
+        // results over every float in [-104, 88.72] (verified exhaustively on
+        // gfx950), but denormal results come out as zero: only used where
+        // every consumer adds a constant that absorbs denormals.
         const char* math_helpers() {
             return R"(__device__ __forceinline__ float porch_rcp(float d) {
     const float r = __builtin_amdgcn_rcpf(d);
@@ -272,6 +312,20 @@ __device__ __forceinline__ float porch_exp(float x) {
 }
 __device__ __forceinline__ float porch_exp_finite(float x) {
     return porch_exp_reduced(__builtin_fmaxf(x, -104.0f));
+}
+__device__ __forceinline__ float porch_exp_flush_reduced(float x) {
+    const float L = 1.44269502162933349609375f;
+    const float ph = x * L;
+    float u = __builtin_fmaf(-ph, 0.693145751953125f, x);
+    u = __builtin_fmaf(-ph, 1.428606765330187045e-06f, u);
+    const float r = __builtin_amdgcn_exp2f(ph);
+    return __builtin_fmaf(r, u, r);
+}
+__device__ __forceinline__ float porch_exp_flush(float x) {
+    return porch_exp_flush_reduced(x < -104.0f ? -104.0f : x);
+}
+__device__ __forceinline__ float porch_exp_flush_finite(float x) {
+    return porch_exp_flush_reduced(__builtin_fmaxf(x, -104.0f));
 }
 )";
         }

@@ -50,9 +50,20 @@ namespace porch::cg {
         // Range of node `id` (computed once, on first use).
         const vrange& range_of(int id);
 
+        // The nodes whose values leave the expression (stored, reduced,
+        // staged).  Until they are declared, no node counts as consumed only
+        // inside the expression.
+        void declare_roots(std::vector<int> ids);
+        // Is every use of `id` an addition or subtraction of a constant c
+        // with |c| >= 2^-100?  Then c + v rounds to c for any denormal v, so a
+        // denormal value of `id` may be flushed to zero unseen.
+        bool denormals_absorbed(int id);
+
       private:
         std::vector<std::map<int, std::vector<std::string>>> frames_;
         std::vector<vrange> ranges_;
+        std::vector<int> roots_;
+        bool roots_declared_ = false;
         int counter_ = 0;
         const std::vector<std::string>* find(int id) const;
     };

@@ -67,6 +67,7 @@ namespace porch::cg {
             std::string body;
             emitter em(*r.expr, body, 1);
             em.indent = "        ";
+            em.declare_roots({r.epilogue});
             epilogue_emitter(em, r, names, "acc");
             const std::string v = em.emit(r.epilogue)[0];
             s += body;
@@ -272,6 +273,7 @@ namespace porch::cg {
             std::string body;
             emitter em(*r.expr, body, 1);
             em.indent = "            ";
+            em.declare_roots({r.epilogue});
             const std::vector<std::string> names{"q0", "q1"};
             epilogue_emitter(em, r, names, "acc_v");
             const std::string v = em.emit(r.epilogue)[0];

@@ -63,6 +63,7 @@ namespace porch::cg {
             std::string body;
             emitter em(*r.expr, body, 1);
             em.indent = "        ";
+            em.declare_roots({r.root});
             const std::vector<std::string> names = coordinate_names(rank);
             em.load = [&](int id) {
                 const knode& n = r.expr->at(id);
@@ -148,6 +149,7 @@ namespace porch::cg {
             std::string body;
             emitter em(*r.expr, body, 4);
             em.indent = "        ";
+            em.declare_roots({r.root});
             em.condition = [&](const kcond& c) {
                 return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
             };
@@ -217,6 +219,7 @@ namespace porch::cg {
                 std::string tail_body;
                 emitter te(*r.expr, tail_body, 1);
                 te.indent = "        ";
+                te.declare_roots({r.root});
                 te.condition = em.condition;
                 te.row_value = em.row_value;
                 te.load = [&](int id) {
@@ -422,6 +425,8 @@ namespace porch::cg {
             const int64_t others = ir::numel(other_shape);
             const size_t n_stage = t.staged.size();
             const std::vector<char> in_stage = staged_mask(k, t);
+            std::vector<int> tiled_roots(t.staged.begin(), t.staged.end());
+            tiled_roots.push_back(r.root);
 
             // Phase 1 width: elements per lane along p.
             int64_t V = 1;
@@ -580,6 +585,7 @@ namespace porch::cg {
                 std::string body;
                 emitter em(k, body, static_cast<int>(V));
                 em.indent = indent;
+                em.declare_roots(tiled_roots);
                 em.condition = cond_fn;
                 em.row_value = [](int) -> std::string {
                     throw std::logic_error("row value in a pointwise kernel");
@@ -680,6 +686,7 @@ namespace porch::cg {
                 std::string body;
                 emitter em(k, body, static_cast<int>(W));
                 em.indent = indent;
+                em.declare_roots(tiled_roots);
                 em.condition = cond_fn;
                 em.row_value = [](int) -> std::string {
                     throw std::logic_error("row value in a pointwise kernel");

@@ -61,6 +61,7 @@ namespace porch::cg {
         std::string body;
         emitter em(k, body, 1);
         em.indent = "            ";
+        em.declare_roots({r.producer});
         em.load = [&](int id) {
             const knode& n = k.at(id);
             return std::vector<std::string>{

@@ -310,9 +310,14 @@ namespace porch::cg {
             return code;
         };
 
+        std::vector<int> row_roots;
+        for (const row_reduction& red : r.reductions) row_roots.push_back(red.producer);
+        if (r.output >= 0) row_roots.push_back(r.output);
+
         auto make_emitter = [&](std::string& body, size_t pass) {
             auto em = std::make_unique<emitter>(k, body, width);
             em->indent = ragged ? "                " : "            ";
+            em->declare_roots(row_roots);
             emitter* self = em.get();
             em->load = [&, self](int id) {
                 for (const int h : hoisted) {

@@ -34,8 +34,28 @@ def body(expr):
 def test_logistic_of_relu_takes_both_fast_forms():
     x = placeholder([64, 128])
     b = body(porch.logistic(porch.relu(x)))
-    assert "porch_rcp(" in b and "porch_exp_finite(-" in b
-    assert "1.0f /" not in b and "expf(" not in b
+    # exp's only consumer is 1 + e, which absorbs denormals: the flushing form
+    assert "porch_rcp(" in b and "porch_exp_flush_finite(-" in b
+    assert "1.0f /" not in b and not re.search(r"\bexpf\(", b)
+
+
+EXP_FORMS = r"\b(porch_exp_flush_finite|porch_exp_flush|porch_exp_finite|porch_exp|expf)\("
+
+
+@pytest.mark.parametrize("make,fn", [
+    (lambda e: e, "porch_exp_finite"),                    # stored: denormals visible
+    (lambda e: 1.0 + e, "porch_exp_flush_finite"),
+    (lambda e: 2.0 - e, "porch_exp_flush_finite"),
+    (lambda e: e - 0.5, "porch_exp_flush_finite"),
+    (lambda e: 1e-38 + e, "porch_exp_finite"),            # constant below 2^-100
+    (lambda e: (1.0 + e) * e, "porch_exp_finite"),        # a multiply sees e itself
+    (lambda e: porch.sum(1.0 + e, 1), "porch_exp_flush_finite"),
+    (lambda e: porch.sum(e, 1), "porch_exp_finite"),      # reduced directly
+])
+def test_flushing_exp_only_where_consumers_absorb_denormals(make, fn):
+    x = placeholder([64, 256])
+    b = body(make(porch.exp(porch.minimum(x, 88.0))))
+    assert set(re.findall(EXP_FORMS, b)) == {fn}
 
 
 def test_unknown_operands_keep_ieee_division_and_expf():
@@ -68,7 +88,7 @@ def test_reciprocal_fast_form_only_when_tame(make, fast):
 ])
 def test_exp_form_follows_the_argument_range(make, fn):
     b = body(make(placeholder([256])))
-    called = set(re.findall(r"\b(porch_exp_finite|porch_exp|expf)\(", b))
+    called = set(re.findall(EXP_FORMS, b))
     assert called == {fn.split("(")[0]}, called
     assert fn in b
 
@@ -140,6 +160,25 @@ def test_fast_exp_within_2_ulp(gpu):
         out = gpu.materialize(expr).cpu()
         ref = host.evaluate(expr)
         assert ulp_distance(out, ref).max() <= 2
+
+
+@pytest.mark.gpu
+def test_flushing_exp_consumers_within_2_ulp(gpu):
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.uniform(-120, 90, size=1 << 20),
+                        rng.uniform(-105, -80, size=1 << 18),
+                        [-np.inf, np.inf, np.nan, -104.0, -87.5, 0.0]]).astype(np.float32)
+    t = gpu.tensor([x.size], x)
+    for make in (lambda v: gpu.logistic(gpu.relu(v)),
+                 lambda v: 2.0 - gpu.exp(gpu.minimum(v, 0.0)),  # e <= 1: no cancellation
+                 lambda v: gpu.exp(gpu.minimum(88.0, v)) + 0.25):
+        expr = make(t)
+        assert "porch_exp_flush" in gpu.kernel_source(expr, 0)
+        out = gpu.materialize(expr).cpu()
+        ref = host.evaluate(expr)
+        assert np.array_equal(np.isnan(out), np.isnan(ref))
+        keep = ~np.isnan(ref)
+        assert ulp_distance(out[keep], ref[keep]).max() <= 2
 
 
 @pytest.mark.gpu
