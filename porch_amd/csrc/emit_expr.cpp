@@ -339,6 +339,7 @@ __device__ __forceinline__ float porch_exp_flush_finite(float x) {
         s += index_type;
         s += " idx_t;\n";
         s += "#define PORCH_FLT_MAX 3.40282346638528859812e+38f\n";
+        s += "typedef float porch_v4f __attribute__((ext_vector_type(4)));\n";
         s += math_helpers();
         return s;
     }

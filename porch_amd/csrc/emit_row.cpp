@@ -73,7 +73,11 @@ namespace porch::cg {
         const int64_t length = r.shape[col];
         std::vector<int64_t> row_shape(r.shape.begin(), r.shape.end() - 1);
         const int64_t rows = ir::numel(row_shape);
-        const bool block_mode = length > 4096;
+        // Rows of 2048 or more are spread over a whole workgroup (at least
+        // 8 values per lane): a quarter of the registers per lane of the
+        // wave-per-row form, so four times the resident rows to overlap
+        // loads, arithmetic and stores.
+        const bool block_mode = length >= 2048;
         const int lanes = block_mode ? 256 : 64;
 
         // Pass roots: each reduction's producer, then the output.
@@ -176,7 +180,10 @@ namespace porch::cg {
         const int64_t rows_per_group = block_mode ? 1 : 4;
         int64_t rows_per_wave = 1;
         if (!hoisted.empty()) {
-            const int64_t target = static_cast<int64_t>(r.compute_units) * 8 * rows_per_group;
+            // Enough workgroups to fill the machine several times over; each
+            // loads the hoisted values once.
+            const int64_t target =
+                static_cast<int64_t>(r.compute_units) * (block_mode ? 16 : 8) * rows_per_group;
             rows_per_wave = std::max<int64_t>(1, rows / std::max<int64_t>(target, 1));
         }
         const int64_t groups =
@@ -200,9 +207,16 @@ namespace porch::cg {
              kernel_params(r.n_slots) + ") {\n";
         s += "    const int lane = threadIdx.x & 63;\n";
         s += "    const int wave = threadIdx.x >> 6;\n";
+        const size_t n_reductions = r.reductions.size() + (r.reduce_output ? 1 : 0);
         if (block_mode) {
-            s += "    __shared__ float red[4];\n";
+            // One slot per reduction per wave, in two sets alternating by row
+            // iteration: a slot is rewritten two rows later, and every row
+            // passes at least one barrier in between, so one barrier per
+            // reduction suffices.
+            s += "    __shared__ float red[2][" + std::to_string(std::max<size_t>(n_reductions, 1)) +
+                 "][4];\n";
             s += "    const int tl = threadIdx.x;\n";
+            s += "    int it = 0;\n";
         }
         else {
             s += "    const int tl = lane;\n";
@@ -224,6 +238,20 @@ namespace porch::cg {
             if (ragged) code += indent + "    }\n";
             code += indent + "}\n";
         };
+
+        // A leaf whose every element is read exactly once by this kernel
+        // (no broadcast dimension) streams past the caches: non-temporal
+        // loads keep it from evicting data that is reused.
+        auto streaming = [&](const knode& n) {
+            if (!n.index.is_affine) return false;
+            for (size_t d = 0; d < rank; ++d) {
+                if (r.shape[d] > 1 && n.index.w[d] == 0) return false;
+            }
+            return true;
+        };
+        // Large outputs are written with non-temporal stores: they would
+        // only evict the kernel's own streaming inputs from L2 and MALL.
+        const bool stream_output = !r.reduce_output && ir::numel(r.shape) * 4 >= (int64_t{64} << 20);
 
         auto load_text = [&](emitter& em, int id) {
             const knode& n = k.at(id);
@@ -247,8 +275,14 @@ namespace porch::cg {
             }
             if (aligned) {
                 const std::string v = em.fresh("w");
-                em.line("const float4 " + v + " = *reinterpret_cast<const float4*>(" + base +
-                        " + " + idx + ");");
+                if (streaming(n)) {
+                    em.line("const porch_v4f " + v + " = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" +
+                            base + " + " + idx + "));");
+                }
+                else {
+                    em.line("const float4 " + v + " = *reinterpret_cast<const float4*>(" + base +
+                            " + " + idx + ");");
+                }
                 return std::vector<std::string>{v + ".x", v + ".y", v + ".z", v + ".w"};
             }
             const std::string p = em.fresh("p");
@@ -292,6 +326,7 @@ namespace porch::cg {
             s += decompose("row", row_shape, needed, T, "        ");
         }
 
+        size_t next_slot = 0;
         auto reduce_lanes = [&](const std::string& acc, bool is_max) {
             std::string code;
             const std::string op = is_max ? "porch_max(" + acc + ", __shfl_xor(" + acc + ", m, 64))"
@@ -299,13 +334,15 @@ namespace porch::cg {
             code += "        #pragma unroll\n";
             code += "        for (int m = 32; m >= 1; m >>= 1) " + acc + " = " + op + ";\n";
             if (block_mode) {
-                code += "        if (lane == 0) red[wave] = " + acc + ";\n";
+                const std::string slot = "red[it & 1][" + std::to_string(next_slot++) + "]";
+                code += "        if (lane == 0) " + slot + "[wave] = " + acc + ";\n";
                 code += "        __syncthreads();\n";
                 if (is_max)
-                    code += "        " + acc + " = porch_max(porch_max(red[0], red[1]), porch_max(red[2], red[3]));\n";
+                    code += "        " + acc + " = porch_max(porch_max(" + slot + "[0], " + slot +
+                            "[1]), porch_max(" + slot + "[2], " + slot + "[3]));\n";
                 else
-                    code += "        " + acc + " = (red[0] + red[1]) + (red[2] + red[3]);\n";
-                code += "        __syncthreads();\n";
+                    code += "        " + acc + " = (" + slot + "[0] + " + slot + "[1]) + (" + slot +
+                            "[2] + " + slot + "[3]);\n";
             }
             return code;
         };
@@ -396,7 +433,11 @@ namespace porch::cg {
             auto em = make_emitter(body, out_pass);
             const std::vector<std::string> v = em->emit(r.output);
             const std::string base = "row * " + std::to_string(length) + " + " + qc;
-            if (width == 4) {
+            if (width == 4 && stream_output) {
+                em->line("__builtin_nontemporal_store((porch_v4f){" + v[0] + ", " + v[1] + ", " + v[2] +
+                         ", " + v[3] + "}, reinterpret_cast<porch_v4f*>(out + " + base + "));");
+            }
+            else if (width == 4) {
                 em->line("*reinterpret_cast<float4*>(out + " + base + ") = make_float4(" + v[0] +
                          ", " + v[1] + ", " + v[2] + ", " + v[3] + ");");
             }
@@ -407,6 +448,7 @@ namespace porch::cg {
             chunk_close(code, "        ");
             s += code;
         }
+        if (block_mode) s += "        ++it;\n";
         s += "    }\n}\n";
         return kc;
     }

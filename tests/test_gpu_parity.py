@@ -69,7 +69,8 @@ def test_view_chain_bit_exact(gpu, n):
 
 @pytest.mark.parametrize("size", [{"rows": 3, "cols": 7}, {"rows": 17, "cols": 256},
                                   {"rows": 64, "cols": 4100}, {"rows": 8, "cols": 12288},
-                                  {"rows": 8192, "cols": 4096}])
+                                  {"rows": 300, "cols": 2048}, {"rows": 50, "cols": 3000},
+                                  {"rows": 7, "cols": 2050}, {"rows": 8192, "cols": 4096}])
 def test_softmax_within_1e6(gpu, size):
     out, ref, _ = gpu_and_oracle(gpu, "softmax", size)
     assert_close(out, ref, 1e-6)
@@ -79,7 +80,8 @@ def test_softmax_within_1e6(gpu, size):
 # -- config 4: broadcast + logistic + row sum, 1e-5 relative -----------------
 
 @pytest.mark.parametrize("size", [{"rows": 5, "cols": 9}, {"rows": 33, "cols": 2048},
-                                  {"rows": 16384, "cols": 2048}, {"rows": 4, "cols": 10000}])
+                                  {"rows": 16384, "cols": 2048}, {"rows": 4, "cols": 10000},
+                                  {"rows": 100, "cols": 3001}, {"rows": 4097, "cols": 2044}])
 def test_logistic_rowsum_within_1e5(gpu, size):
     out, ref, _ = gpu_and_oracle(gpu, "logistic_rowsum", size)
     assert_close(out, ref, 1e-5)

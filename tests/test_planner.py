@@ -30,8 +30,10 @@ def test_each_benchmark_graph_is_one_fused_kernel(name):
 def test_softmax_reads_the_row_once():
     x = placeholder([8192, 4096])
     source = porch.kernel_source(porch.softmax(x, 1))
-    # one 128-bit load per column chunk, in the first pass only
-    assert source.count("reinterpret_cast<const float4*>(a0") == 1
+    # one 128-bit (non-temporal: read once) load per column chunk, in the
+    # first pass only, and non-temporal 128-bit stores of the 128 MiB result
+    assert source.count("__builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0") == 1
+    assert source.count("__builtin_nontemporal_store(") == 1
     assert len(re.findall(r"\bexpf\(", source)) == 4  # one pass, four lanes
 
 
