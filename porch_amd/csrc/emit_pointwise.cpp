@@ -141,14 +141,15 @@ namespace porch::cg {
                  kernel_params(r.n_slots) + ") {\n";
             s += "    for (idx_t g = (idx_t)blockIdx.x * 256 + threadIdx.x; g < " +
                  std::to_string(groups) + "; g += (idx_t)gridDim.x * 256) {\n";
-            s += "        const idx_t f = g * 4;\n";
+            const std::string ind = "        ";
+            s += ind + "const idx_t f = g * 4;\n";
             const std::vector<bool> used = used_coordinates(*r.expr, r.root, rank);
             if (mode == flat_mode::row_vector)
-                s += decompose("f", r.shape, used, T, "        ");
+                s += decompose("f", r.shape, used, T, ind);
 
             std::string body;
             emitter em(*r.expr, body, 4);
-            em.indent = "        ";
+            em.indent = ind;
             em.declare_roots({r.root});
             em.condition = [&](const kcond& c) {
                 return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
@@ -206,7 +207,7 @@ namespace porch::cg {
             };
             const std::vector<std::string> v = em.emit(r.root);
             s += body;
-            s += "        *reinterpret_cast<float4*>(out + f) = make_float4(" + v[0] +
+            s += ind + "*reinterpret_cast<float4*>(out + f) = make_float4(" + v[0] +
                  ", " + v[1] + ", " + v[2] + ", " + v[3] + ");\n";
             s += "    }\n";
             if (tail != 0) {
@@ -475,6 +476,17 @@ namespace porch::cg {
                     hoisted.push_back(static_cast<int>(id));
             }
 
+            // A leaf whose every element is read once by this kernel (no
+            // broadcast dimension) streams past the caches: non-temporal
+            // loads keep it from evicting data that is reused.
+            auto streaming = [&](const knode& n) {
+                if (!n.index.is_affine) return false;
+                for (size_t d = 0; d < rank; ++d) {
+                    if (r.shape[d] > 1 && n.index.w[d] == 0) return false;
+                }
+                return true;
+            };
+
             kernel_code kc;
             kc.kind = "pointwise.tiled";
             kc.name = "porch_tiled";
@@ -612,8 +624,13 @@ namespace porch::cg {
                     if (vl.ok) {
                         const std::string w = em.fresh("w");
                         const std::string type = vl.width == 4 ? "float4" : "float2";
-                        em.line("const " + type + " " + w + " = *reinterpret_cast<const " + type +
-                                "*>(" + base + " + " + idx + " - " + std::to_string(vl.m) + ");");
+                        const std::string addr = base + " + " + idx + " - " + std::to_string(vl.m);
+                        if (vl.width == 4 && streaming(n))
+                            em.line("const porch_v4f " + w + " = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" +
+                                    addr + "));");
+                        else
+                            em.line("const " + type + " " + w + " = *reinterpret_cast<const " + type +
+                                    "*>(" + addr + ");");
                         for (int64_t e = 0; e < V; ++e) lanes[e] = w + lane_name(vl.m + vl.step * e);
                         return lanes;
                     }
@@ -718,8 +735,12 @@ namespace porch::cg {
                     const vector_load vl = plan_vector_load(n, q, W, r.slot_elems);
                     if (vl.ok && vl.width == 4 && vl.m == 0 && vl.step == 1) {
                         const std::string w = em.fresh("w");
-                        em.line("const float4 " + w + " = *reinterpret_cast<const float4*>(" +
-                                base + " + " + idx + ");");
+                        if (streaming(n))
+                            em.line("const porch_v4f " + w + " = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" +
+                                    base + " + " + idx + "));");
+                        else
+                            em.line("const float4 " + w + " = *reinterpret_cast<const float4*>(" +
+                                    base + " + " + idx + ");");
                         return std::vector<std::string>{w + ".x", w + ".y", w + ".z", w + ".w"};
                     }
                     const std::string ptr = em.fresh("p");
