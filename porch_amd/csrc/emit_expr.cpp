@@ -21,14 +21,17 @@ namespace porch::cg {
     }
 
     bool emitter::denormals_absorbed(int id) {
+        return only_added_to_constants(id, std::ldexp(1.0F, -100));
+    }
+
+    bool emitter::only_added_to_constants(int id, float least) {
         if (!roots_declared_) return false;
         for (const int r : roots_) {
             if (r == id) return false;
         }
-        const float tiny = std::ldexp(1.0F, -100);
         auto big_constant = [&](int c) {
             const knode& n = k.at(c);
-            return n.op == kop::constant && std::fabs(n.value) >= tiny;
+            return n.op == kop::constant && std::fabs(n.value) >= least;
         };
         int users = 0;
         for (size_t u = 0; u < k.nodes.size(); ++u) {
@@ -125,7 +128,14 @@ namespace porch::cg {
                 // overflow handling (and the NaN test when NaN is impossible).
                 const vrange& r = range_of(n.a);
                 const char* fn = "expf";
-                if (!std::isnan(r.hi) && r.hi <= 88.0F) {
+                if (relaxed && relaxed(id) && !std::isnan(r.hi) && r.hi <= 0.0F &&
+                    only_added_to_constants(id, 1.0F)) {
+                    // exp2(x log2 e): relative error <= |x| 2^-24 + 1 ulp, so
+                    // for x <= 0 an absolute error below 2^-22.4, under one
+                    // ulp of every constant (>= 1 in magnitude) it is added to.
+                    fn = "porch_exp_relaxed";
+                }
+                else if (!std::isnan(r.hi) && r.hi <= 88.0F) {
                     // Where denormal results vanish in the consumer, the
                     // shorter sequence that flushes them is exact enough.
                     if (denormals_absorbed(id)) fn = r.nan ? "porch_exp_flush" : "porch_exp_flush_finite";
@@ -145,10 +155,12 @@ namespace porch::cg {
                 // reciprocal plus one Newton step, which is the correctly
                 // rounded 1/x there.
                 const bool tame = reciprocal_is_tame(range_of(n.a));
+                // In a relaxed context the hardware reciprocal alone (1 ulp).
+                const char* fast = (relaxed && relaxed(id)) ? "__builtin_amdgcn_rcpf(" : "porch_rcp(";
                 for (int e = 0; e < width; ++e) {
                     const std::string name = fresh("v");
                     line("const float " + name + " = " +
-                         (tame ? "porch_rcp(" + a[e] + ")" : "1.0f / " + a[e]) + ";");
+                         (tame ? fast + a[e] + ")" : "1.0f / " + a[e]) + ";");
                     result[e] = name;
                 }
                 break;
@@ -293,6 +305,11 @@ namespace porch::cg {
         // results over every float in [-104, 88.72] (verified exhaustively on
         // gfx950), but denormal results come out as zero: only used where
         // every consumer adds a constant that absorbs denormals.
+        //
+        // porch_exp_relaxed: exp2(x log2 e) in two instructions, relative
+        // error <= |x| 2^-24 + 1 ulp, denormal results flushed; only for
+        // arguments <= 0 whose result is added to constants of magnitude
+        // >= 1 on its way into a sum that is the kernel's result.
         const char* math_helpers() {
             return R"(__device__ __forceinline__ float porch_rcp(float d) {
     const float r = __builtin_amdgcn_rcpf(d);
@@ -312,6 +329,9 @@ __device__ __forceinline__ float porch_exp(float x) {
 }
 __device__ __forceinline__ float porch_exp_finite(float x) {
     return porch_exp_reduced(__builtin_fmaxf(x, -104.0f));
+}
+__device__ __forceinline__ float porch_exp_relaxed(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269502162933349609375f);
 }
 __device__ __forceinline__ float porch_exp_flush_reduced(float x) {
     const float L = 1.44269502162933349609375f;

@@ -58,6 +58,15 @@ namespace porch::cg {
         // with |c| >= 2^-100?  Then c + v rounds to c for any denormal v, so a
         // denormal value of `id` may be flushed to zero unseen.
         bool denormals_absorbed(int id);
+        // Is every use of `id` an addition or subtraction of a constant of
+        // magnitude >= `least` (and is there at least one)?
+        bool only_added_to_constants(int id, float least);
+
+        // Optional: nodes whose values reach the kernel's result only through
+        // a sum that is the result itself (a row program's final sum).  The
+        // result is compared within a relative tolerance, so these nodes may
+        // use instruction sequences a few ulp from correctly rounded.
+        std::function<bool(int id)> relaxed;
 
       private:
         std::vector<std::map<int, std::vector<std::string>>> frames_;

@@ -351,10 +351,39 @@ namespace porch::cg {
         for (const row_reduction& red : r.reductions) row_roots.push_back(red.producer);
         if (r.output >= 0) row_roots.push_back(r.output);
 
+        // Nodes that reach the result only through its final sum: every
+        // user is itself such a node, and no other pass (reduction) reads
+        // them.  Operands precede users in the arena, so one backward sweep.
+        std::vector<char> relaxed(k.nodes.size(), 0);
+        if (r.reduce_output && !r.output_is_max && r.output >= 0) {
+            std::vector<char> other(k.nodes.size(), 0);
+            for (const row_reduction& red : r.reductions)
+                for (const int id : k.postorder(red.producer)) other[id] = 1;
+            std::vector<char> in_output(k.nodes.size(), 0);
+            for (const int id : k.postorder(r.output)) in_output[id] = 1;
+            for (size_t i = k.nodes.size(); i-- > 0;) {
+                if (!in_output[i] || other[i]) continue;
+                if (static_cast<int>(i) == r.output) {
+                    relaxed[i] = 1;
+                    continue;
+                }
+                bool all = true;
+                int users = 0;
+                for (size_t u = i + 1; u < k.nodes.size(); ++u) {
+                    const knode& n = k.nodes[u];
+                    if (n.a != static_cast<int>(i) && n.b != static_cast<int>(i)) continue;
+                    ++users;
+                    if (!relaxed[u]) all = false;
+                }
+                relaxed[i] = (all && users > 0) ? 1 : 0;
+            }
+        }
+
         auto make_emitter = [&](std::string& body, size_t pass) {
             auto em = std::make_unique<emitter>(k, body, width);
             em->indent = ragged ? "                " : "            ";
             em->declare_roots(row_roots);
+            em->relaxed = [&](int id) { return relaxed[static_cast<size_t>(id)] != 0; };
             emitter* self = em.get();
             em->load = [&, self](int id) {
                 for (const int h : hoisted) {

@@ -93,6 +93,30 @@ def test_exp_form_follows_the_argument_range(make, fn):
     assert fn in b
 
 
+RELAXED = ("porch_exp_relaxed(", "__builtin_amdgcn_rcpf(")
+
+
+def logistic_relu(x):
+    return porch.logistic(porch.relu(x))
+
+
+@pytest.mark.parametrize("make,relaxed", [
+    (lambda x: porch.sum(logistic_relu(x), 1), True),                 # result is the sum
+    (lambda x: porch.sum(logistic_relu(x), 1, True), True),
+    (lambda x: porch.max(logistic_relu(x), 1), False),                # a max selects values
+    (lambda x: logistic_relu(x), False),                              # stored elementwise
+    (lambda x: porch.softmax(x, 1), False),
+    # the logistic also feeds a max reduction: not only the final sum
+    (lambda x: porch.sum(logistic_relu(x) - porch.broadcast_to(
+        porch.max(logistic_relu(x), 1, True), [64, 2048]), 1), False),
+    (lambda x: porch.sum(porch.exp(x), 1), False),                    # exp argument unbounded
+])
+def test_relaxed_forms_only_inside_a_final_sum(make, relaxed):
+    b = body(make(placeholder([64, 2048])))
+    for form in RELAXED:
+        assert (form in b) == relaxed, form
+
+
 def test_negation_folds_into_exp_only_for_positive_zero():
     x = placeholder([256])
     assert "expf(-" in body(porch.exp(0.0 - x))
@@ -179,6 +203,23 @@ def test_flushing_exp_consumers_within_2_ulp(gpu):
         assert np.array_equal(np.isnan(out), np.isnan(ref))
         keep = ~np.isnan(ref)
         assert ulp_distance(out[keep], ref[keep]).max() <= 2
+
+
+@pytest.mark.gpu
+def test_relaxed_logistic_row_sums_within_1e5(gpu):
+    rng = np.random.default_rng(9)
+    rows, cols = 257, 2048
+    x = (rng.standard_normal(rows * cols) * 30).astype(np.float32)
+    x[::97] = np.inf
+    x[::89] = -np.inf
+    x[::83] = np.nan
+    x[::79] = -1e30
+    t = gpu.tensor([rows, cols], x)
+    expr = gpu.sum(gpu.logistic(gpu.relu(t)), 1)
+    assert "porch_exp_relaxed(" in gpu.kernel_source(expr, 0)
+    out = gpu.materialize(expr).cpu()
+    ref = host.evaluate(expr)
+    assert np.all(np.abs(out - ref) <= 1e-5 * np.abs(ref))
 
 
 @pytest.mark.gpu
