@@ -55,6 +55,7 @@ namespace porch::cg {
         int n_slots = 0;
         std::vector<int64_t> slot_elems; // floats each slot's buffer holds
         index_width width;
+        int compute_units = 256;
     };
 
     kernel_code emit_pointwise(const pointwise_request& request);

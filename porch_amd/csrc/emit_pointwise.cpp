@@ -492,7 +492,14 @@ namespace porch::cg {
             kc.name = "porch_tiled";
             kc.n_slots = r.n_slots;
             kc.block = block_threads;
-            kc.grid_x = static_cast<unsigned>(ntq * ntp * others);
+            // Persistent workgroups (at most four per compute unit) walk the
+            // tiles: a workgroup's reads of its next tile overlap other
+            // workgroups' stores instead of the whole chip reading, then
+            // writing, in step.
+            const int64_t tiles = ntq * ntp * others;
+            const int64_t resident = static_cast<int64_t>(std::max(r.compute_units, 1)) * 4;
+            const bool persistent = tiles > resident;
+            kc.grid_x = static_cast<unsigned>(persistent ? resident : tiles);
             const char* T = r.width.type();
             const std::vector<std::string> names = coordinate_names(rank);
             const std::string qs = "q" + std::to_string(q);
@@ -507,7 +514,11 @@ namespace porch::cg {
                  std::to_string(tile + 1) + "];\n";
             // Consecutive workgroups walk along p: neighbouring tiles read
             // neighbouring segments of the same source rows.
-            s += "    const idx_t tile_id = blockIdx.x;\n";
+            if (persistent)
+                s += "    for (idx_t tile_id = blockIdx.x; tile_id < " + std::to_string(tiles) +
+                     "; tile_id += gridDim.x) {\n";
+            else
+                s += "    { const idx_t tile_id = blockIdx.x;\n";
             s += "    const idx_t tp = tile_id % " + std::to_string(ntp) + ";\n";
             s += "    const idx_t tq = (tile_id / " + std::to_string(ntp) + ") % " +
                  std::to_string(ntq) + ";\n";
@@ -758,6 +769,9 @@ namespace porch::cg {
                     s += indent + "out[" + output_index(r.shape) + "] = " + v[0] + ";\n";
             }
             if (!guard.empty()) s += "        }\n";
+            s += "    }\n";
+            // The next tile's phase 1 overwrites the stage phase 2 just read.
+            if (persistent) s += "    __syncthreads();\n";
             s += "    }\n}\n";
             return kc;
         }

@@ -383,6 +383,7 @@ namespace porch::plan {
                 r.n_slots = n_slots();
                 r.slot_elems = slot_elems();
                 r.width = width;
+                r.compute_units = compute_units;
                 add_step(cg::emit_pointwise(r), dest);
             }
 
