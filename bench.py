@@ -32,7 +32,9 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -119,11 +121,25 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
                 start.handle, stop.handle))
         _lib.lib.porch_buffer_release(out)
 
-    # Cold JIT: codegen + hiprtc + module load of this graph in this process.
+    # Cold JIT: codegen + hiprtc + module load of this graph in this process
+    # (the persistent code-object cache off, so hiprtc really runs).
+    porch.set_disk_cache(None)
     porch.reset_jit_cache()
     step(0)
     porch.synchronize()
     cold_ms = porch.jit_stats()["last_miss_ms"]
+
+    # Disk-warm JIT: a later process whose code objects are in the persistent
+    # cache.  The code objects are written here; a child process then times
+    # its first materialisation of the graph (codegen + file read + module
+    # load + launch; no hiprtc).
+    with tempfile.TemporaryDirectory(prefix="porch_jit_") as cache:
+        porch.set_disk_cache(cache)
+        porch.reset_jit_cache()
+        step(0)
+        porch.synchronize()
+        porch.set_disk_cache(None)
+        disk_ms = disk_warm_jit_ms(name, cache)
 
     for i in range(warmup):
         step(i)
@@ -176,9 +192,46 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
         "kernel_ms_median": float(np.median(kernel_ms)),
         "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                      "frac": achieved / peak, "traffic": profiled_traffic(name)},
-        "jit_ms": {"cold": cold_ms, "hit": float(np.median(hit_us)) / 1e3},
+        "jit_ms": {"cold": cold_ms, "disk": disk_ms, "hit": float(np.median(hit_us)) / 1e3},
         "steps": steps,
     }
+
+
+def disk_warm_jit_ms(name: str, cache: str):
+    """First-materialisation time of workload `name` in a fresh process whose
+    persistent code-object cache (`cache`) already holds its kernels."""
+    env = dict(os.environ, PORCH_CACHE_DIR=cache)
+    try:
+        done = subprocess.run([sys.executable, os.path.abspath(__file__), "--jit-probe", name],
+                              env=env, capture_output=True, text=True, timeout=300)
+        probe = json.loads(done.stdout.strip().splitlines()[-1])
+    except (subprocess.SubprocessError, ValueError, IndexError) as error:
+        log(f"{name}: disk-warm JIT probe failed: {error}")
+        return None
+    if not probe.get("disk_hits"):
+        log(f"{name}: disk-warm JIT probe compiled instead of reading the cache")
+        return None
+    return probe["first_ms"]
+
+
+def jit_probe(name: str) -> int:
+    """Child side of disk_warm_jit_ms: one materialisation, timed inside the
+    library, then its JIT counters as one JSON line."""
+    import porch_amd as porch
+    from porch_amd.workloads import config_graph, config_inputs, config_shapes
+
+    if not porch.is_available():
+        return 1
+    tensors = [porch.tensor(s, v) for s, v in zip(config_shapes(name), config_inputs(name))]
+    expr = config_graph(name, tensors)
+    porch.synchronize()
+    porch.materialize(expr)
+    porch.synchronize()
+    stats = porch.jit_stats()
+    print(json.dumps({"first_ms": stats["last_miss_ms"], "disk_hits": stats["disk_hits"],
+                      "compiles": stats["compiles"], "module_load_ms": stats["module_load_ms"]}),
+          flush=True)
+    return 0
 
 
 def cpu_baseline(name: str, max_seconds: float = 20.0) -> dict:
@@ -231,7 +284,10 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--configs", default="elementwise,view_chain,softmax,logistic_rowsum,matmul_epilogue")
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--jit-probe", default=None, help=argparse.SUPPRESS)
     args = parser.parse_args()
+    if args.jit_probe:
+        return jit_probe(args.jit_probe)
     if args.gpus != 1:
         print("bench.py measures one GPU: porch's fused-graph path runs every graph on "
               "one device and has no multi-GPU execution; run with --gpus 1.",
@@ -257,6 +313,7 @@ def main() -> int:
         r = results[name]
         log(f"{name}: {r['value']:.1f} {r['unit']} whole-job, kernel {r['kernel_ms_mean']*1e3:.1f} us, "
             f"roofline {r['roofline']['frac']*100:.1f}%, JIT cold {r['jit_ms']['cold']:.1f} ms "
+            f"disk {r['jit_ms']['disk'] if r['jit_ms']['disk'] is None else round(r['jit_ms']['disk'], 2)} ms "
             f"hit {r['jit_ms']['hit']*1e3:.1f} us")
         if not args.no_cpu:
             results[name]["cpu_baseline"] = cpu_baseline(name)

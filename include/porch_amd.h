@@ -230,12 +230,28 @@ typedef struct porch_jit_stats {
     double module_load_ms;   /* host time in hipModuleLoadData */
     double last_miss_ms;     /* last cold materialize: plan+compile+load */
     double last_hit_us;      /* last cache-hit materialize, call to return */
+    uint64_t disk_hits;      /* code objects read from the on-disk cache */
+    double disk_ms;          /* host time reading them */
 } porch_jit_stats;
 
 porch_status porch_get_jit_stats(porch_jit_stats* stats);
 
-/* Drops every cached plan, code object and module (for cold-JIT timing). */
+/* Drops every cached plan, code object and module (for cold-JIT timing).
+ * The on-disk cache is left as it is. */
 porch_status porch_reset_jit_cache(void);
+
+/* Directory of the persistent code-object cache: compiled kernels are
+ * written there and read back by later processes instead of compiling
+ * again.  NULL or "" turns it off for the rest of the process.  By default
+ * the cache is off unless the environment variable PORCH_CACHE_DIR names a
+ * directory.  Entries are checked (full key, hiprtc version, checksum) on
+ * every read, so a stale or damaged file is recompiled, never loaded.
+ * No reference counterpart: the reference's cache lives in memory only,
+ * src/cuda_jit.cpp:358-378. */
+porch_status porch_set_disk_cache(const char* directory);
+
+/* The directory in use ("" when off), copied into out[capacity]. */
+porch_status porch_disk_cache_directory(char* out, size_t capacity);
 
 /* ------------------------------------------------------------------ */
 /* Timing support (HIP events on the calling thread's current stream)   */

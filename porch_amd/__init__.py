@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import builtins
 import ctypes
+import os
 import json
 import threading
 from typing import Iterable, Sequence
@@ -748,3 +749,14 @@ def jit_stats() -> dict:
 
 def reset_jit_cache() -> None:
     check(lib.porch_reset_jit_cache())
+
+
+def set_disk_cache(directory) -> None:
+    """Directory of the persistent code-object cache; None turns it off."""
+    check(lib.porch_set_disk_cache(None if directory is None else os.fsencode(directory)))
+
+
+def disk_cache_directory() -> str:
+    text = ctypes.create_string_buffer(4096)
+    check(lib.porch_disk_cache_directory(text, len(text)))
+    return os.fsdecode(text.value)

@@ -63,6 +63,8 @@ class JitStats(ctypes.Structure):
         ("module_load_ms", ctypes.c_double),
         ("last_miss_ms", ctypes.c_double),
         ("last_hit_us", ctypes.c_double),
+        ("disk_hits", ctypes.c_uint64),
+        ("disk_ms", ctypes.c_double),
     ]
 
 
@@ -129,6 +131,8 @@ _SIGNATURES = {
                                            ctypes.POINTER(ctypes.c_size_t)]),
     "porch_get_jit_stats": (ctypes.c_int32, [ctypes.POINTER(JitStats)]),
     "porch_reset_jit_cache": (ctypes.c_int32, []),
+    "porch_set_disk_cache": (ctypes.c_int32, [ctypes.c_char_p]),
+    "porch_disk_cache_directory": (ctypes.c_int32, [ctypes.c_char_p, ctypes.c_size_t]),
     "porch_event_create": (ctypes.c_int32, [ctypes.POINTER(_P)]),
     "porch_event_record": (ctypes.c_int32, [_P]),
     "porch_event_synchronize": (ctypes.c_int32, [_P]),

@@ -1,6 +1,7 @@
 // The extern "C" boundary declared in include/porch_amd.h.
 
 #include "porch_amd.h"
+#include "disk_cache.hpp"
 
 #include "internal.hpp"
 #include "planner.hpp"
@@ -414,6 +415,22 @@ porch_status porch_get_jit_stats(porch_jit_stats* stats) {
         stats->module_load_ms = c.module_load_ms;
         stats->last_miss_ms = c.last_miss_ms;
         stats->last_hit_us = c.last_hit_us;
+        stats->disk_hits = c.disk_hits;
+        stats->disk_ms = c.disk_ms;
+    });
+}
+
+porch_status porch_set_disk_cache(const char* directory) {
+    return guarded([&] { rt::disk::set_directory(directory == nullptr ? "" : directory); });
+}
+
+porch_status porch_disk_cache_directory(char* out, size_t capacity) {
+    return guarded([&] {
+        require(out != nullptr && capacity > 0, "output buffer is empty");
+        const std::string dir = rt::disk::directory();
+        const size_t n = std::min(dir.size(), capacity - 1);
+        std::memcpy(out, dir.data(), n);
+        out[n] = '\0';
     });
 }
 

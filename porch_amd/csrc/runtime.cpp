@@ -1,14 +1,18 @@
 #include "runtime.hpp"
 
+#include "disk_cache.hpp"
+
 #include "porch/hip_jit.hpp"
 
 #include <sys/syscall.h>
 #include <unistd.h>
 
+#include <chrono>
 #include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <map>
+#include <optional>
 #include <stdexcept>
 #include <unordered_map>
 
@@ -399,6 +403,31 @@ namespace porch::rt {
         }
 
         const hip::api& c = hip::compiler();
+        // The on-disk entry is valid only for the compiler that wrote it.
+        static const std::string compiler_tag = [&] {
+            int major = 0;
+            int minor = 0;
+            if (c.rtc_version != nullptr) (void)c.rtc_version(&major, &minor);
+            return std::string("\0hiprtc ") + std::to_string(major) + "." + std::to_string(minor) +
+                   "\0porch code object 1";
+        }();
+        const std::string disk_key = key + compiler_tag;
+        {
+            const auto read_start = std::chrono::steady_clock::now();
+            if (std::optional<std::string> stored = disk::load(disk_key)) {
+                auto object = std::make_shared<code_object>();
+                object->bytes = std::move(*stored);
+                {
+                    std::scoped_lock lock{counters_mutex()};
+                    counters().disk_hits += 1;
+                    counters().disk_ms += elapsed_ms(read_start);
+                }
+                std::scoped_lock lock{codes().mutex};
+                auto [it, inserted] = codes().entries.emplace(key, object);
+                return it->second;
+            }
+        }
+
         const auto start = std::chrono::steady_clock::now();
         rtc_program program;
         const std::string text{source};
@@ -441,6 +470,7 @@ namespace porch::rt {
             counters().compiles += 1;
             counters().compile_ms += object->compile_ms;
         }
+        disk::store(disk_key, object->bytes);
         std::scoped_lock lock{codes().mutex};
         auto [it, inserted] = codes().entries.emplace(key, object);
         return it->second;

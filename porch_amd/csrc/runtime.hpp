@@ -139,6 +139,8 @@ namespace porch::rt {
         double module_load_ms = 0;
         double last_miss_ms = 0;
         double last_hit_us = 0;
+        uint64_t disk_hits = 0;  // code objects read from the on-disk cache
+        double disk_ms = 0;      // host time reading them
     };
     jit_counters& counters();
     std::mutex& counters_mutex();
