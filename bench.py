@@ -125,9 +125,13 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
     # (the persistent code-object cache off, so hiprtc really runs).
     porch.set_disk_cache(None)
     porch.reset_jit_cache()
+    before = porch.jit_stats()
     step(0)
     porch.synchronize()
-    cold_ms = porch.jit_stats()["last_miss_ms"]
+    after = porch.jit_stats()
+    cold_ms = after["last_miss_ms"]
+    cold_split = {part: after[part] - before[part]
+                  for part in ("codegen_ms", "compile_ms", "module_load_ms")}
 
     # Disk-warm JIT: a later process whose code objects are in the persistent
     # cache.  The code objects are written here; a child process then times
@@ -192,7 +196,9 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
         "kernel_ms_median": float(np.median(kernel_ms)),
         "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                      "frac": achieved / peak, "traffic": profiled_traffic(name)},
-        "jit_ms": {"cold": cold_ms, "disk": disk_ms, "hit": float(np.median(hit_us)) / 1e3},
+        "jit_ms": {"cold": cold_ms, "cold_codegen": cold_split["codegen_ms"],
+                   "cold_hiprtc": cold_split["compile_ms"], "cold_module_load": cold_split["module_load_ms"],
+                   "disk": disk_ms, "hit": float(np.median(hit_us)) / 1e3},
         "steps": steps,
     }
 

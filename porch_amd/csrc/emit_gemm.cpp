@@ -115,8 +115,10 @@ namespace porch::cg {
         // to LDS in the X[k % 2][i][k / 2] layout.
         void operand_code(std::string& load, std::string& store, const char* X,
                           const gemm_operand& op, bool is_a, int64_t rows_ext,
-                          int64_t k_ext, const operand_layout& lay) {
-            const bool i_exact = rows_ext % (is_a ? BM : BN) == 0;
+                          int64_t k_ext, const operand_layout& lay, int tile_rows) {
+            const bool i_exact = rows_ext % tile_rows == 0;
+            // float4 chunks per thread: tile_rows x 16 floats over 256 threads
+            const std::string chunks = std::to_string(tile_rows / 64);
             const bool k_exact = k_ext % BK == 0;
             // i: the m (A) or n (B) coordinate; stride_i / stride_k in memory
             const int64_t stride_i = is_a ? op.stride_row : op.stride_col;
@@ -126,7 +128,7 @@ namespace porch::cg {
             const std::string x{X};
             if (lay.k_major) {
                 // chunk c: i = c >> 2, k = (c & 3) * 4 .. +3
-                load += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                load += "    #pragma unroll\n    for (int i = 0; i < " + chunks + "; ++i) {\n";
                 load += "        const int c = tid + i * 256;\n";
                 load += "        const int ii = c >> 2;\n        const int kq = (c & 3) * 4;\n";
                 load += "        const idx_t gi = " + i0 + " + ii;\n";
@@ -150,7 +152,7 @@ namespace porch::cg {
                 }
                 load += "    }\n";
                 // k = kq, kq+2 go to parity 0, k = kq+1, kq+3 to parity 1
-                store += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                store += "    #pragma unroll\n    for (int i = 0; i < " + chunks + "; ++i) {\n";
                 store += "        const int c = tid + i * 256;\n";
                 store += "        const int ii = c >> 2;\n        const int kq = (c & 3) * 4;\n";
                 store += "        *reinterpret_cast<float2*>(&" + x + "s[nb][0][ii][kq >> 1]) = make_float2(r" +
@@ -163,7 +165,7 @@ namespace porch::cg {
                 // contiguous along i: chunk c: k = c & 15, i = (c >> 4) * 4 .. +3
                 // (a wave reads 16 rows x 64 bytes; its LDS writes spread
                 // over the banks instead of hitting two of them)
-                load += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                load += "    #pragma unroll\n    for (int i = 0; i < " + chunks + "; ++i) {\n";
                 load += "        const int c = tid + i * 256;\n";
                 load += "        const int kk = c & 15;\n        const int iq = (c >> 4) * 4;\n";
                 load += "        const idx_t gi = " + i0 + " + iq;\n";
@@ -186,7 +188,7 @@ namespace porch::cg {
                             std::to_string(stride_k) + "] : 0.0f;\n";
                 }
                 load += "    }\n";
-                store += "    #pragma unroll\n    for (int i = 0; i < 2; ++i) {\n";
+                store += "    #pragma unroll\n    for (int i = 0; i < " + chunks + "; ++i) {\n";
                 store += "        const int c = tid + i * 256;\n";
                 store += "        const int kk = c & 15;\n        const int iq = (c >> 4) * 4;\n";
                 store += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) " + x +
@@ -211,12 +213,19 @@ namespace porch::cg {
         }
 
         kernel_code emit_gemm_mfma(const gemm_request& r) {
-            const int64_t tiles_m = (r.m + BM - 1) / BM;
+            // 256-row tiles (each wave 128 x 64: 4 x 2 MFMA blocks) halve the
+            // LDS reads per MFMA and the B re-reads; used while they still
+            // give every compute unit a tile (measured 2.7% faster at 4096^3).
             const int64_t tiles_n = (r.n + BN - 1) / BN;
+            const int bm = (r.m >= 256 && ((r.m + 255) / 256) * tiles_n >= r.compute_units) ? 256 : BM;
+            const int ib = bm / 64; // 32-row MFMA blocks per wave
+            const int64_t tiles_m = (r.m + bm - 1) / bm;
             const int64_t tiles = tiles_m * tiles_n;
             const int64_t steps = (r.k + BK - 1) / BK;
             const operand_layout la = layout_of(r.a, true, r.m, r.k);
             const operand_layout lb = layout_of(r.b, false, r.n, r.k);
+            const std::string IB = std::to_string(ib);
+            const std::string HALF = std::to_string(bm / 2);
             kernel_code kc;
             kc.kind = "gemm.mfma";
             kc.name = "porch_gemm";
@@ -227,9 +236,11 @@ namespace porch::cg {
             std::string& s = kc.source;
             s = kernel_prologue(r.n_slots, T);
             s += "typedef float floatx16 __attribute__((ext_vector_type(16)));\n";
-            s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" +
+            // Two workgroups per compute unit (two waves per SIMD): the
+            // register budget within which the accumulators stay in VGPRs.
+            s += "extern \"C\" __global__ void __launch_bounds__(256, 2) porch_gemm(" +
                  kernel_params(r.n_slots) + ") {\n";
-            s += "    __shared__ __attribute__((aligned(16))) float As[2][2][" + std::to_string(BM) + "][" +
+            s += "    __shared__ __attribute__((aligned(16))) float As[2][2][" + std::to_string(bm) + "][" +
                  std::to_string(PITCH) + "];\n";
             s += "    __shared__ __attribute__((aligned(16))) float Bs[2][2][" + std::to_string(BN) + "][" +
                  std::to_string(PITCH) + "];\n";
@@ -247,21 +258,21 @@ namespace porch::cg {
                 s += "    const int tile = blockIdx.x;\n";
             }
             s += "    const idx_t m0 = (idx_t)(tile / " + std::to_string(tiles_n) + ") * " +
-                 std::to_string(BM) + ";\n";
+                 std::to_string(bm) + ";\n";
             s += "    const idx_t n0 = (idx_t)(tile % " + std::to_string(tiles_n) + ") * " +
                  std::to_string(BN) + ";\n";
             s += "    const float* __restrict__ A = a" + std::to_string(r.a.slot) + " + " +
                  std::to_string(r.a.offset) + ";\n";
             s += "    const float* __restrict__ B = a" + std::to_string(r.b.slot) + " + " +
                  std::to_string(r.b.offset) + ";\n";
-            s += "    float rA[8];\n    float rB[8];\n";
-            s += "    floatx16 acc[2][2];\n";
-            s += "    #pragma unroll\n    for (int i = 0; i < 2; ++i)\n";
+            s += "    float rA[" + std::to_string(4 * (bm / 64)) + "];\n    float rB[8];\n";
+            s += "    floatx16 acc[" + IB + "][2];\n";
+            s += "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n";
             s += "        #pragma unroll\n        for (int j = 0; j < 2; ++j)\n";
             s += "            #pragma unroll\n            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;\n";
             std::string load_a, store_a, load_b, store_b;
-            operand_code(load_a, store_a, "A", r.a, true, r.m, r.k, la);
-            operand_code(load_b, store_b, "B", r.b, false, r.n, r.k, lb);
+            operand_code(load_a, store_a, "A", r.a, true, r.m, r.k, la, bm);
+            operand_code(load_b, store_b, "B", r.b, false, r.n, r.k, lb, BN);
             // prologue: tile 0
             s += "    {\n        const idx_t k0 = 0;\n        const int nb = 0;\n";
             s += load_a + load_b + store_a + store_b;
@@ -275,46 +286,53 @@ namespace porch::cg {
             // this lane's k parity and row inside each 32-row block
             s += "        const int h = lane >> 5;\n";
             s += "        const int li = lane & 31;\n";
-            s += "        float av[2][8];\n        float bv[2][8];\n";
-            s += "        #pragma unroll\n        for (int b = 0; b < 2; ++b) {\n";
-            s += "            const float4 al = *reinterpret_cast<const float4*>(&As[cb][h][wm * 64 + b * 32 + li][0]);\n";
-            s += "            const float4 ah = *reinterpret_cast<const float4*>(&As[cb][h][wm * 64 + b * 32 + li][4]);\n";
-            s += "            const float4 bl = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][0]);\n";
-            s += "            const float4 bh = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][4]);\n";
+            s += "        float av[" + IB + "][8];\n        float bv[2][8];\n";
+            s += "        #pragma unroll\n        for (int b = 0; b < " + IB + "; ++b) {\n";
+            s += "            const float4 al = *reinterpret_cast<const float4*>(&As[cb][h][wm * " + HALF +
+                 " + b * 32 + li][0]);\n";
+            s += "            const float4 ah = *reinterpret_cast<const float4*>(&As[cb][h][wm * " + HALF +
+                 " + b * 32 + li][4]);\n";
             s += "            av[b][0] = al.x; av[b][1] = al.y; av[b][2] = al.z; av[b][3] = al.w;\n";
             s += "            av[b][4] = ah.x; av[b][5] = ah.y; av[b][6] = ah.z; av[b][7] = ah.w;\n";
+            s += "        }\n";
+            s += "        #pragma unroll\n        for (int b = 0; b < 2; ++b) {\n";
+            s += "            const float4 bl = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][0]);\n";
+            s += "            const float4 bh = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][4]);\n";
             s += "            bv[b][0] = bl.x; bv[b][1] = bl.y; bv[b][2] = bl.z; bv[b][3] = bl.w;\n";
             s += "            bv[b][4] = bh.x; bv[b][5] = bh.y; bv[b][6] = bh.z; bv[b][7] = bh.w;\n";
             s += "        }\n";
             s += "        #pragma unroll\n";
-            s += "        for (int st = 0; st < " + std::to_string(BK / 2) + "; ++st) {\n";
-            s += "            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0][st], bv[0][st], acc[0][0], 0, 0, 0);\n";
-            s += "            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0][st], bv[1][st], acc[0][1], 0, 0, 0);\n";
-            s += "            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1][st], bv[0][st], acc[1][0], 0, 0, 0);\n";
-            s += "            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1][st], bv[1][st], acc[1][1], 0, 0, 0);\n";
-            s += "        }\n";
+            s += "        for (int st = 0; st < " + std::to_string(BK / 2) + "; ++st)\n";
+            s += "            #pragma unroll\n            for (int i = 0; i < " + IB + "; ++i)\n";
+            s += "                #pragma unroll\n                for (int j = 0; j < 2; ++j)\n";
+            s += "                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][st], bv[j][st], acc[i][j], 0, 0, 0);\n";
             if (la.vector && lb.vector) {
-                // Instruction order for the scheduler: the eight 128-bit LDS
-                // reads first, then one of the four global loads after every
-                // four MFMAs, so the next tile's loads leave early and their
-                // latency hides under the remaining MFMAs (measured 7% faster
-                // at 4096^3 than the compiler's own order, which issued them
+                // Instruction order for the scheduler: the 128-bit LDS reads
+                // first, then one of the next tile's global loads after every
+                // four MFMAs, so those loads leave early and their latency
+                // hides under the remaining MFMAs (measured 7% faster at
+                // 4096^3 than the compiler's own order, which issued them
                 // after nearly all MFMAs).
-                s += "        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);\n";
-                for (int g = 0; g < 4; ++g) {
+                const int ds_reads = 2 * ib + 4;
+                const int vmem = bm / 64 + BN / 64;
+                const int mfmas = (BK / 2) * ib * 2;
+                s += "        __builtin_amdgcn_sched_group_barrier(0x100, " + std::to_string(ds_reads) + ", 0);\n";
+                for (int g = 0; g < vmem; ++g) {
                     s += "        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);\n";
                     s += "        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);\n";
                 }
-                s += "        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);\n";
+                s += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(mfmas - 4 * vmem) +
+                     ", 0);\n";
             }
             s += "        if (more) {\n" + store_a + store_b + "        }\n";
             s += "        __syncthreads();\n";
             s += "    }\n";
             // epilogue
-            s += "    #pragma unroll\n    for (int bi = 0; bi < 2; ++bi)\n";
+            s += "    #pragma unroll\n    for (int bi = 0; bi < " + IB + "; ++bi)\n";
             s += "    #pragma unroll\n    for (int bj = 0; bj < 2; ++bj)\n";
             s += "    #pragma unroll\n    for (int v = 0; v < 16; ++v) {\n";
-            s += "        const idx_t q0 = m0 + wm * 64 + bi * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);\n";
+            s += "        const idx_t q0 = m0 + wm * " + HALF +
+                 " + bi * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);\n";
             s += "        const idx_t q1 = n0 + wn * 64 + bj * 32 + (lane & 31);\n";
             s += "        if (q0 < " + std::to_string(r.m) + " && q1 < " + std::to_string(r.n) + ") {\n";
             s += "            const float acc_v = acc[bi][bj][v];\n";

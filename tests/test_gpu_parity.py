@@ -153,6 +153,21 @@ def test_reductions_over_every_axis(gpu):
                                   host.evaluate(expr))
 
 
+@pytest.mark.parametrize("shape", [(6, 70, 9), (3, 5, 2100), (130, 7)])
+def test_softmax_over_every_axis_within_1e6(gpu, shape):
+    """Non-last axes plan the reductions into temporaries (and a column
+    reduction); the last axis is one row program."""
+    porch = gpu
+    rng = np.random.default_rng(sum(shape))
+    x = (rng.standard_normal(int(np.prod(shape))) * 3).astype(np.float32)
+    t = porch.tensor(list(shape), x)
+    for axis in range(len(shape)):
+        expr = porch.softmax(t, axis)
+        out = porch.materialize(expr).cpu().reshape(shape)
+        ref = host.evaluate(expr)
+        assert np.all(np.abs(out - ref) <= 1e-6 * np.abs(ref)), (shape, axis)
+
+
 def test_max_semantics_match_reference(gpu):
     porch = gpu
     t = porch.tensor([2, 5], [-np.inf] * 5 + [1, 2, 3, 4, 5])
@@ -277,6 +292,24 @@ def test_mfma_gemm_edges_and_tails(gpu, m, k, n):
     out = porch.materialize(expr).cpu().reshape(m, n)
     ref = a.astype(np.float64) @ b.astype(np.float64)
     assert (np.abs(out - ref) <= 1e-5 * gemm_bound(a.astype(np.float64), b.astype(np.float64)) + 1e-30).all()
+
+
+@pytest.mark.parametrize("transposed_a", [False, True])
+def test_mfma_wide_tiles_with_tails(gpu, transposed_a):
+    """Enough rows for 256-row tiles, with tails in m, n and k."""
+    porch = gpu
+    m, k, n = 4100, 333, 4000
+    rng = np.random.default_rng(41 + transposed_a)
+    a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, size=(k, n)).astype(np.float32)
+    ta = porch.transpose(porch.tensor([k, m], np.ascontiguousarray(a.T))) if transposed_a \
+        else porch.tensor([m, k], a)
+    expr = porch.matmul(ta, porch.tensor([k, n], b))
+    source = porch.kernel_source(expr, len(porch.plan(expr)["kernels"]) - 1)
+    assert "float As[2][2][256]" in source
+    out = porch.materialize(expr).cpu().reshape(m, n)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    assert (np.abs(out - a64 @ b64) <= 1e-5 * gemm_bound(a64, b64) + 1e-30).all()
 
 
 @pytest.mark.parametrize("layout", ["at", "bt", "both", "offset"])
