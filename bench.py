@@ -240,7 +240,10 @@ def jit_probe(name: str) -> int:
     return 0
 
 
-def cpu_baseline(name: str, max_seconds: float = 20.0) -> dict:
+def cpu_baseline(name: str, min_seconds: float = 10.0) -> dict:
+    """The host evaluator (the oracle, OpenMP over the host's threads) timed
+    on the same workload, repeated until at least `min_seconds` of CPU work
+    has run; the median run is reported."""
     from oracle import host
     from porch_amd.workloads import config_graph, config_inputs, config_shapes
 
@@ -254,32 +257,33 @@ def cpu_baseline(name: str, max_seconds: float = 20.0) -> dict:
         t._state = porch._State(s, porch.device())
         t._state.storage = porch._Storage(None, v)
         tensors.append(t)
-    sample = "full workload"
+    sample = "the full workload"
     scale = 1.0
     if name == "matmul_epilogue":
-        rows = 256  # 1/16 of the rows of A; time scaled by 16
+        rows = 256  # 1/16 of the rows of A and C; time scaled by 16
         a, b, bias = values
         tensors[0]._state = porch._State([rows, 4096], porch.device())
         tensors[0]._state.storage = porch._Storage(None, a[: rows * 4096])
         expr = porch.relu(porch.matmul(tensors[0], tensors[1]) +
                           porch.broadcast_to(tensors[2], [rows, 4096])) - 0.5
-        sample = f"{rows} of 4096 rows of C (time x {4096 // rows})"
+        sample = f"{rows} of the 4096 rows of C per run (time x {4096 // rows})"
         scale = 4096 / rows
     else:
         expr = config_graph(name, tensors)
     times = []
     host.evaluate(expr)  # warm-up
     start = time.perf_counter()
-    while len(times) < 5 and time.perf_counter() - start < max_seconds:
+    while len(times) < 3 or time.perf_counter() - start < min_seconds:
         t0 = time.perf_counter()
         host.evaluate(expr)
         times.append((time.perf_counter() - t0) * scale)
+    spent = time.perf_counter() - start
     seconds = float(np.median(times))
     bound, work = WORK[name]
     value = work / seconds / (1e9 if bound == "hbm" else 1e12)
     return {"value": value, "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
             "cores": host.threads(), "kind": "port",
-            "sample": f"host evaluator, {sample}, median of {len(times)} runs",
+            "sample": f"host evaluator on {sample}, median of {len(times)} runs over {spent:.1f} s",
             "seconds": seconds}
 
 
