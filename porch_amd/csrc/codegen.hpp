@@ -89,6 +89,9 @@ namespace porch::cg {
         bool is_max = false;
         int n_slots = 0;
         index_width width;
+        // > 1: the axis is split into `parts` chunks (grid y); chunk g's
+        // fold goes to out[g * outputs + o] for a second pass to combine.
+        int64_t parts = 1;
     };
 
     kernel_code emit_column_reduce(const column_reduce_request& request);

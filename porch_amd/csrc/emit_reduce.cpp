@@ -1,7 +1,10 @@
 // Reductions over a non-last axis.  One lane per output element folds the
 // axis sequentially; lanes run along the output's contiguous dimension, so
 // each step of the fold is a coalesced read (the reference instead gives
-// every output its own 256-thread block, src/tensor.cpp:896-962).
+// every output its own 256-thread block, src/tensor.cpp:896-962).  When the
+// outputs alone cannot fill the machine, the axis is split into chunks
+// folded by separate workgroups (grid y) into partial results, which a
+// second pass combines in chunk order.
 
 #include "codegen.hpp"
 #include "emit_expr.hpp"
@@ -31,6 +34,9 @@ namespace porch::cg {
         kc.grid_x = static_cast<unsigned>(
             std::clamp<int64_t>((outputs + 255) / 256, 1, int64_t{1} << 22)
         );
+        const int64_t parts = std::max<int64_t>(r.parts, 1);
+        const int64_t chunk = (extent + parts - 1) / parts;
+        kc.grid_y = static_cast<unsigned>(parts);
         const char* T = r.width.type();
         std::vector<std::string> names;
         for (size_t d = 0; d < rank; ++d) names.push_back("q" + std::to_string(d));
@@ -55,9 +61,23 @@ namespace porch::cg {
         }
         s += std::string("        float acc = ") + (r.is_max ? "-PORCH_FLT_MAX" : "0.0f") +
              ";\n";
-        s += std::string("        for (") + T + " q" + std::to_string(r.axis) + " = 0; q" +
-             std::to_string(r.axis) + " < " + std::to_string(extent) + "; ++q" +
-             std::to_string(r.axis) + ") {\n";
+        // Unrolled so that several rows' loads are in flight at once; the
+        // fold itself stays in row order.
+        const std::string qa = "q" + std::to_string(r.axis);
+        if (parts > 1) {
+            s += std::string("        const ") + T + " first = (" + T + ")blockIdx.y * " +
+                 std::to_string(chunk) + ";\n";
+            s += std::string("        const ") + T + " last = first + " + std::to_string(chunk) + " < " +
+                 std::to_string(extent) + " ? first + " + std::to_string(chunk) + " : " +
+                 std::to_string(extent) + ";\n";
+            s += "        #pragma unroll 8\n";
+            s += std::string("        for (") + T + " " + qa + " = first; " + qa + " < last; ++" + qa + ") {\n";
+        }
+        else {
+            s += "        #pragma unroll 8\n";
+            s += std::string("        for (") + T + " " + qa + " = 0; " + qa + " < " +
+                 std::to_string(extent) + "; ++" + qa + ") {\n";
+        }
         std::string body;
         emitter em(k, body, 1);
         em.indent = "            ";
@@ -79,7 +99,8 @@ namespace porch::cg {
         if (r.is_max) s += "            acc = acc > " + v + " ? acc : " + v + ";\n";
         else s += "            acc += " + v + ";\n";
         s += "        }\n";
-        s += "        out[o] = acc;\n";
+        if (parts > 1) s += "        out[(idx_t)blockIdx.y * " + std::to_string(outputs) + " + o] = acc;\n";
+        else s += "        out[o] = acc;\n";
         s += "    }\n}\n";
         return kc;
     }

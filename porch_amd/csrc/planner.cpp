@@ -365,7 +365,41 @@ namespace porch::plan {
                 r.is_max = n.kind == ir::op::max;
                 r.n_slots = n_slots();
                 r.width = width;
-                add_step(cg::emit_column_reduce(r), dest);
+                // Few outputs over a long axis (and enough work to be worth a
+                // second launch): split the axis so that about four
+                // workgroups per compute unit fold chunks of at least 32
+                // rows, then combine the partials.
+                const int64_t extent = shape[r.axis];
+                const int64_t outputs = ir::numel(n.out);
+                const int64_t groups = (outputs + 255) / 256;
+                const int64_t target = static_cast<int64_t>(compute_units) * 4;
+                int64_t parts = std::min(target / std::max<int64_t>(groups, 1), extent / 32);
+                if (extent < 256 || outputs * extent < (int64_t{1} << 20)) parts = 1;
+                if (parts < 2) {
+                    add_step(cg::emit_column_reduce(r), dest);
+                    return;
+                }
+                r.parts = parts;
+                const int partial = static_cast<int>(plan.temp_elems.size());
+                plan.temp_elems.push_back(parts * outputs);
+                add_step(cg::emit_column_reduce(r), {arg_ref::kind::temp, partial});
+                // Second pass: fold the partials [parts, outputs] in order.
+                cg::kexpr k2;
+                cg::knode load;
+                load.op = cg::kop::load;
+                load.slot = g.n_inputs + partial;
+                load.index = cg::ival::constant(0, 2);
+                load.index.w = {outputs, 1};
+                load.box = {{0, parts}, {0, outputs}};
+                cg::column_reduce_request c;
+                c.expr = &k2;
+                c.producer = k2.add(load);
+                c.shape = {parts, outputs};
+                c.axis = 0;
+                c.is_max = r.is_max;
+                c.n_slots = n_slots();
+                c.width = width;
+                add_step(cg::emit_column_reduce(c), dest);
             }
 
             void emit_pointwise(int id, arg_ref dest) {

@@ -168,6 +168,32 @@ def test_softmax_over_every_axis_within_1e6(gpu, shape):
         assert np.all(np.abs(out - ref) <= 1e-6 * np.abs(ref)), (shape, axis)
 
 
+@pytest.mark.parametrize("shape,axis", [((8192, 300), 0), ((4, 3000, 100), 1), ((2049, 1000), 0)])
+def test_long_column_reductions_bit_exact(gpu, shape, axis):
+    """Reductions whose axis is split into chunks and recombined; integer
+    values keep every order exact, so the result must equal the oracle's."""
+    porch = gpu
+    rng = np.random.default_rng(shape[0] + axis)
+    x = rng.integers(-3, 4, size=int(np.prod(shape))).astype(np.float32)
+    t = porch.tensor(list(shape), x)
+    for op in (porch.sum, porch.max):
+        for keep in (False, True):
+            expr = op(t, axis, keep)
+            assert porch.plan(expr)["kernels"][0]["grid"][1] > 1  # split
+            assert_bits_equal(porch.materialize(expr).cpu().reshape(expr.shape()), host.evaluate(expr))
+
+
+def test_softmax_over_a_long_first_axis_within_1e6(gpu):
+    porch = gpu
+    x = (np.random.default_rng(8).standard_normal(6000 * 200) * 3).astype(np.float32)
+    t = porch.tensor([6000, 200], x)
+    expr = porch.softmax(t, 0)
+    assert len(porch.plan(expr)["kernels"]) == 5  # max and sum each split in two
+    out = porch.materialize(expr).cpu().reshape(6000, 200)
+    ref = host.evaluate(expr)
+    assert np.all(np.abs(out - ref) <= 1e-6 * np.abs(ref))
+
+
 def test_max_semantics_match_reference(gpu):
     porch = gpu
     t = porch.tensor([2, 5], [-np.inf] * 5 + [1, 2, 3, 4, 5])

@@ -47,6 +47,19 @@ def test_shared_reductions_are_materialised_once():
     assert len(plan["temps"]) == 2
 
 
+def test_long_column_reductions_split_the_axis():
+    """Few outputs over a long axis: partial folds over chunks of the axis
+    (grid y), then one pass combining them in order."""
+    plan = porch.plan(porch.sum(placeholder([8192, 4096]), 0), compile=True)
+    first, second = plan["kernels"]
+    assert first["kind"] == second["kind"] == "reduce.column"
+    parts = first["grid"][1]
+    assert parts > 1 and first["dest"] == "temp0" and second["dest"] == "output"
+    assert plan["temps"] == [parts * 4096]
+    # enough outputs to fill the machine: one kernel
+    assert len(porch.plan(porch.sum(placeholder([64, 262144]), 0))["kernels"]) == 1
+
+
 def test_nested_reduction_feeds_elementwise_kernel():
     x = placeholder([1, 513])
     plan = porch.plan(porch.sum(x, 1) * 2.0 + 1.0)
