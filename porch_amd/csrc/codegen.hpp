@@ -95,6 +95,10 @@ namespace porch::cg {
     };
 
     kernel_code emit_column_reduce(const column_reduce_request& request);
+    // How many chunks to split the reduced axis into (1: no split): about
+    // four workgroups per compute unit, chunks of at least 32, and only for
+    // reductions of at least 2^20 values over an axis of at least 256.
+    int64_t column_reduce_parts(const column_reduce_request& request, int compute_units);
 
     // C = epilogue(A @ B) with A [M,K], B [K,N] given by element strides.
     struct gemm_operand {

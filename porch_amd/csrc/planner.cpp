@@ -365,16 +365,10 @@ namespace porch::plan {
                 r.is_max = n.kind == ir::op::max;
                 r.n_slots = n_slots();
                 r.width = width;
-                // Few outputs over a long axis (and enough work to be worth a
-                // second launch): split the axis so that about four
-                // workgroups per compute unit fold chunks of at least 32
-                // rows, then combine the partials.
-                const int64_t extent = shape[r.axis];
+                // Few outputs over a long axis: fold chunks of the axis in
+                // separate workgroups, then combine the partials.
                 const int64_t outputs = ir::numel(n.out);
-                const int64_t groups = (outputs + 255) / 256;
-                const int64_t target = static_cast<int64_t>(compute_units) * 4;
-                int64_t parts = std::min(target / std::max<int64_t>(groups, 1), extent / 32);
-                if (extent < 256 || outputs * extent < (int64_t{1} << 20)) parts = 1;
+                const int64_t parts = cg::column_reduce_parts(r, compute_units);
                 if (parts < 2) {
                     add_step(cg::emit_column_reduce(r), dest);
                     return;
