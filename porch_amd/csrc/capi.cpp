@@ -310,6 +310,10 @@ namespace {
                     hit = plan_hit;
                     if (!key.empty()) {
                         std::scoped_lock lock{tables().mutex};
+                        // Bounded: a caller producing ever new tables (say,
+                        // changing shapes) must not grow this without end.
+                        // Entries are rebuilt cheaply from the plan cache.
+                        if (tables().entries.size() >= 4096) tables().entries.clear();
                         tables().entries.emplace(key, entry);
                     }
                 }

@@ -538,6 +538,9 @@ namespace porch::plan {
             rt::counters().codegen_ms += plan->codegen_ms;
         }
         std::scoped_lock lock{cache().mutex};
+        // Bounded like the code-object cache; plans in use stay alive
+        // through their shared owners.
+        if (cache().entries.size() >= 4096) cache().entries.clear();
         auto [it, inserted] = cache().entries.emplace(key, plan);
         return it->second;
     }

@@ -472,6 +472,10 @@ namespace porch::rt {
         }
         disk::store(disk_key, object->bytes);
         std::scoped_lock lock{codes().mutex};
+        // Bounded; modules of dropped code objects stay loaded (plans may
+        // still launch their kernels), and a recompiled identical object
+        // reuses its module.
+        if (codes().entries.size() >= 4096) codes().entries.clear();
         auto [it, inserted] = codes().entries.emplace(key, object);
         return it->second;
     }
