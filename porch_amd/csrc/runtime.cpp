@@ -423,6 +423,7 @@ namespace porch::rt {
                     counters().disk_ms += elapsed_ms(read_start);
                 }
                 std::scoped_lock lock{codes().mutex};
+                if (codes().entries.size() >= 4096) codes().entries.clear();
                 auto [it, inserted] = codes().entries.emplace(key, object);
                 return it->second;
             }
