@@ -184,6 +184,11 @@ namespace porch {
     );
     [[nodiscard]] tensor_expr unsqueeze(tensor_expr value, size_t axis);
     [[nodiscard]] tensor_expr transpose(tensor_expr value);
+    // Rank-N axis permutation: output dimension i is dimension dims[i] of
+    // value.  An extension with no counterpart in the reference (whose
+    // transpose is rank-2 only); a pure index map, so it fuses like
+    // transpose.
+    [[nodiscard]] tensor_expr permute(tensor_expr value, std::vector<size_t> dims);
     [[nodiscard]] tensor_expr broadcast_to(
         tensor_expr value, std::vector<index_t> shape
     );

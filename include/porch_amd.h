@@ -147,6 +147,11 @@ porch_status porch_launch_fused_reduction(
 #define PORCH_OP_MINIMUM 16
 #define PORCH_OP_EXP 17
 #define PORCH_OP_RECIPROCAL 18
+/* Rank-N axis permutation.  No counterpart in the reference, whose only
+ * axis reordering is the rank-2 transpose (src/tensor.cpp:1142-1150); this
+ * generalises it.  rank/dims hold the permutation: output dimension i is
+ * operand dimension dims[i]. */
+#define PORCH_OP_PERMUTE 19
 
 /* One IR node; the flattened form of tensor_expr::node, src/tensor.cpp:48-60.
  * Operands refer to earlier entries, so a node table is topologically
@@ -159,7 +164,8 @@ typedef struct porch_node {
     float scalar;    /* SCALAR: the value */
     int32_t axis;    /* UNSQUEEZE, CONCAT, SUM, MAX */
     int32_t keepdim; /* SUM, MAX */
-    int32_t rank;    /* INPUT, SLICE, RESHAPE, BROADCAST: extents in dims */
+    int32_t rank;    /* INPUT, SLICE, RESHAPE, BROADCAST: extents in dims;
+                        PERMUTE: the permutation's length */
     int64_t dims;    /* offset into porch_graph.dims: shape[rank], then for
                         SLICE strides[rank] */
     int64_t offset;  /* SLICE: storage offset into the source */

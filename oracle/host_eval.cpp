@@ -16,6 +16,9 @@
 //       concat     axis coordinate < lhs extent ? lhs : rhs, with the
 //                  coordinates re-linearised per operand (766-818)
 //       reshape / unsqueeze  identity (731-741)
+//       permute    (no reference counterpart; the rank-N generalisation of
+//                  transpose) output coordinate i is source coordinate
+//                  perm[i]: src = sum_i c_i * contiguous source stride_{perm[i]}
 //   * + - * / in binary32 without contraction, maximum/minimum as the
 //     ternaries l > r ? l : r and l < r ? l : r (616-683), reciprocal as
 //     1.0f / x (863-868), exp as std::exp on float (the reference calls
@@ -144,6 +147,18 @@ namespace {
                     case PORCH_OP_TRANSPOSE:
                         n.shape = {l->shape[1], l->shape[0]};
                         break;
+                    case PORCH_OP_PERMUTE: {
+                        if (n.param_shape.size() != l->shape.size())
+                            throw std::invalid_argument("permute rank");
+                        std::vector<bool> seen(l->shape.size(), false);
+                        for (const int64_t a : n.param_shape) {
+                            if (a < 0 || a >= static_cast<int64_t>(l->shape.size()) || seen[a])
+                                throw std::invalid_argument("permute axes");
+                            seen[a] = true;
+                            n.shape.push_back(l->shape[a]);
+                        }
+                        break;
+                    }
                     case PORCH_OP_CONCAT:
                         n.shape = l->shape;
                         n.shape[n.axis] += r->shape[n.axis];
@@ -247,6 +262,22 @@ namespace {
                     std::vector<int64_t> src(static_cast<size_t>(n));
                     for (int64_t j = 0; j < n; ++j)
                         src[j] = (idx[j] % s[0]) * s[1] + idx[j] / s[0];
+                    eval(nd.lhs, src.data(), n, out);
+                    return;
+                }
+                case PORCH_OP_PERMUTE: {
+                    const std::vector<int64_t> sstr = contiguous(nodes[nd.lhs].shape);
+                    std::vector<int64_t> src(static_cast<size_t>(n));
+                    for (int64_t j = 0; j < n; ++j) {
+                        int64_t rest = idx[j];
+                        int64_t s = 0;
+                        for (size_t d = nd.shape.size(); d > 0; --d) {
+                            const size_t k = d - 1;
+                            s += (rest % nd.shape[k]) * sstr[nd.param_shape[k]];
+                            rest /= nd.shape[k];
+                        }
+                        src[j] = s;
+                    }
                     eval(nd.lhs, src.data(), n, out);
                     return;
                 }
@@ -457,14 +488,14 @@ int32_t porch_oracle_eval(const porch_node* table, int32_t n_nodes, const int64_
             n.keepdim = c.keepdim != 0;
             n.offset = c.offset;
             const bool has_shape = c.op == PORCH_OP_INPUT || c.op == PORCH_OP_SLICE ||
-                                   c.op == PORCH_OP_RESHAPE || c.op == PORCH_OP_BROADCAST;
+                                   c.op == PORCH_OP_RESHAPE || c.op == PORCH_OP_BROADCAST ||
+                                   c.op == PORCH_OP_PERMUTE;
             const int64_t needed = c.op == PORCH_OP_SLICE ? 2 * int64_t{c.rank}
                                    : has_shape          ? int64_t{c.rank}
                                                         : 0;
             if (needed > 0 && (c.dims < 0 || c.rank < 0 || c.dims + needed > n_dims))
                 throw std::invalid_argument("oracle: dims out of range");
-            if (c.op == PORCH_OP_INPUT || c.op == PORCH_OP_SLICE || c.op == PORCH_OP_RESHAPE ||
-                c.op == PORCH_OP_BROADCAST)
+            if (has_shape)
                 n.param_shape.assign(dims + c.dims, dims + c.dims + c.rank);
             if (c.op == PORCH_OP_SLICE)
                 n.strides.assign(dims + c.dims + c.rank, dims + c.dims + 2 * c.rank);

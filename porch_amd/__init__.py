@@ -40,7 +40,7 @@ from ._lib import (
 __all__ = [
     "device", "all", "slice", "tensor", "tensor_expr", "full", "zeros", "add",
     "subtract", "multiply", "divide", "matmul", "reshape", "unsqueeze",
-    "transpose", "broadcast_to", "concat", "sum", "max", "maximum", "minimum",
+    "transpose", "permute", "broadcast_to", "concat", "sum", "max", "maximum", "minimum",
     "exp", "reciprocal", "materialize", "relu", "softmax", "logistic",
     "backend", "backend_kind", "backend_for", "is_backend_available",
     "backend_name", "is_available", "synchronize", "plan", "kernel_source",
@@ -594,6 +594,15 @@ def unsqueeze(value, axis: int) -> tensor_expr:
 
 def transpose(value) -> tensor_expr:
     return _unary("transpose", value)
+
+
+def permute(value, dims: Sequence[int]) -> tensor_expr:
+    """Rank-N axis permutation: output dimension i is dimension dims[i] of
+    value (numpy.transpose's convention).  An extension with no counterpart
+    in the reference, whose transpose is rank-2 only."""
+    node = _Node("permute", _expr(value)._root)
+    node.shape = [int(d) for d in dims]
+    return tensor_expr._wrap(node)
 
 
 def broadcast_to(value, shape: Sequence[int]) -> tensor_expr:

@@ -19,11 +19,12 @@ ERR_OUT_OF_RANGE = 2
 ERR_RUNTIME = 3
 ERR_COMPILATION = 4
 
-# Node kinds (PORCH_OP_*), the reference's expr_kind order.
+# Node kinds (PORCH_OP_*): the reference's expr_kind order, then this
+# backend's extensions (permute).
 OPS = (
     "input", "scalar", "add", "subtract", "multiply", "divide", "matmul",
     "slice", "reshape", "unsqueeze", "transpose", "broadcast", "concat",
-    "sum", "max", "maximum", "minimum", "exp", "reciprocal",
+    "sum", "max", "maximum", "minimum", "exp", "reciprocal", "permute",
 )
 OP = {name: i for i, name in enumerate(OPS)}
 

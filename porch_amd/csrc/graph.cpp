@@ -30,6 +30,7 @@ namespace porch::ir {
             case op::reshape:
             case op::unsqueeze:
             case op::transpose:
+            case op::permute:
             case op::broadcast:
             case op::concat:
                 return true;
@@ -146,6 +147,7 @@ namespace porch::ir {
                     break;
                 case op::reshape:
                 case op::broadcast:
+                case op::permute:
                     n.shape = dims(c.dims, c.rank);
                     break;
                 default:
@@ -309,6 +311,32 @@ namespace porch::ir {
                     }
                     n.out = {lhs->out[1], lhs->out[0]};
                     return;
+                case op::permute: {
+                    if (lhs->is_scalar) {
+                        throw std::invalid_argument(
+                            "permute operand must be a tensor"
+                        );
+                    }
+                    const size_t rank = lhs->out.size();
+                    std::vector<bool> seen(rank, false);
+                    bool valid = n.shape.size() == rank;
+                    for (size_t i = 0; valid && i < rank; ++i) {
+                        const int64_t axis = n.shape[i];
+                        valid = axis >= 0 && static_cast<size_t>(axis) < rank &&
+                                !seen[static_cast<size_t>(axis)];
+                        if (valid) seen[static_cast<size_t>(axis)] = true;
+                    }
+                    if (!valid) {
+                        throw std::invalid_argument(
+                            "permute axes must be a permutation of the operand's dimensions"
+                        );
+                    }
+                    n.out.resize(rank);
+                    for (size_t i = 0; i < rank; ++i) {
+                        n.out[i] = lhs->out[static_cast<size_t>(n.shape[i])];
+                    }
+                    return;
+                }
                 case op::broadcast:
                     if (!lhs->is_scalar) require_broadcastable(lhs->out, n.shape);
                     n.out = n.shape;

@@ -34,9 +34,10 @@ namespace porch::ir {
         minimum = PORCH_OP_MINIMUM,
         exp = PORCH_OP_EXP,
         reciprocal = PORCH_OP_RECIPROCAL,
+        permute = PORCH_OP_PERMUTE,
     };
 
-    constexpr int op_count = 19;
+    constexpr int op_count = 20;
 
     struct node {
         op kind = op::input;
@@ -46,7 +47,8 @@ namespace porch::ir {
         float scalar = 0.0F;
         int64_t axis = 0;
         bool keepdim = false;
-        std::vector<int64_t> shape;   // input / slice / reshape / broadcast
+        std::vector<int64_t> shape;   // input / slice / reshape / broadcast;
+                                      // permute: the permutation
         std::vector<int64_t> strides; // slice
         int64_t offset = 0;           // slice
 

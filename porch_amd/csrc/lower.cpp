@@ -380,6 +380,13 @@ namespace porch::cg {
             }
             case ir::op::transpose:
                 return at(n.lhs, {coords[1], coords[0]});
+            case ir::op::permute: {
+                // output dimension i is operand dimension shape[i]
+                std::vector<ival> child(coords.size());
+                for (size_t i = 0; i < coords.size(); ++i)
+                    child[static_cast<size_t>(n.shape[i])] = coords[i];
+                return at(n.lhs, child);
+            }
             case ir::op::broadcast: {
                 const ir::node& src = g.at(n.lhs);
                 if (src.is_scalar) return at(n.lhs, {});

@@ -157,7 +157,7 @@ namespace porch::plan {
                 if (n.kind == ir::op::input) return true;
                 if (n.kind == ir::op::slice || n.kind == ir::op::reshape ||
                     n.kind == ir::op::unsqueeze || n.kind == ir::op::transpose ||
-                    n.kind == ir::op::broadcast)
+                    n.kind == ir::op::permute || n.kind == ir::op::broadcast)
                     return pure_view_of_input(n.lhs);
                 return false;
             }

@@ -566,6 +566,9 @@ namespace porch {
         return with_axis(ir::op::unsqueeze, value, axis, false);
     }
     tensor_expr transpose(tensor_expr value) { return unary(ir::op::transpose, value); }
+    tensor_expr permute(tensor_expr value, std::vector<size_t> dims) {
+        return with_shape(ir::op::permute, value, std::vector<index_t>(dims.begin(), dims.end()));
+    }
     tensor_expr broadcast_to(tensor_expr value, std::vector<index_t> shape) {
         return with_shape(ir::op::broadcast, value, std::move(shape));
     }

@@ -1,5 +1,5 @@
 """Seeded random graphs mixing every kind of region the planner forms:
-views, concat, broadcasts, elementwise arithmetic, sum/max reductions over
+views (permutes included), concat, broadcasts, elementwise arithmetic, sum/max reductions over
 any axis (fused into row programs, column reductions, or materialised
 temporaries), and matmuls whose operands are expressions and whose results
 feed further ops.
@@ -51,8 +51,11 @@ def random_graph(rng, make):
                 expr = expr - porch.broadcast_to(reduced, shape)
             else:
                 expr = reduced
-        elif kind == 3 and rank == 2:
-            expr = porch.transpose(expr)
+        elif kind == 3 and rank >= 2:
+            if rank == 2 and rng.integers(0, 2):
+                expr = porch.transpose(expr)
+            else:
+                expr = porch.permute(expr, [int(a) for a in rng.permutation(rank)])
         elif kind == 4:
             lazy = porch.tensor(expr)
             items = [porch.slice(int(rng.integers(0, e)), e, int(rng.integers(1, 3))) for e in shape]
