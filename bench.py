@@ -58,6 +58,9 @@ WORK = {
     "logistic_rowsum": ("hbm", 16384 * 2048 * 4 + 2 * 2048 * 4 + 16384 * 4),
     "matmul_epilogue": ("mfma", 2 * 4096 ** 3),
     "copy": ("hbm", 2 * 8192 * 8192 * 4),
+    "batched_transpose": ("hbm", 2 * 64 * 512 * 512 * 4),
+    "heads_permute": ("hbm", 2 * 32 * 1024 * 16 * 128 * 4),
+    "batched_matmul": ("mfma", 2 * 32 * 1024 ** 3),
 }
 DESCRIPTION = {
     "elementwise": "(a + b) * 2 - 1, a, b fp32 [1048576]",
@@ -66,10 +69,14 @@ DESCRIPTION = {
     "logistic_rowsum": "sum(logistic(relu(x*bcast(w) + bcast(bias))), 1), x fp32 [16384,2048]",
     "matmul_epilogue": "relu(A @ B + bcast(bias)) - 0.5, A, B fp32 [4096,4096]",
     "copy": "reshape(x) copy, x fp32 [8192,8192] (byte-counter calibration)",
+    "batched_transpose": "permute(x, [0,2,1]), x fp32 [64,512,512]",
+    "heads_permute": "permute(x, [0,2,1,3]), x fp32 [32,1024,16,128]",
+    "batched_matmul": "relu(batched_matmul(A, B) + bcast(bias)) - 0.5, A, B fp32 [32,1024,1024]",
 }
 # Input copies rotated through so that a step never re-reads cached data.
 ROTATION = {"elementwise": 48, "view_chain": 8, "softmax": 4, "logistic_rowsum": 6,
-            "matmul_epilogue": 1, "copy": 2}
+            "matmul_epilogue": 1, "copy": 2, "batched_transpose": 4, "heads_permute": 2,
+            "batched_matmul": 1}
 # Counter summaries (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) per workload.
 PROFILES = os.path.join(ROOT, "profiles")
 
@@ -268,6 +275,16 @@ def cpu_baseline(name: str, min_seconds: float = 10.0) -> dict:
                           porch.broadcast_to(tensors[2], [rows, 4096])) - 0.5
         sample = f"{rows} of the 4096 rows of C per run (time x {4096 // rows})"
         scale = 4096 / rows
+    elif name == "batched_matmul":
+        entries = 1  # 1 of the 32 batch entries; time scaled by 32
+        a, b, bias = values
+        for i, (shape, v) in enumerate(((([entries, 1024, 1024]), a), (([entries, 1024, 1024]), b))):
+            tensors[i]._state = porch._State(shape, porch.device())
+            tensors[i]._state.storage = porch._Storage(None, v[: entries * 1024 * 1024])
+        expr = porch.relu(porch.batched_matmul(tensors[0], tensors[1]) +
+                          porch.broadcast_to(tensors[2], [entries, 1024, 1024])) - 0.5
+        sample = f"{entries} of the 32 batch entries per run (time x {32 // entries})"
+        scale = 32 / entries
     else:
         expr = config_graph(name, tensors)
     times = []

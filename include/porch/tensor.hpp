@@ -179,6 +179,11 @@ namespace porch {
     [[nodiscard]] tensor multiply(const tensor& lhs, const tensor& rhs);
     [[nodiscard]] tensor divide(const tensor& lhs, const tensor& rhs);
     [[nodiscard]] tensor_expr matmul(tensor_expr lhs, tensor_expr rhs);
+    // [B, M, K] @ [B, K, N] -> [B, M, N]: matmul per batch entry.  An
+    // extension with no counterpart in the reference (whose matmul is
+    // rank-2 only); broadcast_to a rank-2 operand to share it across the
+    // batch without copying it.
+    [[nodiscard]] tensor_expr batched_matmul(tensor_expr lhs, tensor_expr rhs);
     [[nodiscard]] tensor_expr reshape(
         tensor_expr value, std::vector<index_t> shape
     );

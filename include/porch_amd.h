@@ -152,6 +152,12 @@ porch_status porch_launch_fused_reduction(
  * generalises it.  rank/dims hold the permutation: output dimension i is
  * operand dimension dims[i]. */
 #define PORCH_OP_PERMUTE 19
+/* Batched matmul: [B, M, K] @ [B, K, N] -> [B, M, N], each batch entry the
+ * rank-2 matmul's sequential fp32 sum over k.  No counterpart in the
+ * reference, whose matmul is rank-2 only (src/tensor.cpp:366-385); lhs and
+ * rhs are the operands, as for MATMUL.  A shared operand is a broadcast_to
+ * of a rank-2 tensor to [B, K, N] (a view: it is not copied). */
+#define PORCH_OP_BATCHED_MATMUL 20
 
 /* One IR node; the flattened form of tensor_expr::node, src/tensor.cpp:48-60.
  * Operands refer to earlier entries, so a node table is topologically

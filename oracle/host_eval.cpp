@@ -26,6 +26,8 @@
 //     hardware, so exp is compared within a tolerance);
 //   * matmul as s = 0.0f; for k: s += L(row*K + k) * R(k*N + col)
 //     (684-721), without FMA contraction;
+//   * batched_matmul (no reference counterpart) as that matmul for each
+//     batch entry b over L(b*M*K + ...) and R(b*K*N + ...);
 //   * every sum/max — nested ones first, as lower_nested_reductions does
 //     (964-989) — with the block-reduction order of
 //     fused_reduction_kernel_source (896-962): 256 lanes each fold the
@@ -134,6 +136,12 @@ namespace {
                             l->shape[1] != r->shape[0])
                             throw std::invalid_argument("matmul shapes");
                         n.shape = {l->shape[0], r->shape[1]};
+                        break;
+                    case PORCH_OP_BATCHED_MATMUL:
+                        if (l->shape.size() != 3 || r->shape.size() != 3 ||
+                            l->shape[0] != r->shape[0] || l->shape[2] != r->shape[1])
+                            throw std::invalid_argument("batched_matmul shapes");
+                        n.shape = {l->shape[0], l->shape[1], r->shape[2]};
                         break;
                     case PORCH_OP_SLICE:
                     case PORCH_OP_RESHAPE:
@@ -372,7 +380,7 @@ namespace {
             prepare(n.lhs);
             prepare(n.rhs);
             if (n.op == PORCH_OP_SUM || n.op == PORCH_OP_MAX) done[id] = reduce(id);
-            if (n.op == PORCH_OP_MATMUL) done[id] = matmul(id);
+            if (n.op == PORCH_OP_MATMUL || n.op == PORCH_OP_BATCHED_MATMUL) done[id] = matmul(id);
         }
 
         std::vector<float> reduce(int id) {
@@ -437,22 +445,27 @@ namespace {
             return result;
         }
 
+        // matmul, and batched_matmul as one matmul per batch entry.
         std::vector<float> matmul(int id) {
             const onode& n = nodes[id];
             const std::vector<float> a = evaluate_all(n.lhs);
             const std::vector<float> b = evaluate_all(n.rhs);
-            const int64_t M = n.shape[0];
-            const int64_t N = n.shape[1];
-            const int64_t K = nodes[n.lhs].shape[1];
-            std::vector<float> c(static_cast<size_t>(M * N), 0.0F);
+            const bool batched = n.op == PORCH_OP_BATCHED_MATMUL;
+            const int64_t batch = batched ? n.shape[0] : 1;
+            const int64_t M = n.shape[batched ? 1 : 0];
+            const int64_t N = n.shape[batched ? 2 : 1];
+            const int64_t K = nodes[n.lhs].shape[batched ? 2 : 1];
+            std::vector<float> c(static_cast<size_t>(batch * M * N), 0.0F);
             // Row i accumulates over k in order: per element exactly
             // s = 0; s += a[i,0]*b[0,j]; s += a[i,1]*b[1,j]; ...
 #pragma omp parallel for schedule(static)
-            for (int64_t i = 0; i < M; ++i) {
-                float* row = c.data() + i * N;
+            for (int64_t bi = 0; bi < batch * M; ++bi) {
+                const int64_t e = bi / (M > 0 ? M : 1);
+                const int64_t i = bi % (M > 0 ? M : 1);
+                float* row = c.data() + (e * M + i) * N;
                 for (int64_t k = 0; k < K; ++k) {
-                    const float x = a[static_cast<size_t>(i * K + k)];
-                    const float* brow = b.data() + k * N;
+                    const float x = a[static_cast<size_t>((e * M + i) * K + k)];
+                    const float* brow = b.data() + (e * K + k) * N;
                     for (int64_t j = 0; j < N; ++j) {
                         const float p = x * brow[j];
                         row[j] = row[j] + p;

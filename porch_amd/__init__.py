@@ -39,7 +39,7 @@ from ._lib import (
 
 __all__ = [
     "device", "all", "slice", "tensor", "tensor_expr", "full", "zeros", "add",
-    "subtract", "multiply", "divide", "matmul", "reshape", "unsqueeze",
+    "subtract", "multiply", "divide", "matmul", "batched_matmul", "reshape", "unsqueeze",
     "transpose", "permute", "broadcast_to", "concat", "sum", "max", "maximum", "minimum",
     "exp", "reciprocal", "materialize", "relu", "softmax", "logistic",
     "backend", "backend_kind", "backend_for", "is_backend_available",
@@ -578,6 +578,13 @@ def divide(lhs: tensor, rhs: tensor) -> tensor:
 
 def matmul(lhs, rhs) -> tensor_expr:
     return _binary("matmul", lhs, rhs)
+
+
+def batched_matmul(lhs, rhs) -> tensor_expr:
+    """[B, M, K] @ [B, K, N] -> [B, M, N]: matmul per batch entry.  An
+    extension with no counterpart in the reference, whose matmul is rank-2
+    only; broadcast_to a rank-2 operand to share it across the batch."""
+    return _binary("batched_matmul", lhs, rhs)
 
 
 def reshape(value, shape: Sequence[int]) -> tensor_expr:

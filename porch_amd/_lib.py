@@ -20,11 +20,11 @@ ERR_RUNTIME = 3
 ERR_COMPILATION = 4
 
 # Node kinds (PORCH_OP_*): the reference's expr_kind order, then this
-# backend's extensions (permute).
+# backend's extensions (permute, batched_matmul).
 OPS = (
     "input", "scalar", "add", "subtract", "multiply", "divide", "matmul",
     "slice", "reshape", "unsqueeze", "transpose", "broadcast", "concat",
-    "sum", "max", "maximum", "minimum", "exp", "reciprocal", "permute",
+    "sum", "max", "maximum", "minimum", "exp", "reciprocal", "permute", "batched_matmul",
 )
 OP = {name: i for i, name in enumerate(OPS)}
 

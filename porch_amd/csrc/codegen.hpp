@@ -100,18 +100,22 @@ namespace porch::cg {
     // reductions of at least 2^20 values over an axis of at least 256.
     int64_t column_reduce_parts(const column_reduce_request& request, int compute_units);
 
-    // C = epilogue(A @ B) with A [M,K], B [K,N] given by element strides.
+    // C = epilogue(A @ B) with A [M,K], B [K,N] given by element strides;
+    // batched: C[b] = epilogue(A[b] @ B[b]) for b < batch.
     struct gemm_operand {
         int slot = -1;
         int64_t offset = 0;
-        int64_t stride_row = 0; // A: per m, B: per k
-        int64_t stride_col = 0; // A: per k, B: per n
+        int64_t stride_row = 0;   // A: per m, B: per k
+        int64_t stride_col = 0;   // A: per k, B: per n
+        int64_t stride_batch = 0; // per batch entry (0: shared)
     };
     struct gemm_request {
         const kexpr* expr = nullptr;
+        bool batched = false;     // epilogue over (b, m, n), output [batch, m, n]
+        int64_t batch = 1;
         int64_t m = 0, n = 0, k = 0;
         gemm_operand a, b;
-        int epilogue = -1;        // kexpr over (m, n); row_value 0 = acc
+        int epilogue = -1;        // kexpr over (m, n) or (b, m, n); row_value 0 = acc
         int n_slots = 0;
         index_width width;
         int compute_units = 256;

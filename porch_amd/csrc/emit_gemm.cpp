@@ -1,9 +1,11 @@
-// Rank-2 matmul with a fused elementwise epilogue.
+// Rank-2 (and batched) matmul with a fused elementwise epilogue.
 //
 // The reference emits a per-output K loop inside the elementwise kernel
 // (reference src/tensor.cpp:684-721).  Here small products use the same
 // one-output-per-lane K loop (sequential fp32 sum, exactly the reference's
-// order), and large ones use LDS-tiled fp32 MFMA.
+// order), and large ones use LDS-tiled fp32 MFMA.  A batched product runs
+// the same kernels over (batch entry, tile) pairs, each entry's operands
+// offset by their batch strides.
 
 #include "codegen.hpp"
 #include "emit_expr.hpp"
@@ -15,8 +17,10 @@ namespace porch::cg {
     namespace {
 
         std::string operand_index(const gemm_operand& op, const std::string& row,
-                                  const std::string& col) {
+                                  const std::string& col, const std::string& batch = "") {
             std::string s = std::to_string(op.offset);
+            if (!batch.empty() && op.stride_batch != 0)
+                s += " + (idx_t)(" + batch + ") * " + std::to_string(op.stride_batch);
             s += " + (idx_t)(" + row + ") * " + std::to_string(op.stride_row);
             s += " + (idx_t)(" + col + ") * " + std::to_string(op.stride_col);
             return s;
@@ -44,25 +48,35 @@ namespace porch::cg {
             kc.name = "porch_gemm";
             kc.n_slots = r.n_slots;
             kc.block = 256;
-            const int64_t outputs = r.m * r.n;
+            const int64_t outputs = r.batch * r.m * r.n;
             kc.grid_x = static_cast<unsigned>(
                 std::clamp<int64_t>((outputs + 255) / 256, 1, int64_t{1} << 22)
             );
             const char* T = r.width.type();
-            const std::vector<std::string> names{"q0", "q1"};
+            const std::vector<std::string> names =
+                r.batched ? std::vector<std::string>{"qb", "q0", "q1"}
+                          : std::vector<std::string>{"q0", "q1"};
             std::string& s = kc.source;
             s = kernel_prologue(r.n_slots, T);
             s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" +
                  kernel_params(r.n_slots) + ") {\n";
             s += "    for (idx_t o = (idx_t)blockIdx.x * 256 + threadIdx.x; o < " +
                  std::to_string(outputs) + "; o += (idx_t)gridDim.x * 256) {\n";
-            s += "        const idx_t q0 = o / " + std::to_string(r.n) + ";\n";
+            if (r.batched) {
+                s += "        const idx_t qb = o / " + std::to_string(r.m * r.n) + ";\n";
+                s += "        const idx_t q0 = (o / " + std::to_string(r.n) + ") % " +
+                     std::to_string(r.m) + ";\n";
+            }
+            else {
+                s += "        const idx_t q0 = o / " + std::to_string(r.n) + ";\n";
+            }
             s += "        const idx_t q1 = o % " + std::to_string(r.n) + ";\n";
+            const std::string batch = r.batched ? "qb" : "";
             s += "        float acc = 0.0f;\n";
             s += "        for (idx_t kk = 0; kk < " + std::to_string(r.k) + "; ++kk) {\n";
             s += "            acc += a" + std::to_string(r.a.slot) + "[" +
-                 operand_index(r.a, "q0", "kk") + "] * a" + std::to_string(r.b.slot) + "[" +
-                 operand_index(r.b, "kk", "q1") + "];\n";
+                 operand_index(r.a, "q0", "kk", batch) + "] * a" + std::to_string(r.b.slot) + "[" +
+                 operand_index(r.b, "kk", "q1", batch) + "];\n";
             s += "        }\n";
             std::string body;
             emitter em(*r.expr, body, 1);
@@ -209,6 +223,8 @@ namespace porch::cg {
                              k_ext % 4 == 0;
             else
                 lay.vector = op.offset % 4 == 0 && stride_k % 4 == 0 && rows_ext % 4 == 0;
+            // every batch entry's base must keep the 16-byte alignment
+            lay.vector = lay.vector && op.stride_batch % 4 == 0;
             return lay;
         }
 
@@ -217,10 +233,12 @@ namespace porch::cg {
             // LDS reads per MFMA and the B re-reads; used while they still
             // give every compute unit a tile (measured 2.7% faster at 4096^3).
             const int64_t tiles_n = (r.n + BN - 1) / BN;
-            const int bm = (r.m >= 256 && ((r.m + 255) / 256) * tiles_n >= r.compute_units) ? 256 : BM;
+            const int bm =
+                (r.m >= 256 && ((r.m + 255) / 256) * tiles_n * r.batch >= r.compute_units) ? 256 : BM;
             const int ib = bm / 64; // 32-row MFMA blocks per wave
             const int64_t tiles_m = (r.m + bm - 1) / bm;
             const int64_t tiles = tiles_m * tiles_n;
+            const int64_t total = tiles * r.batch; // workgroups: (batch entry, tile) pairs
             const int64_t steps = (r.k + BK - 1) / BK;
             const operand_layout la = layout_of(r.a, true, r.m, r.k);
             const operand_layout lb = layout_of(r.b, false, r.n, r.k);
@@ -231,7 +249,7 @@ namespace porch::cg {
             kc.name = "porch_gemm";
             kc.n_slots = r.n_slots;
             kc.block = 256;
-            kc.grid_x = static_cast<unsigned>(tiles);
+            kc.grid_x = static_cast<unsigned>(total);
             const char* T = r.width.type();
             std::string& s = kc.source;
             s = kernel_prologue(r.n_slots, T);
@@ -250,21 +268,32 @@ namespace porch::cg {
             s += "    const int wm = wave >> 1;\n    const int wn = wave & 1;\n";
             // Workgroups are dispatched round-robin over the 8 XCDs; give
             // each XCD a contiguous band of tile rows so its L2 holds them.
-            if (tiles % 8 == 0) {
-                s += "    const int tile = (blockIdx.x % 8) * " + std::to_string(tiles / 8) +
+            // (For a batched product the bands run over (entry, tile) pairs,
+            // entry-major, so an XCD holds whole entries where it can.)
+            const std::string lin = r.batched ? "lin" : "tile";
+            if (total % 8 == 0) {
+                s += "    const int " + lin + " = (blockIdx.x % 8) * " + std::to_string(total / 8) +
                      " + blockIdx.x / 8;\n";
             }
             else {
-                s += "    const int tile = blockIdx.x;\n";
+                s += "    const int " + lin + " = blockIdx.x;\n";
+            }
+            if (r.batched) {
+                s += "    const idx_t qb = lin / " + std::to_string(tiles) + ";\n";
+                s += "    const int tile = lin % " + std::to_string(tiles) + ";\n";
             }
             s += "    const idx_t m0 = (idx_t)(tile / " + std::to_string(tiles_n) + ") * " +
                  std::to_string(bm) + ";\n";
             s += "    const idx_t n0 = (idx_t)(tile % " + std::to_string(tiles_n) + ") * " +
                  std::to_string(BN) + ";\n";
-            s += "    const float* __restrict__ A = a" + std::to_string(r.a.slot) + " + " +
-                 std::to_string(r.a.offset) + ";\n";
-            s += "    const float* __restrict__ B = a" + std::to_string(r.b.slot) + " + " +
-                 std::to_string(r.b.offset) + ";\n";
+            auto base = [&r](const gemm_operand& op) {
+                std::string b = "a" + std::to_string(op.slot) + " + " + std::to_string(op.offset);
+                if (r.batched && op.stride_batch != 0)
+                    b += " + qb * " + std::to_string(op.stride_batch);
+                return b;
+            };
+            s += "    const float* __restrict__ A = " + base(r.a) + ";\n";
+            s += "    const float* __restrict__ B = " + base(r.b) + ";\n";
             s += "    float rA[" + std::to_string(4 * (bm / 64)) + "];\n    float rB[8];\n";
             s += "    floatx16 acc[" + IB + "][2];\n";
             s += "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n";
@@ -340,11 +369,17 @@ namespace porch::cg {
             emitter em(*r.expr, body, 1);
             em.indent = "            ";
             em.declare_roots({r.epilogue});
-            const std::vector<std::string> names{"q0", "q1"};
+            const std::vector<std::string> names =
+                r.batched ? std::vector<std::string>{"qb", "q0", "q1"}
+                          : std::vector<std::string>{"q0", "q1"};
             epilogue_emitter(em, r, names, "acc_v");
             const std::string v = em.emit(r.epilogue)[0];
             s += body;
-            s += "            out[q0 * " + std::to_string(r.n) + " + q1] = " + v + ";\n";
+            if (r.batched)
+                s += "            out[(qb * " + std::to_string(r.m) + " + q0) * " + std::to_string(r.n) +
+                     " + q1] = " + v + ";\n";
+            else
+                s += "            out[q0 * " + std::to_string(r.n) + " + q1] = " + v + ";\n";
             s += "        }\n    }\n}\n";
             return kc;
         }
@@ -354,7 +389,7 @@ namespace porch::cg {
     kernel_code emit_gemm(const gemm_request& r) {
         // Small products keep the reference's sequential K loop (their
         // launch is latency-bound anyway); large ones use MFMA.
-        if (r.m * r.n * r.k < (int64_t{1} << 18) || r.m < 32 || r.n < 32)
+        if (r.batch * r.m * r.n * r.k < (int64_t{1} << 18) || r.m < 32 || r.n < 32)
             return emit_gemm_scalar(r);
         return emit_gemm_mfma(r);
     }

@@ -121,7 +121,8 @@ namespace porch::ir {
                 return static_cast<int>(index);
             };
             const bool binary = is_elementwise_binary(n.kind) ||
-                                n.kind == op::matmul || n.kind == op::concat;
+                                n.kind == op::matmul || n.kind == op::batched_matmul ||
+                                n.kind == op::concat;
             const bool unary = !binary && n.kind != op::input &&
                                n.kind != op::scalar;
             n.lhs = (binary || unary) ? operand(c.lhs) : -1;
@@ -238,6 +239,29 @@ namespace porch::ir {
                         );
                     }
                     n.out = {lhs->out[0], rhs->out[1]};
+                    return;
+                case op::batched_matmul:
+                    if (lhs->is_scalar || rhs->is_scalar) {
+                        throw std::invalid_argument(
+                            "batched_matmul operands must be tensors"
+                        );
+                    }
+                    if (lhs->out.size() != 3 || rhs->out.size() != 3) {
+                        throw std::invalid_argument(
+                            "batched_matmul requires rank-3 tensors"
+                        );
+                    }
+                    if (lhs->out[0] != rhs->out[0]) {
+                        throw std::invalid_argument(
+                            "batched_matmul batch dimensions must match"
+                        );
+                    }
+                    if (lhs->out[2] != rhs->out[1]) {
+                        throw std::invalid_argument(
+                            "batched_matmul inner dimensions must match"
+                        );
+                    }
+                    n.out = {lhs->out[0], lhs->out[1], rhs->out[2]};
                     return;
                 case op::slice: {
                     if (n.strides.size() != n.shape.size()) {

@@ -35,9 +35,10 @@ namespace porch::ir {
         exp = PORCH_OP_EXP,
         reciprocal = PORCH_OP_RECIPROCAL,
         permute = PORCH_OP_PERMUTE,
+        batched_matmul = PORCH_OP_BATCHED_MATMUL,
     };
 
-    constexpr int op_count = 20;
+    constexpr int op_count = 21;
 
     struct node {
         op kind = op::input;

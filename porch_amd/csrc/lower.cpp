@@ -467,6 +467,7 @@ namespace porch::cg {
             case ir::op::sum:
             case ir::op::max:
             case ir::op::matmul:
+            case ir::op::batched_matmul:
                 throw std::logic_error(
                     "reduction or matmul reached the pointwise lowering"
                 );

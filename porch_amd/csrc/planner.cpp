@@ -17,8 +17,12 @@ namespace porch::plan {
                    kind == ir::op::reciprocal;
         }
 
+        bool is_product(ir::op kind) {
+            return kind == ir::op::matmul || kind == ir::op::batched_matmul;
+        }
+
         bool is_boundary(ir::op kind) {
-            return ir::is_reduction(kind) || kind == ir::op::matmul;
+            return ir::is_reduction(kind) || is_product(kind);
         }
 
         struct builder {
@@ -109,15 +113,16 @@ namespace porch::plan {
             // gemm
             // ---------------------------------------------------------
             int epilogue_matmul(int id) {
-                // The single matmul reached from `id` through elementwise
-                // nodes only (so the epilogue runs at the matmul's (m, n)).
+                // The single matmul (or batched matmul) reached from `id`
+                // through elementwise nodes only (so the epilogue runs at
+                // the product's own coordinates).
                 std::set<int> found;
                 std::set<int> seen;
                 std::function<void(int)> walk = [&](int x) {
                     if (x < 0 || seen.count(x) || temp_of.count(x)) return;
                     seen.insert(x);
                     const ir::node& n = g.at(x);
-                    if (n.kind == ir::op::matmul) {
+                    if (is_product(n.kind)) {
                         found.insert(x);
                         return;
                     }
@@ -162,10 +167,25 @@ namespace porch::plan {
                 return false;
             }
 
-            cg::gemm_operand operand(int id, int64_t rows, int64_t cols) {
+            // Operand `id` of shape [rows, cols] or [batch, rows, cols]: a
+            // strided view read in place, or a materialised temporary.
+            // Whether node `id` reads node `target` (directly or not).
+            bool depends_on(int id, int target) const {
+                std::set<int> seen;
+                std::function<bool(int)> walk = [&](int x) {
+                    if (x < 0 || !seen.insert(x).second) return false;
+                    if (x == target) return true;
+                    const ir::node& n = g.at(x);
+                    return walk(n.lhs) || walk(n.rhs);
+                };
+                return walk(id);
+            }
+
+            cg::gemm_operand operand(int id, const std::vector<int64_t>& shape) {
+                const size_t rank = shape.size();
                 if (pure_view_of_input(id)) {
                     cg::kexpr k;
-                    cg::lowering low(g, k, {rows, cols});
+                    cg::lowering low(g, k, shape);
                     bind_inputs(low);
                     const int root = low.at(id, low.identity());
                     const cg::knode& n = k.at(root);
@@ -173,8 +193,9 @@ namespace porch::plan {
                         cg::gemm_operand op;
                         op.slot = n.slot;
                         op.offset = n.index.c0;
-                        op.stride_row = n.index.w[0];
-                        op.stride_col = n.index.w[1];
+                        op.stride_batch = rank == 3 ? n.index.w[0] : 0;
+                        op.stride_row = n.index.w[rank - 2];
+                        op.stride_col = n.index.w[rank - 1];
                         return op;
                     }
                 }
@@ -182,7 +203,8 @@ namespace porch::plan {
                 cg::gemm_operand op;
                 op.slot = g.n_inputs + t.index;
                 op.offset = 0;
-                op.stride_row = cols;
+                op.stride_batch = rank == 3 ? shape[1] * shape[2] : 0;
+                op.stride_row = shape[rank - 1];
                 op.stride_col = 1;
                 return op;
             }
@@ -191,21 +213,34 @@ namespace porch::plan {
                 const int mm = epilogue_matmul(id);
                 if (mm < 0) return false;
                 const ir::node& m = g.at(mm);
-                const int64_t M = g.at(m.lhs).out[0];
-                const int64_t K = g.at(m.lhs).out[1];
-                const int64_t N = g.at(m.rhs).out[1];
+                const std::vector<int64_t>& ls = g.at(m.lhs).out;
+                const std::vector<int64_t>& rs = g.at(m.rhs).out;
+                const bool batched = m.kind == ir::op::batched_matmul;
+                const size_t o = batched ? 1 : 0; // leading batch axis
+                const int64_t M = ls[o];
+                const int64_t K = ls[o + 1];
+                const int64_t N = rs[o + 1];
                 cg::gemm_request r;
+                r.batched = batched;
+                r.batch = batched ? ls[0] : 1;
                 r.m = M;
                 r.n = N;
                 r.k = K;
-                r.a = operand(m.lhs, M, K);
-                r.b = operand(m.rhs, K, N);
+                r.a = operand(m.lhs, ls);
+                r.b = operand(m.rhs, rs);
                 // Other boundaries in the epilogue region.
                 std::set<int> others;
                 boundaries(id, others, {mm}, true);
+                // A boundary that reads the product itself (softmax over a
+                // product: its row max and sum) needs the product
+                // materialised anyway; an epilogue would compute it a second
+                // time.  Leave the region to the row or pointwise paths,
+                // which read that one temporary.
+                for (const int b : others)
+                    if (depends_on(b, mm)) return false;
                 for (const int b : others) ensure_temp(b);
                 cg::kexpr k;
-                cg::lowering low(g, k, {M, N});
+                cg::lowering low(g, k, m.out);
                 bind_inputs(low);
                 cg::binding acc;
                 acc.what = cg::binding::kind::row_value;
@@ -239,7 +274,7 @@ namespace porch::plan {
                 // the row value.
                 if (!seen.insert({id, elementwise_path}).second) return true;
                 const ir::node& n = g.at(id);
-                if (n.kind == ir::op::matmul) return true; // materialised
+                if (is_product(n.kind)) return true; // materialised
                 if (ir::is_reduction(n.kind)) return false; // not via broadcast
                 if (n.kind == ir::op::broadcast && elementwise_path &&
                     n.out == row_shape) {
@@ -292,7 +327,7 @@ namespace porch::plan {
                     boundaries(producer, all, {}, false);
                     for (const int r : reductions) boundaries(g.at(r).lhs, all, {}, false);
                     for (const int b : all) {
-                        if (g.at(b).kind == ir::op::matmul) mms.insert(b);
+                        if (is_product(g.at(b).kind)) mms.insert(b);
                         else if (!reductions.count(b)) return false;
                     }
                 }

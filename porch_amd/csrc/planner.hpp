@@ -6,7 +6,8 @@
 // per-launch module loading (src/cuda_jit.cpp:789-948).
 //
 // A graph is split into the fewest kernels the kernel classes allow:
-//   1. an elementwise region over exactly one matmul -> gemm with epilogue;
+//   1. an elementwise region over exactly one matmul (or batched matmul)
+//      -> gemm with epilogue;
 //   2. a region whose reductions all run along the last axis of one row
 //      space and are consumed through broadcasts -> one row program
 //      (softmax, normalisations, a root reduction over the last axis);

@@ -559,6 +559,9 @@ namespace porch {
     tensor_expr matmul(tensor_expr lhs, tensor_expr rhs) {
         return binary(ir::op::matmul, lhs, rhs);
     }
+    tensor_expr batched_matmul(tensor_expr lhs, tensor_expr rhs) {
+        return binary(ir::op::batched_matmul, lhs, rhs);
+    }
     tensor_expr reshape(tensor_expr value, std::vector<index_t> shape) {
         return with_shape(ir::op::reshape, value, std::move(shape));
     }

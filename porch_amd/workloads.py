@@ -14,6 +14,14 @@ porch_amd.synth):
                                          bias ~ N(0,.01) [1,4096]
 and `copy`, reshape(x) over x [8192,8192]: a plain copy of known size used to
 calibrate hardware byte counters.
+
+Three more measure the IR extensions (permute, batched_matmul):
+  batched_transpose  permute(x, [0, 2, 1])  x ~ U[-1,1] [64,512,512]
+  heads_permute      permute(x, [0, 2, 1, 3])
+                                         x ~ U[-1,1] [32,1024,16,128]
+  batched_matmul     relu(batched_matmul(A, B) + bias) - 0.5
+                                         A, B ~ U(-1,1)/32 [32,1024,1024],
+                                         bias ~ N(0,.01) [1,1,1024]
 """
 
 from __future__ import annotations
@@ -45,6 +53,13 @@ def config_inputs(name: str, size: dict | None = None) -> list[np.ndarray]:
                 synth.normal(cols, 403, 0.0, 0.1)]
     if name == "copy":
         return [synth.uniform(s["n"] * s["n"], 601, -1.0, 1.0)]
+    if name in ("batched_transpose", "heads_permute"):
+        return [synth.uniform(int(np.prod(config_shapes(name, size)[0])), 701, -1.0, 1.0)]
+    if name == "batched_matmul":
+        b, m, k, n = s["batch"], s["m"], s["k"], s["n"]
+        return [synth.uniform(b * m * k, 801, -1.0, 1.0) / np.float32(32.0),
+                synth.uniform(b * k * n, 802, -1.0, 1.0) / np.float32(32.0),
+                synth.normal(n, 803, 0.0, 0.01)]
     if name == "matmul_epilogue":
         m, k, n = s["m"], s["k"], s["n"]
         return [synth.uniform(m * k, 501, -1.0, 1.0) / np.float32(64.0),
@@ -60,6 +75,9 @@ CONFIG_SIZES = {
     "logistic_rowsum": {"rows": 16384, "cols": 2048},
     "matmul_epilogue": {"m": 4096, "k": 4096, "n": 4096},
     "copy": {"n": 8192},
+    "batched_transpose": {"batch": 64, "rows": 512, "cols": 512},
+    "heads_permute": {"batch": 32, "seq": 1024, "heads": 16, "dim": 128},
+    "batched_matmul": {"batch": 32, "m": 1024, "k": 1024, "n": 1024},
 }
 
 
@@ -78,6 +96,13 @@ def config_shapes(name: str, size: dict | None = None) -> list[list[int]]:
         return [[s["m"], s["k"]], [s["k"], s["n"]], [1, s["n"]]]
     if name == "copy":
         return [[s["n"], s["n"]]]
+    if name == "batched_transpose":
+        return [[s["batch"], s["rows"], s["cols"]]]
+    if name == "heads_permute":
+        return [[s["batch"], s["seq"], s["heads"], s["dim"]]]
+    if name == "batched_matmul":
+        b, m, k, n = s["batch"], s["m"], s["k"], s["n"]
+        return [[b, m, k], [b, k, n], [1, 1, n]]
     raise ValueError(name)
 
 
@@ -109,4 +134,14 @@ def config_graph(name: str, tensors, size: dict | None = None):
     if name == "copy":
         (x,) = tensors
         return porch.reshape(x, [s["n"] * s["n"]])
+    if name == "batched_transpose":
+        (x,) = tensors
+        return porch.permute(x, [0, 2, 1])
+    if name == "heads_permute":
+        (x,) = tensors
+        return porch.permute(x, [0, 2, 1, 3])
+    if name == "batched_matmul":
+        a, b, bias = tensors
+        shape = [s["batch"], s["m"], s["n"]]
+        return porch.relu(porch.batched_matmul(a, b) + porch.broadcast_to(bias, shape)) - 0.5
     raise ValueError(name)

@@ -1,0 +1,191 @@
+"""batched_matmul: [B, M, K] @ [B, K, N] -> [B, M, N] (an extension; the
+reference's matmul is rank-2 only, src/tensor.cpp:366-385).
+
+The oracle's batched product is pinned against numpy's matmul on integer
+data (every sum exact in binary32, so order-free), against the oracle's own
+rank-2 matmul (the reference's per-element k order) entry by entry, and by a
+planted mistake (one entry's operand reused for all).  The planner tests pin
+that strided, permuted and broadcast (shared) operands are read in place and
+which kernel class each size reaches; the GPU tests check the MFMA and
+scalar kernels bit-exact on integer data and within a float64-derived bound
+on real-valued data.
+"""
+
+import numpy as np
+import pytest
+
+import porch_amd as porch
+from oracle import host
+from tests.helpers import placeholder
+
+
+def ints(shape, rng, lo=-3, hi=4):
+    return rng.integers(lo, hi, size=shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 5, 3), (3, 5, 7, 4), (6, 17, 33, 9), (2, 8, 0, 5)])
+def test_oracle_matches_numpy(shape):
+    b, m, k, n = shape
+    rng = np.random.default_rng(sum(shape))
+    x, y = ints([b, m, k], rng), ints([b, k, n], rng)
+    out = host.evaluate(porch.batched_matmul(placeholder([b, m, k], x), placeholder([b, k, n], y)))
+    assert out.shape == (b, m, n)
+    assert np.array_equal(out, np.matmul(x.astype(np.float64), y.astype(np.float64)).astype(np.float32))
+
+
+def test_oracle_entries_equal_rank_two_matmul_bit_for_bit():
+    # real-valued data: each entry must follow the rank-2 matmul's k order
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((4, 9, 50)).astype(np.float32)
+    y = rng.standard_normal((4, 50, 7)).astype(np.float32)
+    out = host.evaluate(porch.batched_matmul(placeholder([4, 9, 50], x), placeholder([4, 50, 7], y)))
+    for e in range(4):
+        ref = host.evaluate(porch.matmul(placeholder([9, 50], x[e]), placeholder([50, 7], y[e])))
+        assert np.array_equal(out[e].view(np.uint32), ref.view(np.uint32)), e
+
+
+def test_oracle_planted_mistake_is_caught():
+    # every entry multiplied by entry 0's right operand: numpy disagrees
+    rng = np.random.default_rng(5)
+    x, y = ints([3, 4, 6], rng), ints([3, 6, 5], rng)
+    wrong = host.evaluate(porch.batched_matmul(
+        placeholder([3, 4, 6], x), porch.broadcast_to(placeholder([1, 6, 5], y[:1]), [3, 6, 5])))
+    assert not np.array_equal(wrong, np.matmul(x, y))
+
+
+@pytest.mark.parametrize("lhs, rhs, message", [
+    ([2, 3, 4], [3, 4, 5], "batched_matmul batch dimensions must match"),
+    ([2, 3, 4], [2, 5, 6], "batched_matmul inner dimensions must match"),
+    ([3, 4], [4, 5], "batched_matmul requires rank-3 tensors"),
+    ([2, 3, 4], [4, 5], "batched_matmul requires rank-3 tensors"),
+])
+def test_shape_errors(lhs, rhs, message):
+    with pytest.raises(porch.InvalidArgument, match=message):
+        porch.batched_matmul(placeholder(lhs), placeholder(rhs)).shape()
+
+
+def test_scalar_operand_is_rejected():
+    with pytest.raises(porch.InvalidArgument, match="batched_matmul operands must be tensors"):
+        porch.batched_matmul(placeholder([2, 3, 4]), 2.0).shape()
+
+
+def test_rank_two_matmul_still_rejects_rank_three():
+    # the reference's own rule for matmul is unchanged
+    with pytest.raises(porch.InvalidArgument, match="matmul requires rank-2 tensors"):
+        porch.matmul(placeholder([2, 3, 4]), placeholder([2, 4, 5])).shape()
+
+
+def plain(make, b, m, k, n):
+    return porch.batched_matmul(make([b, m, k]), make([b, k, n]))
+
+
+def with_epilogue(make, b, m, k, n):
+    bias = porch.broadcast_to(make([1, 1, n]), [b, m, n])
+    return porch.relu(porch.batched_matmul(make([b, m, k]), make([b, k, n])) + bias) - 0.5
+
+
+def shared_weight(make, b, m, k, n):
+    # one [k, n] weight for every entry: a broadcast view, batch stride 0
+    return porch.batched_matmul(make([b, m, k]), porch.broadcast_to(make([k, n]), [b, k, n]))
+
+
+def permuted_operands(make, b, m, k, n):
+    # A stored [m, b, k] (heads interleaved), B stored [b, n, k] (transposed)
+    a = porch.permute(make([m, b, k]), [1, 0, 2])
+    bt = porch.permute(make([b, n, k]), [0, 2, 1])
+    return porch.batched_matmul(a, bt) * 2.0
+
+
+def expression_operand(make, b, m, k, n):
+    # an operand that is itself arithmetic: materialised first
+    return porch.batched_matmul(make([b, m, k]) * 2.0 - 1.0, make([b, k, n]))
+
+
+def attention_scores(make, b, m, k, n):
+    # softmax over the last axis of a batched product (row program after gemm)
+    return porch.softmax(porch.batched_matmul(make([b, m, k]), make([b, k, n])) * 0.125, 2)
+
+
+FORMS = {
+    "plain": plain,
+    "with_epilogue": with_epilogue,
+    "shared_weight": shared_weight,
+    "permuted_operands": permuted_operands,
+    "expression_operand": expression_operand,
+}
+
+SIZES = [(4, 256, 256, 256), (3, 130, 70, 200), (8, 64, 300, 130), (2, 33, 17, 40), (1, 96, 64, 160),
+         (5, 1, 40, 64)]
+
+
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_forms_plan_and_compile(form):
+    for size in SIZES:
+        plan = porch.plan(FORMS[form](placeholder, *size), compile=True)
+        kinds = [k["kind"] for k in plan["kernels"]]
+        assert kinds[-1] in ("gemm.mfma", "gemm.scalar"), (form, size, plan)
+        if form == "expression_operand":
+            assert len(kinds) == 2 and kinds[0].startswith("pointwise"), (size, plan)
+        else:
+            assert len(kinds) == 1, (form, size, plan)  # operands read in place
+
+
+def test_large_products_use_mfma_over_every_entry():
+    plan = porch.plan(plain(placeholder, 16, 512, 64, 512))
+    (kernel,) = plan["kernels"]
+    assert kernel["kind"] == "gemm.mfma"
+    assert kernel["grid"][0] == 16 * 4 * 4  # (entry, 128x128 tile) pairs
+
+
+def test_shared_weight_has_no_batch_offset():
+    source = porch.kernel_source(shared_weight(placeholder, 4, 256, 256, 256), 0)
+    assert "const float* __restrict__ B = a1 + 0;" in source
+    assert "const float* __restrict__ A = a0 + 0 + qb * 65536;" in source
+
+
+def test_softmax_over_product_forms_gemm_then_row():
+    kinds = [k["kind"] for k in porch.plan(attention_scores(placeholder, 4, 128, 64, 128))["kernels"]]
+    assert kinds == ["gemm.mfma", "row"]
+
+
+@pytest.mark.gpu
+def test_batched_forms_bit_exact_on_integers(gpu):
+    rng = np.random.default_rng(8)
+
+    def make(shape):
+        return gpu.tensor(list(shape), ints(shape, rng).reshape(-1))
+
+    for form in sorted(FORMS):
+        for size in SIZES:
+            print("batched case", form, size, flush=True)
+            expr = FORMS[form](make, *size)
+            ref = host.evaluate(expr)
+            out = gpu.materialize(expr).cpu().reshape(expr.shape())
+            assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (form, size)
+
+
+@pytest.mark.gpu
+def test_batched_real_values_within_float64_bound(gpu):
+    rng = np.random.default_rng(9)
+    b, m, k, n = 6, 384, 512, 320
+    x = rng.uniform(-1, 1, size=(b, m, k)).astype(np.float32)
+    y = rng.uniform(-1, 1, size=(b, k, n)).astype(np.float32)
+    out = gpu.materialize(porch.batched_matmul(gpu.tensor([b, m, k], x.reshape(-1)),
+                                               gpu.tensor([b, k, n], y.reshape(-1)))).cpu().reshape(b, m, n)
+    exact = np.matmul(x.astype(np.float64), y.astype(np.float64))
+    # |sum error| <= k * eps * sum |x||y| for any summation order
+    bound = k * np.finfo(np.float32).eps * np.matmul(np.abs(x).astype(np.float64), np.abs(y).astype(np.float64))
+    assert np.all(np.abs(out - exact) <= bound)
+
+
+@pytest.mark.gpu
+def test_softmax_of_batched_scores(gpu):
+    rng = np.random.default_rng(10)
+
+    def make(shape):
+        return gpu.tensor(list(shape), ints(shape, rng).reshape(-1))
+
+    expr = attention_scores(make, 4, 128, 64, 128)
+    ref = host.evaluate(expr)
+    out = gpu.materialize(expr).cpu().reshape(expr.shape())
+    np.testing.assert_allclose(out, ref, rtol=2e-6, atol=1e-7)

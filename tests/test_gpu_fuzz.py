@@ -1,8 +1,8 @@
 """Seeded random graphs mixing every kind of region the planner forms:
 views (permutes included), concat, broadcasts, elementwise arithmetic, sum/max reductions over
 any axis (fused into row programs, column reductions, or materialised
-temporaries), and matmuls whose operands are expressions and whose results
-feed further ops.
+temporaries), and matmuls and batched matmuls whose operands are expressions
+and whose results feed further ops.
 
 Leaves hold small integers and the graphs are sized so every intermediate
 stays far below 2^24: sums, maxima and matmul accumulations are then exact in
@@ -86,6 +86,13 @@ def random_graph(rng, make):
                 expr = porch.matmul(leaf([n, shape[0]]), expr)
             if rng.integers(0, 2):  # an epilogue over the product
                 expr = porch.relu(expr + porch.broadcast_to(leaf([1, expr.shape()[1]]), expr.shape())) - 1.0
+        elif kind == 9 and rank == 3 and matmuls < 2:
+            matmuls += 1
+            n = int(rng.integers(1, 70))
+            other = leaf([shape[0], shape[2], n])
+            if rng.integers(0, 2):  # a weight shared by every entry
+                other = porch.broadcast_to(leaf([shape[2], n]), [shape[0], shape[2], n])
+            expr = porch.batched_matmul(expr, other)
         elif kind == 10:
             expr = expr + leaf(shape) * 2.0
         else:

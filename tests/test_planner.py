@@ -83,6 +83,17 @@ def test_matmul_read_through_a_view_is_not_fused_as_epilogue():
     assert len(plan["temps"]) == 1
 
 
+def test_product_read_by_reductions_is_computed_once():
+    # softmax over a product: one gemm into a temporary, one row program
+    # (not a second gemm recomputing the product in an epilogue)
+    m = porch.matmul(placeholder([256, 64]), placeholder([64, 256]))
+    plan = porch.plan(porch.softmax(m * 0.125, 1))
+    assert [k["kind"] for k in plan["kernels"]] == ["gemm.mfma", "row"]
+    # a column reduction of the product beside it: also one gemm
+    plan = porch.plan(m - porch.broadcast_to(porch.sum(m, 0, True), [256, 256]))
+    assert [k["kind"] for k in plan["kernels"]].count("gemm.mfma") == 1
+
+
 def test_transposed_operand_feeds_gemm_without_copy():
     a = placeholder([64, 32])
     b = placeholder([64, 48])
