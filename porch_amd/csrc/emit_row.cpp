@@ -249,9 +249,9 @@ namespace porch::cg {
             }
             return true;
         };
-        // Large outputs are written with non-temporal stores: they would
-        // only evict the kernel's own streaming inputs from L2 and MALL.
-        const bool stream_output = !r.reduce_output && ir::numel(r.shape) * 4 >= (int64_t{64} << 20);
+        // Outputs use ordinary stores: with non-temporal loads already
+        // keeping the inputs out of the way, non-temporal stores measured
+        // 3-5% slower on softmax [8192, 4096] (A/B in one process).
 
         auto load_text = [&](emitter& em, int id) {
             const knode& n = k.at(id);
@@ -462,11 +462,7 @@ namespace porch::cg {
             auto em = make_emitter(body, out_pass);
             const std::vector<std::string> v = em->emit(r.output);
             const std::string base = "row * " + std::to_string(length) + " + " + qc;
-            if (width == 4 && stream_output) {
-                em->line("__builtin_nontemporal_store((porch_v4f){" + v[0] + ", " + v[1] + ", " + v[2] +
-                         ", " + v[3] + "}, reinterpret_cast<porch_v4f*>(out + " + base + "));");
-            }
-            else if (width == 4) {
+            if (width == 4) {
                 em->line("*reinterpret_cast<float4*>(out + " + base + ") = make_float4(" + v[0] +
                          ", " + v[1] + ", " + v[2] + ", " + v[3] + ");");
             }

@@ -155,7 +155,7 @@ def test_permute_cases_plan_and_compile(name):
 
 def test_kept_inner_axis_streams_with_vector_loads():
     source = porch.kernel_source(heads_split(placeholder), 0)
-    assert "reinterpret_cast<const float4*>(a0" in source
+    assert "__builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0" in source
 
 
 @pytest.mark.gpu

@@ -31,10 +31,20 @@ def test_softmax_reads_the_row_once():
     x = placeholder([8192, 4096])
     source = porch.kernel_source(porch.softmax(x, 1))
     # one 128-bit (non-temporal: read once) load per column chunk, in the
-    # first pass only, and non-temporal 128-bit stores of the 128 MiB result
+    # first pass only, and 128-bit stores of the result
     assert source.count("__builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0") == 1
-    assert source.count("__builtin_nontemporal_store(") == 1
+    assert source.count("*reinterpret_cast<float4*>(out + ") == 1
     assert len(re.findall(r"\bexpf\(", source)) == 4  # one pass, four lanes
+
+
+def test_flat_kernel_streams_leaves_read_once():
+    # each element of x is read once: non-temporal; the broadcast row w is
+    # re-read by every row: an ordinary (cached) 128-bit load
+    x = placeholder([64, 2048])
+    w = placeholder([1, 2048])
+    source = porch.kernel_source(x * porch.broadcast_to(w, [64, 2048]), 0)
+    assert "__builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0 + " in source
+    assert "*reinterpret_cast<const float4*>(a1 + " in source
 
 
 def test_shared_reductions_are_materialised_once():
