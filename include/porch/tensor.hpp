@@ -116,6 +116,16 @@ namespace porch {
             std::vector<index_t> shape, std::vector<float32_t> values,
             cuda_jit::device_buffer device_values, device placement = device{}
         );
+        // A realised tensor over existing device storage, read through
+        // `layout` (element strides, possibly zero, and an offset).  An
+        // extension: the reference rejects non-contiguous storage
+        // (src/tensor.cpp:1193-1197).  The storage is shared, not copied;
+        // expressions read it in place, and data() gathers the values in
+        // row-major order on the device.
+        tensor(
+            tensor_layout layout, cuda_jit::device_buffer storage,
+            device placement = device{}
+        );
 
         [[nodiscard]] std::span<const index_t> shape() const noexcept;
         [[nodiscard]] std::span<const index_t> strides() const noexcept;

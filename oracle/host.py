@@ -67,7 +67,7 @@ def evaluate(expression, host_inputs=None) -> np.ndarray:
 
     nodes, dims, n_dims, inputs, _ = porch.serialize(expression)
     if host_inputs is None:
-        host_inputs = [t.data() for t in inputs]
+        host_inputs = [t._storage_values() for t in inputs]
     shape = porch.tensor_expr(expression).shape() if not isinstance(expression, porch.tensor) \
         else list(expression.shape())
     return evaluate_table(nodes, dims, n_dims, host_inputs, shape)

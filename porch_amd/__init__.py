@@ -38,7 +38,7 @@ from ._lib import (
 )
 
 __all__ = [
-    "device", "all", "slice", "tensor", "tensor_expr", "full", "zeros", "add",
+    "device", "all", "slice", "tensor", "tensor_layout", "tensor_expr", "full", "zeros", "add",
     "subtract", "multiply", "divide", "matmul", "batched_matmul", "reshape", "unsqueeze",
     "transpose", "permute", "broadcast_to", "concat", "sum", "max", "maximum", "minimum",
     "exp", "reciprocal", "materialize", "relu", "softmax", "logistic",
@@ -231,7 +231,8 @@ def serialize(root: "_Node | tensor_expr"):
                 slot_of[key] = len(inputs)
                 inputs.append(t)
             c.input = slot_of[key]
-            shape = list(t.shape())
+            # strided storage enters as its flat span, read through a slice
+            shape = list(t.shape()) if t.is_contiguous() else [t._state.layout.span()]
         c.rank = len(shape)
         c.dims = len(dims)
         dims.extend(shape)
@@ -265,7 +266,8 @@ def _infer(root: _Node):
 
 
 class _State:
-    __slots__ = ("shape", "placement", "storage", "expression", "lock", "__weakref__")
+    __slots__ = ("shape", "placement", "storage", "expression", "lock", "layout", "dense",
+                 "__weakref__")
 
     def __init__(self, shape: Sequence[int], placement: device):
         self.shape = tuple(int(e) for e in shape)
@@ -273,6 +275,8 @@ class _State:
         self.storage: _Storage | None = None
         self.expression: _Node | None = None
         self.lock = threading.Lock()
+        self.layout: tensor_layout | None = None  # strided storage; None: contiguous
+        self.dense: tensor | None = None          # strided: row-major copy for data()
 
     def realized(self) -> _Storage:
         storage = self.storage
@@ -302,18 +306,80 @@ def _checked_numel(shape: Sequence[int]) -> int:
     return count
 
 
+class tensor_layout:  # noqa: N801 - porch's spelling
+    """porch::tensor_layout: shape, element strides and storage offset, with
+    the reference's checks (src/tensor.cpp:1089-1116)."""
+
+    __slots__ = ("_shape", "_strides", "_offset")
+
+    def __init__(self, shape: Sequence[int], strides: Sequence[int] | None = None,
+                 storage_offset: int = 0):
+        self._shape = tuple(int(e) for e in shape)
+        if strides is None:
+            self._strides = _contiguous_strides(self._shape)
+            self._offset = 0
+        else:
+            self._strides = tuple(int(e) for e in strides)
+            self._offset = int(storage_offset)
+            if len(self._strides) != len(self._shape):
+                raise InvalidArgument("tensor layout rank mismatch")
+            if self._offset < 0:
+                raise InvalidArgument("tensor layout offset must be non-negative")
+            if any(st < 0 for st in self._strides):
+                raise InvalidArgument("tensor layout strides must be non-negative")
+        _checked_numel(self._shape)
+
+    def shape(self) -> tuple[int, ...]:
+        return self._shape
+
+    def strides(self) -> tuple[int, ...]:
+        return self._strides
+
+    def storage_offset(self) -> int:
+        return self._offset
+
+    def rank(self) -> int:
+        return len(self._shape)
+
+    def numel(self) -> int:
+        return _checked_numel(self._shape)
+
+    def is_contiguous(self) -> bool:
+        return self._offset == 0 and self._strides == _contiguous_strides(self._shape)
+
+    def span(self) -> int:
+        """Floats of storage the layout reaches."""
+        if self.numel() == 0:
+            return 0
+        return self._offset + builtins.sum((e - 1) * st for e, st in zip(self._shape, self._strides)) + 1
+
+
 class tensor:  # noqa: N801 - porch's spelling
     """porch::tensor: a shared handle to realized or pending values.
 
     tensor(shape, values, placement=device()) uploads host values;
     tensor(expr) records a pending expression (the reference's implicit
-    tensor_expr -> tensor conversion) that materialises once on first use.
+    tensor_expr -> tensor conversion) that materialises once on first use;
+    tensor(layout, storage, placement=device()) reads existing device storage
+    (a device_data() buffer) through a strided layout, an extension: the
+    reference rejects non-contiguous storage (src/tensor.cpp:1193-1197).
     """
 
     __slots__ = ("_state",)
 
     def __init__(self, shape, values=None, placement: device | None = None):
         placement = placement if placement is not None else device()
+        if isinstance(shape, tensor_layout):
+            layout, buffer = shape, values
+            if not isinstance(buffer, _Buffer):
+                raise InvalidArgument("strided tensors take a device buffer as storage")
+            if buffer.size_bytes() < layout.span() * 4:
+                raise InvalidArgument("tensor device storage is too small")
+            self._state = _State(layout.shape(), placement)
+            self._state.storage = _Storage(buffer, None)
+            if not layout.is_contiguous():
+                self._state.layout = layout
+            return
         if isinstance(shape, tensor_expr):
             out_shape, scalar, inputs, where = _infer(shape._root)
             if not inputs:
@@ -345,13 +411,20 @@ class tensor:  # noqa: N801 - porch's spelling
         return self._state.shape
 
     def strides(self) -> tuple[int, ...]:
+        if self._state.layout is not None:
+            return self._state.layout.strides()
         return _contiguous_strides(self._state.shape)
 
     def storage_offset(self) -> int:
-        return 0
+        return 0 if self._state.layout is None else self._state.layout.storage_offset()
 
     def is_contiguous(self) -> bool:
-        return True
+        return self._state.layout is None
+
+    def layout(self) -> tensor_layout:
+        if self._state.layout is not None:
+            return self._state.layout
+        return tensor_layout(self._state.shape)
 
     def rank(self) -> int:
         return len(self._state.shape)
@@ -364,7 +437,13 @@ class tensor:  # noqa: N801 - porch's spelling
 
     # values
     def data(self) -> np.ndarray:
-        """Host values (read-only view); materialises and waits for the GPU."""
+        """Host values (read-only view); materialises and waits for the GPU.
+        Strided storage is gathered into row-major order on the device once."""
+        if self._state.layout is not None:
+            with self._state.lock:
+                if self._state.dense is None:
+                    self._state.dense = materialize(tensor_expr(self))
+            return self._state.dense.data()
         storage = self._state.realized()
         with storage.lock:
             if storage.host is None:
@@ -375,6 +454,17 @@ class tensor:  # noqa: N801 - porch's spelling
 
     def cpu(self) -> np.ndarray:
         return np.array(self.data(), copy=True)
+
+    def _storage_values(self) -> np.ndarray:
+        """The raw storage (for strided storage: the span its layout reaches),
+        as the node table's input slot holds it."""
+        if self._state.layout is None:
+            return self.data()
+        storage = self._state.realized()
+        with storage.lock:
+            if storage.host is None:
+                storage.host = storage.buffer.download(self._state.layout.span())
+            return storage.host
 
     def device_data(self) -> _Buffer:
         return self._state.realized().buffer
@@ -396,7 +486,7 @@ class tensor:  # noqa: N801 - porch's spelling
         strides = self.strides()
         out_shape: list[int] = []
         out_strides: list[int] = []
-        offset = 0
+        offset = self.storage_offset()
         for dim, index in enumerate(indices):
             extent = shape[dim]
             stride = strides[dim]
@@ -427,7 +517,10 @@ class tensor:  # noqa: N801 - porch's spelling
         for dim in range(len(indices), self.rank()):
             out_shape.append(shape[dim])
             out_strides.append(strides[dim])
-        node = _Node("slice", tensor_expr(self)._root)
+        # offsets and strides are in storage elements: over strided storage
+        # the slice applies to the raw storage, not to the view
+        source = tensor_expr(self)._root if self.is_contiguous() else _storage_node(self)
+        node = _Node("slice", source)
         node.shape = out_shape
         node.strides = out_strides
         node.offset = offset
@@ -459,6 +552,12 @@ class tensor:  # noqa: N801 - porch's spelling
         return tensor_expr(other) / tensor_expr(self)
 
 
+def _storage_node(value: "tensor") -> _Node:
+    node = _Node("input")
+    node.input = value
+    return node
+
+
 def _normalize_endpoint(index: int, extent: int) -> int:
     if index < 0:
         index += extent
@@ -481,10 +580,15 @@ class tensor_expr:  # noqa: N801 - porch's spelling
             state = value._state
             if state.storage is None and state.expression is not None:
                 self._root = state.expression  # inline a pending tensor
+            elif state.layout is not None:
+                # strided storage: the view is a slice of the raw storage
+                view = _Node("slice", _storage_node(value))
+                view.shape = list(state.layout.shape())
+                view.strides = list(state.layout.strides())
+                view.offset = state.layout.storage_offset()
+                self._root = view
             else:
-                node = _Node("input")
-                node.input = value
-                self._root = node
+                self._root = _storage_node(value)
         else:
             node = _Node("scalar")
             node.scalar = float(np.float32(value))

@@ -53,6 +53,10 @@ namespace porch {
         device placement;
         std::shared_ptr<realized_storage> realized;
         std::shared_ptr<lazy_materialization> lazy;
+        // Strided storage: the values gathered in row-major order, made once
+        // on first data().
+        std::once_flag dense_once;
+        std::shared_ptr<realized_storage> dense;
 
         state(tensor_layout l, device p) : layout(std::move(l)), placement(p) {}
 
@@ -142,6 +146,24 @@ namespace porch {
             return true;
         }
 
+        // Floats of storage a layout reaches: offset + sum (extent-1)*stride + 1.
+        size_t storage_span(const tensor_layout& layout) {
+            if (layout.numel() == 0) return 0;
+            index_t last = layout.storage_offset();
+            for (size_t d = 0; d < layout.rank(); ++d)
+                last += (layout.shape()[d] - 1) * layout.strides()[d];
+            return static_cast<size_t>(last) + 1;
+        }
+
+        // The input node of a tensor's storage (for strided storage, the
+        // flat span its layout reaches).
+        node_ptr storage_node(const tensor& value) {
+            auto n = std::make_shared<tensor_expr::node>();
+            n->kind = ir::op::input;
+            n->input = value;
+            return n;
+        }
+
         // The DAG of an expression as a node table, inputs in first-visit
         // order (lhs before rhs), as the reference numbers them
         // (src/tensor.cpp:261-277).
@@ -193,7 +215,10 @@ namespace porch {
                             inputs.push_back(t);
                         }
                         out.input = found->second;
-                        out.shape.assign(t.shape().begin(), t.shape().end());
+                        if (t.is_contiguous())
+                            out.shape.assign(t.shape().begin(), t.shape().end());
+                        else // strided storage, read through a slice above
+                            out.shape = {static_cast<index_t>(storage_span(t.layout()))};
                         g.n_inputs = static_cast<int>(inputs.size());
                     }
                     else {
@@ -370,8 +395,27 @@ namespace porch {
     size_t tensor::numel() const noexcept { return state_->layout.numel(); }
     device tensor::placement() const noexcept { return state_->placement; }
 
+    tensor::tensor(tensor_layout layout, cuda_jit::device_buffer storage, device placement)
+        : state_(std::make_shared<state>(std::move(layout), placement)) {
+        if (storage.size_bytes() < storage_span(state_->layout) * sizeof(float32_t))
+            throw std::invalid_argument("tensor device storage is too small");
+        state_->realized = std::make_shared<realized_storage>(
+            std::move(storage), std::vector<float32_t>{}, false
+        );
+    }
+
     std::span<const float32_t> tensor::data() const {
-        std::shared_ptr<realized_storage> storage = state_->storage();
+        std::shared_ptr<realized_storage> storage;
+        if (state_->layout.is_contiguous()) {
+            storage = state_->storage();
+        }
+        else {
+            std::call_once(state_->dense_once, [this] {
+                const tensor dense = materialize(tensor_expr{*this});
+                state_->dense = detail::tensor_access::state(dense)->storage();
+            });
+            storage = state_->dense;
+        }
         std::scoped_lock lock{storage->host_mutex};
         if (!storage->host_current) {
             storage->host.resize(numel());
@@ -440,7 +484,10 @@ namespace porch {
         (void)ir::checked_numel(out_shape);
         auto n = std::make_shared<tensor_expr::node>();
         n->kind = ir::op::slice;
-        n->lhs = detail::expr_access::root(tensor_expr{*this});
+        // Offsets and strides above are in storage elements: over strided
+        // storage the slice applies to the raw storage, not to the view.
+        n->lhs = is_contiguous() ? detail::expr_access::root(tensor_expr{*this})
+                                 : storage_node(*this);
         n->shape = std::move(out_shape);
         n->strides = std::move(out_strides);
         n->offset = offset;
@@ -459,10 +506,19 @@ namespace porch {
             root_ = st->lazy->expression;
             return;
         }
-        auto n = std::make_shared<tensor_expr::node>();
-        n->kind = ir::op::input;
-        n->input = value;
-        root_ = std::move(n);
+        if (!value.is_contiguous()) {
+            // Strided storage: the view is a slice of the raw storage.
+            const tensor_layout& layout = value.layout();
+            auto view = std::make_shared<tensor_expr::node>();
+            view->kind = ir::op::slice;
+            view->lhs = storage_node(value);
+            view->shape.assign(layout.shape().begin(), layout.shape().end());
+            view->strides.assign(layout.strides().begin(), layout.strides().end());
+            view->offset = layout.storage_offset();
+            root_ = std::move(view);
+            return;
+        }
+        root_ = storage_node(value);
     }
 
     tensor_expr::tensor_expr(float32_t value) {

@@ -25,6 +25,17 @@ def placeholder(shape, values=None) -> porch.tensor:
     return t
 
 
+def strided_placeholder(layout, storage_values) -> porch.tensor:
+    """A host-only tensor over strided storage (the raw storage values)."""
+    t = porch.tensor.__new__(porch.tensor)
+    t._state = porch._State(list(layout.shape()), porch.device())
+    host = np.ascontiguousarray(np.asarray(storage_values, dtype=np.float32).reshape(-1))
+    t._state.storage = porch._Storage(None, host)
+    if not layout.is_contiguous():
+        t._state.layout = layout
+    return t
+
+
 def kat_cases():
     with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
         data = json.load(f)
