@@ -82,6 +82,9 @@ namespace porch::hip {
                     hip_library, t.event_elapsed_time, "hipEventElapsedTime"
                 );
                 ok &= bind(hip_library, t.event_destroy, "hipEventDestroy");
+                ok &= bind(hip_library, t.event_query, "hipEventQuery");
+                ok &= bind(hip_library, t.host_malloc, "hipHostMalloc");
+                ok &= bind(hip_library, t.host_free, "hipHostFree");
                 ok &= bind(hip_library, t.malloc_async, "hipMallocAsync");
                 ok &= bind(hip_library, t.free_async, "hipFreeAsync");
                 ok &= bind(

@@ -66,6 +66,9 @@ namespace porch::hip {
         error_t (*event_synchronize)(event_t);
         error_t (*event_elapsed_time)(float*, event_t, event_t);
         error_t (*event_destroy)(event_t);
+        error_t (*event_query)(event_t);
+        error_t (*host_malloc)(void**, size_t, unsigned);
+        error_t (*host_free)(void*);
         error_t (*malloc_async)(void**, size_t, stream_t);
         error_t (*free_async)(void*, stream_t);
         error_t (*device_get_default_mem_pool)(mem_pool_t*, int);

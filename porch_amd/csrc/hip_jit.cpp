@@ -119,13 +119,17 @@ namespace porch::hip_jit {
         std::shared_ptr<rt::stream> s = rt::current_stream();
         device_buffer_state& state = *buffer_access::state(buffer);
         state.before_write(s);
-        const hip::api& h = hip::runtime();
-        hip::check(
-            h.memcpy_htod_async(state.ptr, source.data(), source.size_bytes(), s->handle()),
-            "hipMemcpyHtoDAsync"
-        );
-        // The source span may be released as soon as this returns.
-        s->synchronize();
+        // Staged through pinned memory, the DMA runs behind the caller;
+        // without a staging chunk the copy is direct and waited for.  Either
+        // way the source span may be released as soon as this returns.
+        if (!rt::upload_staged(state.ptr, source.data(), source.size_bytes(), *s)) {
+            const hip::api& h = hip::runtime();
+            hip::check(
+                h.memcpy_htod_async(state.ptr, source.data(), source.size_bytes(), s->handle()),
+                "hipMemcpyHtoDAsync"
+            );
+            s->synchronize();
+        }
         state.after_write(s);
     }
 

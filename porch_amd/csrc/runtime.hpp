@@ -69,6 +69,17 @@ namespace porch::rt {
     // Makes `consumer` wait for all work queued so far on `producer`.
     void order_after(const stream& consumer, const stream& producer);
 
+    // A host-to-device copy that returns before the DMA ends: the source is
+    // copied (by several host threads when large) into pinned staging chunks
+    // (hipHostMalloc) in pieces of at most 32 MiB, each piece's DMA is queued
+    // on `s` as soon as it is staged, and a chunk is reused once an event
+    // recorded after its DMA has completed.  Chunks (powers of two from
+    // 1 MiB) are pooled up to 512 MiB of pinned memory.  Returns false,
+    // having done nothing, only when no chunk can be had.
+    bool upload_staged(void* dst, const void* src, size_t bytes, const stream& s);
+    // Pinned bytes held by the staging pool.
+    size_t staging_bytes();
+
     struct buffer_state {
         explicit buffer_state(size_t requested_bytes);
         ~buffer_state();

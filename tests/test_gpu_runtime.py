@@ -104,3 +104,46 @@ def test_events_time_the_stream(gpu):
     stop.synchronize()
     assert 0.0 < start.elapsed_ms(stop) < 1000.0
     assert y.cpu()[0] == 2.0
+
+
+@pytest.mark.gpu
+def test_staged_uploads_round_trip(gpu):
+    """Uploads return before their DMA ends (pinned staging chunks, 32 MiB
+    pieces): every buffer must still hold exactly what was uploaded, also
+    when chunks are reused while earlier DMAs are pending and the source
+    array is overwritten right after the call returns."""
+    rng = np.random.default_rng(12)
+    sizes = [1, 3, 1 << 18, (1 << 20) + 7, (9 << 20) + 5, 40 << 20, 100 << 20]
+    expected, buffers = [], []
+    source = np.empty(max(sizes), np.float32)
+    for n in sizes * 2:
+        values = rng.standard_normal(n).astype(np.float32)
+        source[:n] = values
+        buffers.append(gpu._Buffer.upload(source[:n]))
+        source[:n] = -1.0  # the caller may reuse its memory at once
+        expected.append(values)
+    for buf, values in zip(buffers, expected):
+        got = buf.download(values.size)
+        assert np.array_equal(got.view(np.uint32), values.view(np.uint32)), values.size
+
+
+@pytest.mark.gpu
+def test_staged_uploads_from_several_threads(gpu):
+    import threading
+
+    results = {}
+
+    def worker(k):
+        values = np.full((12 << 20) + k, float(k), np.float32)
+        buf = gpu._Buffer.upload(values)
+        t = gpu.tensor._realized([values.size], buf, None, gpu.device())
+        results[k] = gpu.materialize(t * 2.0).cpu()
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(6)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for k in range(6):
+        assert results[k].size == (12 << 20) + k
+        assert np.all(results[k] == 2.0 * k)
