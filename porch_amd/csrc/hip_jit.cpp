@@ -139,12 +139,17 @@ namespace porch::hip_jit {
         std::shared_ptr<rt::stream> s = rt::current_stream();
         device_buffer_state& state = *buffer_access::state(buffer);
         state.before_read(s);
-        const hip::api& h = hip::runtime();
-        hip::check(
-            h.memcpy_dtoh_async(target.data(), state.ptr, target.size_bytes(), s->handle()),
-            "hipMemcpyDtoHAsync"
-        );
-        s->synchronize();
+        // Large results come back through pinned chunks, pipelined with the
+        // copy out of them; small ones (or without a chunk) directly.
+        if (target.size_bytes() < (size_t{1} << 20) ||
+            !rt::download_staged(target.data(), state.ptr, target.size_bytes(), *s)) {
+            const hip::api& h = hip::runtime();
+            hip::check(
+                h.memcpy_dtoh_async(target.data(), state.ptr, target.size_bytes(), s->handle()),
+                "hipMemcpyDtoHAsync"
+            );
+            s->synchronize();
+        }
     }
 
     void synchronize() { rt::current_stream()->synchronize(); }

@@ -269,99 +269,143 @@ namespace porch::rt {
     } // namespace
 
     namespace {
-        // One piece through one chunk; false when no chunk can be had.
-        bool stage_piece(void* dst, const void* src, size_t bytes, const stream& s);
+        // A chunk of at least `bytes`, marked busy; nullptr when the pool is
+        // full of chunks other callers are filling or draining.
+        staging_chunk* acquire_chunk(const hip::api& h, size_t bytes) {
+            size_t size = size_t{1} << 20;
+            while (size < bytes) size <<= 1;
+            staging_pool& pool = staging();
+            std::scoped_lock lock{pool.mutex};
+            for (auto& c : pool.chunks) {
+                if (c->bytes == size && chunk_idle(h, *c)) {
+                    c->busy = true;
+                    return c.get();
+                }
+            }
+            // Make room: free idle chunks of other sizes, then wait for
+            // pending ones, until the new chunk fits under the cap.
+            for (const bool wait : {false, true}) {
+                for (auto it = pool.chunks.begin();
+                     it != pool.chunks.end() && pool.total + size > staging_cap;) {
+                    staging_chunk& c = **it;
+                    if (wait && c.pending && !c.busy)
+                        hip::check(h.event_synchronize(c.done), "hipEventSynchronize");
+                    if (chunk_idle(h, c)) {
+                        (void)h.host_free(c.host);
+                        (void)h.event_destroy(c.done);
+                        pool.total -= c.bytes;
+                        it = pool.chunks.erase(it);
+                    }
+                    else {
+                        ++it;
+                    }
+                }
+            }
+            if (pool.total + size > staging_cap) return nullptr;
+            auto fresh = std::make_unique<staging_chunk>();
+            hip::check(h.host_malloc(&fresh->host, size, 0), "hipHostMalloc");
+            const hip::error_t made = h.event_create_with_flags(&fresh->done, hip::event_disable_timing);
+            if (made != hip::success) (void)h.host_free(fresh->host);
+            hip::check(made, "hipEventCreateWithFlags");
+            fresh->bytes = size;
+            fresh->busy = true;
+            pool.total += size;
+            pool.chunks.push_back(std::move(fresh));
+            return pool.chunks.back().get();
+        }
+
+        // Hands a chunk back; `pending`: its event was recorded behind work
+        // that still reads or writes it.
+        void release_chunk(staging_chunk* c, bool pending) {
+            std::scoped_lock lock{staging().mutex};
+            c->busy = false;
+            c->pending = pending;
+        }
+
+        constexpr size_t staging_piece = size_t{32} << 20;
     } // namespace
 
     bool upload_staged(void* dst, const void* src, size_t bytes, const stream& s) {
         // Pieces of at most 32 MiB, each through its own chunk: the host
         // copy of one piece overlaps the DMA of the previous one.
-        constexpr size_t piece = size_t{32} << 20;
+        const hip::api& h = hip::runtime();
         for (size_t done = 0; done < bytes;) {
-            const size_t n = std::min(piece, bytes - done);
-            if (!stage_piece(static_cast<char*>(dst) + done, static_cast<const char*>(src) + done, n, s)) {
+            const size_t n = std::min(staging_piece, bytes - done);
+            char* to = static_cast<char*>(dst) + done;
+            const char* from = static_cast<const char*>(src) + done;
+            staging_chunk* chunk = acquire_chunk(h, n);
+            if (chunk == nullptr) {
                 if (done == 0) return false;
                 // Chunks all taken by other threads: copy the rest directly.
-                const hip::api& h = hip::runtime();
-                hip::check(h.memcpy_htod_async(static_cast<char*>(dst) + done,
-                                               static_cast<const char*>(src) + done, bytes - done,
-                                               s.handle()),
-                           "hipMemcpyHtoDAsync");
+                hip::check(h.memcpy_htod_async(to, from, bytes - done, s.handle()), "hipMemcpyHtoDAsync");
                 s.synchronize();
                 return true;
             }
+            staged_copy(chunk->host, from, n);
+            hip::error_t queued = h.memcpy_htod_async(to, chunk->host, n, s.handle());
+            if (queued == hip::success) queued = h.event_record(chunk->done, s.handle());
+            if (queued != hip::success) {
+                // The copy may be in flight: wait before the chunk is reused.
+                (void)h.stream_synchronize(s.handle());
+                release_chunk(chunk, false);
+                hip::check(queued, "hipMemcpyHtoDAsync");
+            }
+            release_chunk(chunk, true);
             done += n;
         }
         return true;
     }
 
-    namespace {
-    bool stage_piece(void* dst, const void* src, size_t bytes, const stream& s) {
-        if (bytes == 0) return true;
-        size_t size = size_t{1} << 20;
-        while (size < bytes) size <<= 1;
-        if (size > staging_largest) return false;
+    bool download_staged(void* dst, const void* src, size_t bytes, const stream& s) {
+        // Rounds of up to four 32 MiB pieces: all of a round's DMAs are
+        // queued into pinned chunks, then each piece is copied out as soon
+        // as its DMA is done, while the later ones still run.
         const hip::api& h = hip::runtime();
-        staging_pool& pool = staging();
-        staging_chunk* chunk = nullptr;
-        {
-            std::scoped_lock lock{pool.mutex};
-            for (auto& c : pool.chunks) {
-                if (c->bytes == size && chunk_idle(h, *c)) {
-                    chunk = c.get();
-                    break;
-                }
+        constexpr size_t round = 4;
+        void* device = const_cast<void*>(src);
+        size_t done = 0;
+        while (done < bytes) {
+            staging_chunk* chunks[round] = {};
+            size_t sizes[round] = {};
+            size_t count = 0;
+            hip::error_t queued = hip::success;
+            for (size_t at = done; count < round && at < bytes && queued == hip::success;) {
+                const size_t n = std::min(staging_piece, bytes - at);
+                staging_chunk* chunk = acquire_chunk(h, n);
+                if (chunk == nullptr) break;
+                chunks[count] = chunk;
+                sizes[count] = n;
+                ++count;
+                queued = h.memcpy_dtoh_async(chunk->host, static_cast<char*>(device) + at, n, s.handle());
+                if (queued == hip::success) queued = h.event_record(chunk->done, s.handle());
+                at += n;
             }
-            if (chunk == nullptr) {
-                // Make room: free idle chunks of other sizes, then wait for
-                // pending ones, until the new chunk fits under the cap.
-                for (const bool wait : {false, true}) {
-                    for (auto it = pool.chunks.begin();
-                         it != pool.chunks.end() && pool.total + size > staging_cap;) {
-                        staging_chunk& c = **it;
-                        if (wait && c.pending && !c.busy)
-                            hip::check(h.event_synchronize(c.done), "hipEventSynchronize");
-                        if (chunk_idle(h, c)) {
-                            (void)h.host_free(c.host);
-                            (void)h.event_destroy(c.done);
-                            pool.total -= c.bytes;
-                            it = pool.chunks.erase(it);
-                        }
-                        else {
-                            ++it;
-                        }
-                    }
+            if (queued != hip::success) (void)h.stream_synchronize(s.handle());
+            hip::error_t waited = hip::success;
+            for (size_t i = 0; i < count; ++i) {
+                if (queued == hip::success && waited == hip::success) {
+                    waited = h.event_synchronize(chunks[i]->done);
+                    if (waited == hip::success)
+                        staged_copy(static_cast<char*>(dst) + done, chunks[i]->host, sizes[i]);
                 }
-                if (pool.total + size > staging_cap) return false; // all chunks being filled
-                auto fresh = std::make_unique<staging_chunk>();
-                hip::check(h.host_malloc(&fresh->host, size, 0), "hipHostMalloc");
-                const hip::error_t made = h.event_create_with_flags(&fresh->done, hip::event_disable_timing);
-                if (made != hip::success) (void)h.host_free(fresh->host);
-                hip::check(made, "hipEventCreateWithFlags");
-                fresh->bytes = size;
-                pool.total += size;
-                chunk = fresh.get();
-                pool.chunks.push_back(std::move(fresh));
+                done += sizes[i];
+                release_chunk(chunks[i], false);
             }
-            chunk->busy = true;
-        }
-        hip::error_t queued = hip::success;
-        staged_copy(chunk->host, src, bytes);
-        queued = h.memcpy_htod_async(dst, chunk->host, bytes, s.handle());
-        if (queued == hip::success) queued = h.event_record(chunk->done, s.handle());
-        {
-            std::scoped_lock lock{pool.mutex};
-            chunk->busy = false;
-            chunk->pending = queued == hip::success;
-        }
-        if (queued != hip::success) {
-            // The copy may be in flight: wait before the chunk is reused.
-            (void)h.stream_synchronize(s.handle());
-            hip::check(queued, "hipMemcpyHtoDAsync");
+            hip::check(queued, "hipMemcpyDtoHAsync");
+            hip::check(waited, "hipEventSynchronize");
+            if (count == 0) {
+                if (done == 0) return false;
+                // Chunks all taken by other threads: copy the rest directly.
+                hip::check(h.memcpy_dtoh_async(static_cast<char*>(dst) + done,
+                                               static_cast<char*>(device) + done, bytes - done,
+                                               s.handle()),
+                           "hipMemcpyDtoHAsync");
+                s.synchronize();
+                return true;
+            }
         }
         return true;
     }
-    } // namespace
 
     size_t staging_bytes() {
         std::scoped_lock lock{staging().mutex};

@@ -77,6 +77,10 @@ namespace porch::rt {
     // 1 MiB) are pooled up to 512 MiB of pinned memory.  Returns false,
     // having done nothing, only when no chunk can be had.
     bool upload_staged(void* dst, const void* src, size_t bytes, const stream& s);
+    // A device-to-host copy through the same pinned chunks, pipelined:
+    // waits until `dst` holds the data.  Returns false, having done
+    // nothing, only when no chunk can be had.
+    bool download_staged(void* dst, const void* src, size_t bytes, const stream& s);
     // Pinned bytes held by the staging pool.
     size_t staging_bytes();
 
