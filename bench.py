@@ -14,7 +14,9 @@ the per-launch duration behind `roofline.achieved`).
 The headline line is the view chain (strided slices + transposes + concat
 over x fp32 [4096, 4096]): HBM GB/s of algorithmic bytes (all of x read, the
 output written).  The other workloads are reported beside it under
-"configs", each with its roofline fraction and JIT latency.  The host
+"configs", each with its roofline fraction and JIT latency, followed by three
+workloads of the IR extensions (a batched transpose and a head permute via
+permute, and a batched matmul with an epilogue).  The host
 evaluator (the oracle, OpenMP) is timed on this machine's cores as the CPU
 baseline.
 
@@ -309,7 +311,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--configs", default="elementwise,view_chain,softmax,logistic_rowsum,matmul_epilogue")
+    parser.add_argument("--configs", default="elementwise,view_chain,softmax,logistic_rowsum,matmul_epilogue,"
+                                             "batched_transpose,heads_permute,batched_matmul")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--jit-probe", default=None, help=argparse.SUPPRESS)
     args = parser.parse_args()
