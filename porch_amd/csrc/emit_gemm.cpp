@@ -306,12 +306,29 @@ namespace porch::cg {
             s += "    {\n        const idx_t k0 = 0;\n        const int nb = 0;\n";
             s += load_a + load_b + store_a + store_b;
             s += "    }\n    __syncthreads();\n";
+            // With both operands on the 128-bit path the next tile's global
+            // loads and LDS stores are issued in the same block as the
+            // MFMAs, so the scheduler can interleave both with them (the last
+            // step reloads its own tile, in bounds, into the idle buffer);
+            // otherwise they are skipped on the last step.
+            const int vmem = bm / 64 + BN / 64;
+            const int mfmas = (BK / 2) * ib * 2;
+            const int ds_writes = (la.k_major ? 2 : 4) * (bm / 64) + (lb.k_major ? 2 : 4) * (BN / 64);
+            const bool scheduled = la.vector && lb.vector;
+            const bool interleave = scheduled && 4 * vmem + 4 + ds_writes <= mfmas;
             s += "    for (int t = 0; t < " + std::to_string(steps) + "; ++t) {\n";
             s += "        const int cb = t & 1;\n";
             s += "        const int nb = cb ^ 1;\n";
-            s += "        const idx_t k0 = (idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
-            s += "        const bool more = t + 1 < " + std::to_string(steps) + ";\n";
-            s += "        if (more) {\n" + load_a + load_b + "        }\n";
+            if (interleave) {
+                s += "        const idx_t k0 = (idx_t)(t + 1 < " + std::to_string(steps) + " ? t + 1 : t) * " +
+                     std::to_string(BK) + ";\n";
+                s += "        {\n" + load_a + load_b + "        }\n";
+            }
+            else {
+                s += "        const idx_t k0 = (idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
+                s += "        const bool more = t + 1 < " + std::to_string(steps) + ";\n";
+                s += "        if (more) {\n" + load_a + load_b + "        }\n";
+            }
             // this lane's k parity and row inside each 32-row block
             s += "        const int h = lane >> 5;\n";
             s += "        const int li = lane & 31;\n";
@@ -335,25 +352,37 @@ namespace porch::cg {
             s += "            #pragma unroll\n            for (int i = 0; i < " + IB + "; ++i)\n";
             s += "                #pragma unroll\n                for (int j = 0; j < 2; ++j)\n";
             s += "                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][st], bv[j][st], acc[i][j], 0, 0, 0);\n";
-            if (la.vector && lb.vector) {
+            if (interleave) s += "        {\n" + store_a + store_b + "        }\n";
+            if (scheduled) {
                 // Instruction order for the scheduler: the 128-bit LDS reads
                 // first, then one of the next tile's global loads after every
                 // four MFMAs, so those loads leave early and their latency
                 // hides under the remaining MFMAs (measured 7% faster at
                 // 4096^3 than the compiler's own order, which issued them
-                // after nearly all MFMAs).
+                // after nearly all MFMAs).  Then, after a gap of MFMAs that
+                // covers the loads' latency, one LDS store of the next tile
+                // after each MFMA, instead of all of them after the last
+                // MFMA (another 4% at 4096^3).
                 const int ds_reads = 2 * ib + 4;
-                const int vmem = bm / 64 + BN / 64;
-                const int mfmas = (BK / 2) * ib * 2;
                 s += "        __builtin_amdgcn_sched_group_barrier(0x100, " + std::to_string(ds_reads) + ", 0);\n";
                 for (int g = 0; g < vmem; ++g) {
                     s += "        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);\n";
                     s += "        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);\n";
                 }
-                s += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(mfmas - 4 * vmem) +
-                     ", 0);\n";
+                int rest = mfmas - 4 * vmem;
+                if (interleave) {
+                    const int gap = std::min(16, rest - ds_writes);
+                    s += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(gap) + ", 0);\n";
+                    for (int g = 0; g < ds_writes; ++g) {
+                        s += "        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);\n";
+                        s += "        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);\n";
+                    }
+                    rest -= gap + ds_writes;
+                }
+                if (rest > 0)
+                    s += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(rest) + ", 0);\n";
             }
-            s += "        if (more) {\n" + store_a + store_b + "        }\n";
+            if (!interleave) s += "        if (more) {\n" + store_a + store_b + "        }\n";
             s += "        __syncthreads();\n";
             s += "    }\n";
             // epilogue
