@@ -2,6 +2,7 @@
 reference's geometry, buffers, and compile errors."""
 
 import ctypes
+import re
 
 import numpy as np
 import pytest
@@ -147,3 +148,26 @@ def test_staged_uploads_from_several_threads(gpu):
     for k in range(6):
         assert results[k].size == (12 << 20) + k
         assert np.all(results[k] == 2.0 * k)
+
+
+@pytest.mark.gpu
+def test_realised_lazy_tensor_is_read_not_recomputed(gpu):
+    """A pending tensor is inlined into later expressions; once realised, its
+    buffer is read instead (the reference re-inlines its expression at every
+    use, src/tensor.cpp:1323-1325)."""
+    x = gpu.tensor([512, 512], np.arange(512 * 512, dtype=np.float32))
+    pending = gpu.tensor(gpu.exp(x * 1e-6) + 1.0)
+    def body(expr):  # the kernel itself, without the shared helper definitions
+        source = gpu.kernel_source(expr)
+        return source[source.index('extern "C"'):]
+
+    inlined = gpu.plan(pending * 2.0)
+    computes_exp = re.compile(r"\bexpf\(|porch_exp")
+    assert computes_exp.search(body(pending * 2.0))  # the exp is recomputed in the consumer
+    pending.realize()
+    assert not computes_exp.search(body(pending * 2.0))  # the consumer reads the buffer
+    nodes, _, _, inputs, _ = gpu.serialize((pending * 2.0)._root)
+    assert len(inputs) == 1 and inputs[0] is pending
+    assert len(inlined["kernels"]) == 1
+    out = gpu.materialize(pending * 2.0).cpu()
+    assert np.array_equal(out.view(np.uint32), (pending.cpu() * np.float32(2)).view(np.uint32))
