@@ -332,9 +332,9 @@ def main() -> int:
         return 1
     info = synth.device_info()
     log(f"device: {info}")
-    configs = [c for c in args.configs.split(",") if c]
+    workload_names = [c for c in args.configs.split(",") if c]
     results = {}
-    for name in configs:
+    for name in workload_names:
         # Matmul steps are long; keep its timed region short.
         steps = args.steps if WORK[name][0] == "hbm" else max(3, args.steps // 40)
         warmup = args.warmup if WORK[name][0] == "hbm" else max(1, args.warmup // 10)
@@ -350,7 +350,7 @@ def main() -> int:
             log(f"{name}: cpu {results[name]['cpu_baseline']['value']:.2f} "
                 f"{results[name]['cpu_baseline']['unit']} on {results[name]['cpu_baseline']['cores']} threads")
 
-    head = "view_chain" if "view_chain" in results else configs[0]
+    head = "view_chain" if "view_chain" in results else workload_names[0]
     h = results[head]
     line = {
         "metric": METRIC,

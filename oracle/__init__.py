@@ -1,5 +1,5 @@
 """Test infrastructure: the porch host evaluator (liboracle.so).
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use
-this package, as the checker; the product never imports it.
+this package, to compare results against; the product never imports it.
 """

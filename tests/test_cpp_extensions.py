@@ -1,7 +1,7 @@
 """The C++ API of the IR extensions (permute, batched_matmul, tensors over
 strided storage) through a test program built against include/porch/*.hpp
 and libporch_amd.so (tests/cpp/extensions_test.cpp, recipe
-tests/cpp/Makefile).  The program's own assertions are the checker: exact
+tests/cpp/Makefile).  The program's own assertions decide: exact
 values computed by plain loops in the program."""
 
 import os

@@ -1,6 +1,6 @@
 """The reference's own test program, compiled unchanged from its
 tests/tensor_test.cpp against include/porch/*.hpp and libporch_amd.so
-(recipe: oracle/Makefile `ref`).  Its assertions are the checker."""
+(recipe: oracle/Makefile `ref`).  Its own assertions decide each case."""
 
 import os
 import subprocess

@@ -1,4 +1,4 @@
-"""Pins the host evaluator (the oracle) before it is trusted as the checker.
+"""Pins the host evaluator (the oracle) before results are compared against it.
 
 Checks: every known-answer vector of the reference's tests, and — where
 those leave room — independent statements of the result (numpy slicing for
