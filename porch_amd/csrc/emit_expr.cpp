@@ -202,6 +202,18 @@ namespace porch::cg {
         return result;
     }
 
+    void emitter::open_scope(const std::string& condition) {
+        line("if (" + condition + ") {");
+        indent += "    ";
+        frames_.emplace_back();
+    }
+
+    void emitter::close_scope() {
+        frames_.pop_back();
+        indent.resize(indent.size() - 4);
+        line("}");
+    }
+
     std::string index_text(const ival& v, const std::vector<std::string>& names) {
         if (!v.is_affine) {
             // Generic code refers to q{d}; the kernel declares those names.

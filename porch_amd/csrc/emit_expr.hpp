@@ -46,6 +46,10 @@ namespace porch::cg {
         std::vector<std::string> emit(int id);
         std::string fresh(const char* prefix);
         void line(const std::string& text);
+        // `if (condition) {` with a scope of its own: values emitted until
+        // close_scope() are not reused after it.
+        void open_scope(const std::string& condition);
+        void close_scope();
 
         // Range of node `id` (computed once, on first use).
         const vrange& range_of(int id);

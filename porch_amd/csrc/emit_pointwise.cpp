@@ -8,6 +8,7 @@
 #include "emit_expr.hpp"
 
 #include <algorithm>
+#include <functional>
 #include <stdexcept>
 
 namespace porch::cg {
@@ -258,6 +259,9 @@ namespace porch::cg {
         struct tiling {
             int p = -1;                 // coordinate the staged leaves run along
             std::vector<int> staged;    // kexpr roots evaluated in phase 1
+            // Per staged root: the selects above it and the branch each must
+            // take (true: the first operand) for its value to be used.
+            std::vector<std::vector<std::pair<kcond, bool>>> guards;
         };
 
         tiling choose_tiling(const pointwise_request& r) {
@@ -342,7 +346,51 @@ namespace porch::cg {
                 stack.push_back(n.a);
                 stack.push_back(n.b);
             }
-            if (t.staged.empty() || t.staged.size() > 8) t.p = -1;
+            if (t.staged.empty() || t.staged.size() > 8) {
+                t.p = -1;
+                return t;
+            }
+            // Phase 1 computes the staged values ahead of the selects above
+            // them, so each is computed only where those selects take its
+            // branch: elsewhere its loads may fall outside their buffers.
+            // A staged root reached along more than one path, or through a
+            // select with a non-affine condition, is not staged.
+            t.guards.assign(t.staged.size(), {});
+            std::vector<char> reached(t.staged.size(), 0);
+            std::vector<std::pair<kcond, bool>> path;
+            int visits = 0;
+            bool ok = true;
+            std::function<void(int)> walk = [&](int id) {
+                if (!ok || id < 0) return;
+                if (++visits > 4096) {
+                    ok = false;
+                    return;
+                }
+                for (size_t i = 0; i < t.staged.size(); ++i) {
+                    if (t.staged[i] != id) continue;
+                    if (reached[i]) ok = false;
+                    reached[i] = 1;
+                    t.guards[i] = path;
+                    return;
+                }
+                const knode& n = r.expr->at(id);
+                if (n.op == kop::select) {
+                    if (!n.cond.lhs.is_affine) {
+                        ok = ok && r.expr->loads(id).empty();
+                        return;
+                    }
+                    path.emplace_back(n.cond, true);
+                    walk(n.a);
+                    path.back().second = false;
+                    walk(n.b);
+                    path.pop_back();
+                    return;
+                }
+                walk(n.a);
+                walk(n.b);
+            };
+            walk(r.root);
+            if (!ok) t.p = -1;
             return t;
         }
 
@@ -445,6 +493,9 @@ namespace porch::cg {
             for (const int64_t v : {int64_t{4}, int64_t{2}}) {
                 if (extent_p % v != 0) continue;
                 bool uniform = true;
+                for (const auto& guard : t.guards)
+                    for (const auto& [c, branch] : guard)
+                        if (!uniform_over(c, p, v)) uniform = false;
                 bool useful = false;
                 for (size_t id = 0; id < k.nodes.size(); ++id) {
                     if (!in_stage[id]) continue;
@@ -664,10 +715,17 @@ namespace porch::cg {
                     return lanes;
                 };
                 for (size_t i = 0; i < n_stage; ++i) {
+                    std::string guard;
+                    for (const auto& [c, branch] : t.guards[i]) {
+                        if (!guard.empty()) guard += " && ";
+                        guard += branch ? cond_fn(c) : "!(" + cond_fn(c) + ")";
+                    }
+                    if (!guard.empty()) em.open_scope(guard);
                     const std::vector<std::string> v = em.emit(t.staged[i]);
                     for (int64_t e = 0; e < V; ++e)
                         em.line("stage[" + std::to_string(i) + "][pl + " + std::to_string(e) +
                                 "][ql] = " + v[e] + ";");
+                    if (!guard.empty()) em.close_scope();
                 }
                 code += body;
                 if (!guard.empty()) code += "            }\n";

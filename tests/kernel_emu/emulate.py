@@ -1,0 +1,90 @@
+"""Runs a graph's generated kernels on the CPU with guarded buffers —
+TEST INFRASTRUCTURE ONLY (see prelude.hpp).
+
+emulate(expr) compiles each kernel of the graph's plan as host C++ with
+clang, runs it over its whole grid twice (buffers against their upper
+guard, then against their lower one), and reports, per kernel, whether
+every access stayed inside the buffers it was given, sized exactly as on
+the device (inputs, temporaries and the destination).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import os
+import subprocess
+
+import numpy as np
+
+import porch_amd as porch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CLANG = os.environ.get("PORCH_EMU_CXX", "/opt/rocm/llvm/bin/clang++")
+BUILD = os.path.join(HERE, "_build")
+
+
+def available() -> bool:
+    return os.path.exists(CLANG)
+
+
+def _input_floats(t) -> int:
+    if t.is_contiguous():
+        return int(np.prod(t.shape(), dtype=np.int64)) if len(t.shape()) else 1
+    return t.layout().span()
+
+
+def _program(source: str, name: str, sizes: list[int], grid, block: int) -> str:
+    args = ", ".join(f"b{i}" for i in range(len(sizes)))
+    decls = "".join(f"    float* b{i} = emu::guarded({n}, tail);\n" for i, n in enumerate(sizes))
+    return (
+        '#include "prelude.hpp"\n#include "runner.hpp"\n' + source +
+        "\nint main(int argc, char** argv) {\n"
+        "    const bool tail = argc > 1 && argv[1][0] == '1';\n" + decls +
+        f"    emu::run({{{grid[0]}, {grid[1]}, {grid[2]}}}, {block}, [&] {{ {name}({args}); }});\n"
+        '    std::puts("ok");\n    return 0;\n}\n'
+    )
+
+
+def run_kernel(source: str, name: str, sizes: list[int], grid, block: int = 256,
+               timeout: float = 120.0) -> tuple[bool, str]:
+    """Builds and runs one kernel over `grid` with guarded buffers of
+    `sizes` floats (its parameters in order); (stayed in bounds, detail)."""
+    os.makedirs(BUILD, exist_ok=True)
+    program = _program(source, name, sizes, grid, block)
+    key = hashlib.sha1(program.encode()).hexdigest()[:16]
+    cpp = os.path.join(BUILD, f"k_{key}.cpp")
+    exe = os.path.join(BUILD, f"k_{key}")
+    if not os.path.exists(exe):
+        with open(cpp, "w") as f:
+            f.write(program)
+        built = subprocess.run([CLANG, "-std=c++20", "-O1", "-pthread", "-w", "-I", HERE, cpp, "-o", exe + ".tmp"],
+                               capture_output=True, text=True, timeout=300)
+        if built.returncode != 0:
+            return False, "build: " + built.stderr[-2000:]
+        os.replace(exe + ".tmp", exe)
+    for placement in ("1", "0"):
+        try:
+            ran = subprocess.run([exe, placement], capture_output=True, text=True, timeout=timeout)
+        except subprocess.TimeoutExpired:
+            return False, f"timed out (placement {placement})"
+        if ran.returncode != 0 or "ok" not in ran.stdout:
+            return False, f"placement {placement}: exit {ran.returncode} {ran.stderr[-500:]}"
+    return True, ""
+
+
+def emulate(expr, timeout: float = 120.0) -> list[dict]:
+    """Per kernel of the plan: {"kind", "ok", "detail"}."""
+    expr = porch.tensor_expr(expr)
+    plan = porch.plan(expr)
+    _, _, _, inputs, _ = porch.serialize(expr._root)
+    input_floats = [max(_input_floats(t), 1) for t in inputs]
+    temps = [max(int(n), 1) for n in plan["temps"]]
+    out_floats = max(int(np.prod(plan["out_shape"], dtype=np.int64)) if plan["out_shape"] else 1, 1)
+    results = []
+    for i, k in enumerate(plan["kernels"]):
+        slots = input_floats + temps
+        dest = out_floats if k["dest"] == "output" else temps[int(k["dest"][4:])]
+        ok, detail = run_kernel(porch.kernel_source(expr, i), k["name"], slots[: k["slots"]] + [dest],
+                                k["grid"], k["block"], timeout)
+        results.append({"kind": k["kind"], "ok": ok, "detail": detail})
+    return results

@@ -1,0 +1,96 @@
+// CPU build of generated porch kernels — TEST INFRASTRUCTURE ONLY.
+//
+// Lets a generated HIP kernel source compile as host C++ (clang) and run
+// with one std::thread per work-item, so that every memory access it makes
+// can be checked on the CPU against the exact buffer sizes: the driver
+// places each buffer against an inaccessible guard region, and an access
+// outside a buffer faults in this process instead of on a GPU.  Values are
+// not the point (the oracle checks those); addresses are.
+//
+// Emulated: thread/block indices, __syncthreads (a barrier over the
+// block's threads), wave64 __shfl_xor and v_mfma_f32_32x32x2f32 (barriers
+// over the wave's 64 threads, operand layouts as on gfx950), LDS arrays
+// (function-local statics, shared by the block's threads; blocks run one
+// after another).  The rest of the device builtins map to host math.
+#pragma once
+
+#include <barrier>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+
+namespace emu {
+    struct dim3 {
+        unsigned x = 0, y = 0, z = 0;
+    };
+    inline thread_local dim3 thread_idx;
+    inline thread_local dim3 block_idx;
+    inline dim3 grid_dim;
+    inline dim3 block_dim;
+    inline std::barrier<>* block_barrier = nullptr;
+    inline std::barrier<>* wave_barrier[16] = {};
+    inline float wave_a[16][64];
+    inline float wave_b[16][64];
+
+    inline int wave() { return static_cast<int>(thread_idx.x / 64); }
+    inline int lane() { return static_cast<int>(thread_idx.x % 64); }
+    inline void syncthreads() { block_barrier->arrive_and_wait(); }
+
+    inline float shfl_xor(float v, int mask, int width) {
+        const int w = wave();
+        const int l = lane();
+        wave_a[w][l] = v;
+        wave_barrier[w]->arrive_and_wait();
+        const int src = ((l ^ mask) & (width - 1)) | (l & ~(width - 1));
+        const float r = wave_a[w][src];
+        wave_barrier[w]->arrive_and_wait();
+        return r;
+    }
+
+    typedef float v16 __attribute__((ext_vector_type(16)));
+
+    // v_mfma_f32_32x32x2f32: lane l holds A[l % 32][l / 32] and
+    // B[l / 32][l % 32]; accumulator register v of lane l is
+    // C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+    inline v16 mfma_32x32x2(float a, float b, v16 c) {
+        const int w = wave();
+        const int l = lane();
+        wave_a[w][l] = a;
+        wave_b[w][l] = b;
+        wave_barrier[w]->arrive_and_wait();
+        v16 out = c;
+        for (int v = 0; v < 16; ++v) {
+            const int i = 8 * (v / 4) + 4 * (l / 32) + v % 4;
+            const int j = l % 32;
+            out[v] = c[v] + wave_a[w][i] * wave_b[w][j] + wave_a[w][i + 32] * wave_b[w][j + 32];
+        }
+        wave_barrier[w]->arrive_and_wait();
+        return out;
+    }
+} // namespace emu
+
+#define threadIdx (emu::thread_idx)
+#define blockIdx (emu::block_idx)
+#define gridDim (emu::grid_dim)
+#define blockDim (emu::block_dim)
+#define __global__
+#define __device__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__ static
+#define __restrict__ __restrict
+#define __syncthreads() emu::syncthreads()
+#define __shfl_xor(v, m, w) emu::shfl_xor((v), (m), (w))
+#define __builtin_amdgcn_rcpf(x) (1.0f / (x))
+#define __builtin_amdgcn_exp2f(x) exp2f(x)
+#define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
+#define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu::mfma_32x32x2((a), (b), (c))
+
+struct __attribute__((aligned(16))) float4 {
+    float x, y, z, w;
+};
+struct __attribute__((aligned(8))) float2 {
+    float x, y;
+};
+inline float4 make_float4(float a, float b, float c, float d) { return {a, b, c, d}; }
+inline float2 make_float2(float a, float b) { return {a, b}; }

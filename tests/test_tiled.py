@@ -73,6 +73,15 @@ def select_in_store_phase(make, rows, cols, split):
     return porch.transpose(x) + porch.concat(u, v, 1)
 
 
+def transposed_concat_branch(make, rows, cols):
+    """concat(x1, transpose(x2), 1): the transposed leaf is staged in phase 1
+    but sits in the select's second branch, so it is loaded only where that
+    branch is taken (elsewhere its index runs before the start of x2)."""
+    x1 = make([rows, cols])
+    x2 = make([cols, rows])
+    return porch.concat(x1, porch.transpose(x2), 1) + 1.0
+
+
 # (builder, sizes, phase-1 vector type or None, hoisted select count, float4 stores)
 CASES = {
     "interleave_512x256": (interleaved_concat, (512, 256), "float4", 1, True),
@@ -89,6 +98,8 @@ CASES = {
     "concat_inside_100x68": (concat_inside_transpose, (100, 68), "float4", 1, True),
     "store_select_132x64_68": (select_in_store_phase, (132, 64, 68), "float4", 0, True),
     "store_select_132x64_70": (select_in_store_phase, (132, 64, 70), "float4", 0, False),
+    "concat_branch_300x4": (transposed_concat_branch, (300, 4), "float4", 0, True),
+    "concat_branch_130x6": (transposed_concat_branch, (130, 6), "float2", 0, False),
 }
 
 
