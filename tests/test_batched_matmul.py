@@ -189,3 +189,17 @@ def test_softmax_of_batched_scores(gpu):
     ref = host.evaluate(expr)
     out = gpu.materialize(expr).cpu().reshape(expr.shape())
     np.testing.assert_allclose(out, ref, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape_a, shape_b", [([2, 3, 0], [2, 0, 4]), ([0, 3, 5], [0, 5, 4]),
+                                              ([2, 0, 5], [2, 5, 4])])
+def test_empty_extents(gpu, shape_a, shape_b):
+    # an empty inner axis gives zeros (the sum of no products); an empty
+    # batch or row axis gives an empty result
+    a = gpu.tensor(shape_a, np.zeros(int(np.prod(shape_a)), np.float32))
+    b = gpu.tensor(shape_b, np.zeros(int(np.prod(shape_b)), np.float32))
+    out = gpu.materialize(gpu.batched_matmul(a, b) + 1.0)
+    expected_shape = (shape_a[0], shape_a[1], shape_b[2])
+    assert tuple(out.shape()) == expected_shape
+    assert np.array_equal(out.cpu().reshape(expected_shape), np.ones(expected_shape, np.float32))

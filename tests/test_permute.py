@@ -196,3 +196,10 @@ def test_large_batched_transpose_bit_exact(gpu):
     t = gpu.tensor(shape, x.reshape(-1))
     out = gpu.materialize(porch.permute(t, [0, 2, 1])).cpu().reshape(64, 512, 512)
     assert np.array_equal(out, np.transpose(x, (0, 2, 1)))
+
+
+@pytest.mark.gpu
+def test_permute_of_an_empty_tensor(gpu):
+    t = gpu.tensor([3, 0, 2], np.zeros(0, np.float32))
+    out = gpu.materialize(gpu.permute(t, [2, 0, 1]) * 2.0)
+    assert tuple(out.shape()) == (2, 3, 0) and out.cpu().size == 0

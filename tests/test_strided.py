@@ -146,3 +146,11 @@ def test_strided_operands_bit_exact(gpu):
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), i
     assert np.array_equal(gpu.materialize(gpu.matmul(at, b)).cpu().reshape(rows, 160),
                           (dense.astype(np.float64) @ b.cpu().reshape(cols, 160)).astype(np.float32))
+
+
+@pytest.mark.gpu
+def test_empty_strided_tensor(gpu):
+    storage = gpu.tensor([8], np.arange(8, dtype=np.float32)).device_data()
+    t = gpu.tensor(gpu.tensor_layout([4, 0], [2, 1], 3), storage)
+    assert t.numel() == 0 and t.cpu().size == 0
+    assert gpu.materialize(t + 1.0).cpu().size == 0
