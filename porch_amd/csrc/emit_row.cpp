@@ -3,7 +3,7 @@
 // a 256-thread block and a shared-memory tree (896-962): softmax becomes
 // four launches and about four reads of the input.  A row program runs the
 // whole row-space graph in one kernel: one wave64 per row (a workgroup per
-// row for rows longer than 4096), the row's leaves read once into
+// long row, a segment of a wave per short row), the row's leaves read once into
 // registers, each reduction folded in registers and finished with a wave
 // butterfly (plus LDS across waves in workgroup mode), and the outputs - or
 // the row's final reduction - written in the same pass.
@@ -82,7 +82,6 @@ namespace porch::cg {
         // 24.1 us, A/B in one process).
         const bool single_fold = r.reduce_output && r.reductions.empty();
         const bool block_mode = length >= 2048 && !(single_fold && length < 4096);
-        const int lanes = block_mode ? 256 : 64;
 
         // Pass roots: each reduction's producer, then the output.
         std::vector<int> pass_roots;
@@ -102,6 +101,26 @@ namespace porch::cg {
             }
         }
         const int width = (all_affine && uniform_selects && length % 4 == 0) ? 4 : 1;
+        // Lanes per row: the workgroup, or the wave - or, for rows shorter
+        // than a wave's 64 values (x width), the smallest power-of-two
+        // segment of lanes that covers the row, with 64 / seg rows per wave
+        // at once (softmax [262144, 32]: 8 rows per wave instead of 1, with
+        // 3 butterfly steps per reduction instead of 6).
+        int seg = 64;
+        if (!block_mode) {
+            seg = 1;
+            while (seg < 64 && static_cast<int64_t>(seg) * width < length) seg *= 2;
+        }
+        // Waves per workgroup in workgroup mode: 4, or up to 16 for rows
+        // beyond 16384 so that a lane holds at most 64 of the row's values
+        // and the row fits the register cache (read once).  Softmax
+        // [1024, 65536] otherwise reads every row three times.
+        int block_waves = 4;
+        if (block_mode) {
+            while (block_waves < 16 && length > static_cast<int64_t>(block_waves) * 64 * 64) block_waves *= 2;
+        }
+        const int lanes = block_mode ? 64 * block_waves : seg;
+        const int rows_per_seg_wave = block_mode ? 1 : 64 / seg; // rows a wave holds at once
         const int64_t per_chunk = static_cast<int64_t>(lanes) * width;
         const int64_t chunks = (length + per_chunk - 1) / per_chunk;
         const bool ragged = length % per_chunk != 0;
@@ -181,7 +200,7 @@ namespace porch::cg {
         };
         if (!plan_caches(false) && !plan_caches(true)) cached.clear();
 
-        const int64_t rows_per_group = block_mode ? 1 : 4;
+        const int64_t rows_per_group = block_mode ? 1 : 4 * rows_per_seg_wave;
         int64_t rows_per_wave = 1;
         if (!hoisted.empty()) {
             // Enough workgroups to fill the machine several times over; each
@@ -198,7 +217,7 @@ namespace porch::cg {
         kc.kind = "row";
         kc.name = "porch_row";
         kc.n_slots = r.n_slots;
-        kc.block = 256;
+        kc.block = block_mode ? static_cast<unsigned>(lanes) : 256;
         kc.grid_x = static_cast<unsigned>(std::min<int64_t>(groups, int64_t{1} << 22));
         const char* T = r.width.type();
         const std::vector<std::string> names = coordinate_names(rank);
@@ -207,7 +226,7 @@ namespace porch::cg {
         std::string& s = kc.source;
         s = kernel_prologue(r.n_slots, T);
         s += "__device__ __forceinline__ float porch_max(float a, float b) { return a > b ? a : b; }\n";
-        s += "extern \"C\" __global__ void __launch_bounds__(256) porch_row(" +
+        s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(kc.block) + ") porch_row(" +
              kernel_params(r.n_slots) + ") {\n";
         s += "    const int lane = threadIdx.x & 63;\n";
         s += "    const int wave = threadIdx.x >> 6;\n";
@@ -218,13 +237,21 @@ namespace porch::cg {
             // passes at least one barrier in between, so one barrier per
             // reduction suffices.
             s += "    __shared__ float red[2][" + std::to_string(std::max<size_t>(n_reductions, 1)) +
-                 "][4];\n";
+                 "][" + std::to_string(block_waves) + "];\n";
             s += "    const int tl = threadIdx.x;\n";
             s += "    int it = 0;\n";
         }
-        else {
+        else if (seg == 64) {
             s += "    const int tl = lane;\n";
         }
+        else {
+            s += "    const int tl = lane & " + std::to_string(seg - 1) + ";\n";
+            s += "    const int sub = lane / " + std::to_string(seg) + ";\n";
+        }
+        // With several rows per wave the last iteration may hold fewer rows
+        // than segments: `live` guards every access of a segment without one
+        // (the loop itself stays uniform across the wave).
+        const bool segmented = !block_mode && seg < 64;
         const std::string W = std::to_string(width);
         const std::string NC = std::to_string(chunks);
         for (const int id : cached) {
@@ -236,10 +263,16 @@ namespace porch::cg {
             code += indent + "for (int j = 0; j < " + NC + "; ++j) {\n";
             code += indent + "    const " + T + " " + qc + " = (" + T + ")(j * " +
                     std::to_string(lanes) + " + tl) * " + W + ";\n";
-            if (ragged) code += indent + "    if (" + qc + " < " + std::to_string(length) + ") {\n";
+            if (ragged && segmented)
+                code += indent + "    if (live && " + qc + " < " + std::to_string(length) + ") {\n";
+            else if (ragged)
+                code += indent + "    if (" + qc + " < " + std::to_string(length) + ") {\n";
+            else if (segmented)
+                code += indent + "    if (live) {\n";
         };
+        const bool guarded = ragged || segmented;
         auto chunk_close = [&](std::string& code, const std::string& indent) {
-            if (ragged) code += indent + "    }\n";
+            if (guarded) code += indent + "    }\n";
             code += indent + "}\n";
         };
 
@@ -301,6 +334,7 @@ namespace porch::cg {
         }
         if (!hoisted.empty()) {
             std::string code;
+            if (segmented) code += "    const bool live = true;\n";
             chunk_open(code, "    ");
             std::string body;
             emitter em(k, body, width);
@@ -321,9 +355,17 @@ namespace porch::cg {
             s += "    for (idx_t row = blockIdx.x; row < " + std::to_string(rows) +
                  "; row += gridDim.x) {\n";
         }
-        else {
+        else if (!segmented) {
             s += "    for (idx_t row = (idx_t)blockIdx.x * 4 + wave; row < " +
                  std::to_string(rows) + "; row += (idx_t)gridDim.x * 4) {\n";
+        }
+        else {
+            const std::string G = std::to_string(rows_per_seg_wave);
+            s += "    for (idx_t first = ((idx_t)blockIdx.x * 4 + wave) * " + G + "; first < " +
+                 std::to_string(rows) + "; first += (idx_t)gridDim.x * " + std::to_string(4 * rows_per_seg_wave) +
+                 ") {\n";
+            s += "        const idx_t row = first + sub;\n";
+            s += "        const bool live = row < " + std::to_string(rows) + ";\n";
         }
         {
             std::vector<bool> needed(row_shape.size(), true);
@@ -335,18 +377,26 @@ namespace porch::cg {
             std::string code;
             const std::string op = is_max ? "porch_max(" + acc + ", __shfl_xor(" + acc + ", m, 64))"
                                           : acc + " + __shfl_xor(" + acc + ", m, 64)";
-            code += "        #pragma unroll\n";
-            code += "        for (int m = 32; m >= 1; m >>= 1) " + acc + " = " + op + ";\n";
+            if (lanes > 1) {
+                code += "        #pragma unroll\n";
+                code += "        for (int m = " + std::to_string(std::min(lanes, 64) / 2) + "; m >= 1; m >>= 1) " +
+                        acc + " = " + op + ";\n";
+            }
             if (block_mode) {
                 const std::string slot = "red[it & 1][" + std::to_string(next_slot++) + "]";
                 code += "        if (lane == 0) " + slot + "[wave] = " + acc + ";\n";
                 code += "        __syncthreads();\n";
-                if (is_max)
-                    code += "        " + acc + " = porch_max(porch_max(" + slot + "[0], " + slot +
-                            "[1]), porch_max(" + slot + "[2], " + slot + "[3]));\n";
-                else
-                    code += "        " + acc + " = (" + slot + "[0] + " + slot + "[1]) + (" + slot +
-                            "[2] + " + slot + "[3]);\n";
+                // Pairwise over the wave partials, in a fixed order.
+                std::vector<std::string> terms;
+                for (int w = 0; w < block_waves; ++w) terms.push_back(slot + "[" + std::to_string(w) + "]");
+                while (terms.size() > 1) {
+                    std::vector<std::string> next;
+                    for (size_t t = 0; t + 1 < terms.size(); t += 2)
+                        next.push_back(is_max ? "porch_max(" + terms[t] + ", " + terms[t + 1] + ")"
+                                              : "(" + terms[t] + " + " + terms[t + 1] + ")");
+                    terms = next;
+                }
+                code += "        " + acc + " = " + terms[0] + ";\n";
             }
             return code;
         };
@@ -385,7 +435,7 @@ namespace porch::cg {
 
         auto make_emitter = [&](std::string& body, size_t pass) {
             auto em = std::make_unique<emitter>(k, body, width);
-            em->indent = ragged ? "                " : "            ";
+            em->indent = guarded ? "                " : "            ";
             em->declare_roots(row_roots);
             em->relaxed = [&](int id) { return relaxed[static_cast<size_t>(id)] != 0; };
             emitter* self = em.get();
@@ -457,6 +507,7 @@ namespace porch::cg {
         if (r.reduce_output) {
             s += fold_pass(out_pass, r.output, r.output_is_max, "acc_out");
             if (block_mode) s += "        if (threadIdx.x == 0) out[row] = acc_out;\n";
+            else if (segmented) s += "        if (tl == 0 && live) out[row] = acc_out;\n";
             else s += "        if (lane == 0) out[row] = acc_out;\n";
         }
         else {

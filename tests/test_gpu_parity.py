@@ -70,18 +70,50 @@ def test_view_chain_bit_exact(gpu, n):
 @pytest.mark.parametrize("size", [{"rows": 3, "cols": 7}, {"rows": 17, "cols": 256},
                                   {"rows": 64, "cols": 4100}, {"rows": 8, "cols": 12288},
                                   {"rows": 300, "cols": 2048}, {"rows": 50, "cols": 3000},
-                                  {"rows": 7, "cols": 2050}, {"rows": 8192, "cols": 4096}])
+                                  {"rows": 7, "cols": 2050}, {"rows": 8192, "cols": 4096},
+                                  # workgroups of 8 and 16 waves; 131072 exceeds the register cache
+                                  {"rows": 5, "cols": 33000}, {"rows": 3, "cols": 65536},
+                                  {"rows": 2, "cols": 131072}])
 def test_softmax_within_1e6(gpu, size):
     out, ref, _ = gpu_and_oracle(gpu, "softmax", size)
     assert_close(out, ref, 1e-6)
     assert np.allclose(out.sum(axis=1), 1.0, atol=2e-5)
 
 
+# short rows: several rows per wave (lane segments of 1 to 32), row counts
+# that leave the last wave's segments partly empty
+@pytest.mark.parametrize("cols", [1, 2, 3, 5, 8, 31, 32, 33, 64, 100, 128, 200, 255])
+def test_softmax_short_rows_within_1e6(gpu, cols):
+    size = {"rows": 1001, "cols": cols}
+    out, ref, _ = gpu_and_oracle(gpu, "softmax", size)
+    assert_close(out, ref, 1e-6)
+    assert np.allclose(out.sum(axis=1), 1.0, atol=2e-5)
+
+
+@pytest.mark.parametrize("cols", [1, 4, 7, 16, 40, 128, 260])
+def test_logistic_rowsum_short_rows_within_1e5(gpu, cols):
+    out, ref, _ = gpu_and_oracle(gpu, "logistic_rowsum", {"rows": 999, "cols": cols})
+    assert_close(out, ref, 1e-5)
+
+
+def test_short_row_sums_exact_on_integers(gpu):
+    # integer data: the segment butterflies must add every element once
+    rng = np.random.default_rng(17)
+    for cols in (1, 3, 8, 24, 64, 96):
+        x = rng.integers(-50, 50, size=(777, cols)).astype(np.float32)
+        t = gpu.tensor([777, cols], x.reshape(-1))
+        out = gpu.materialize(gpu.sum(t, 1)).cpu()
+        assert np.array_equal(out, x.sum(axis=1).astype(np.float32)), cols
+        mx = gpu.materialize(gpu.max(t, 1)).cpu()
+        assert np.array_equal(mx, x.max(axis=1)), cols
+
+
 # -- config 4: broadcast + logistic + row sum, 1e-5 relative -----------------
 
 @pytest.mark.parametrize("size", [{"rows": 5, "cols": 9}, {"rows": 33, "cols": 2048},
                                   {"rows": 16384, "cols": 2048}, {"rows": 4, "cols": 10000},
-                                  {"rows": 100, "cols": 3001}, {"rows": 4097, "cols": 2044}])
+                                  {"rows": 100, "cols": 3001}, {"rows": 4097, "cols": 2044},
+                                  {"rows": 3, "cols": 70000}])
 def test_logistic_rowsum_within_1e5(gpu, size):
     out, ref, _ = gpu_and_oracle(gpu, "logistic_rowsum", size)
     assert_close(out, ref, 1e-5)

@@ -65,6 +65,11 @@ def test_staged_leaf_under_a_concat_branch_is_guarded():
     ("view_chain", {"n": 130}),
     ("softmax", {"rows": 7, "cols": 2100}),
     ("softmax", {"rows": 33, "cols": 100}),
+    ("softmax", {"rows": 1001, "cols": 3}),
+    ("softmax", {"rows": 77, "cols": 32}),
+    ("logistic_rowsum", {"rows": 999, "cols": 1}),
+    ("logistic_rowsum", {"rows": 35, "cols": 40}),
+    ("softmax", {"rows": 3, "cols": 65536}),
     ("logistic_rowsum", {"rows": 9, "cols": 2052}),
     ("matmul_epilogue", {"m": 200, "k": 70, "n": 136}),
 ])
