@@ -1,10 +1,12 @@
-// Reductions over a non-last axis.  One lane per output element folds the
-// axis sequentially; lanes run along the output's contiguous dimension, so
-// each step of the fold is a coalesced read (the reference instead gives
-// every output its own 256-thread block, src/tensor.cpp:896-962).  When the
-// outputs alone cannot fill the machine, the axis is split into chunks
-// folded by separate workgroups (grid y) into partial results, which a
-// second pass combines in chunk order.
+// Reductions over a non-last axis.  Lanes run along the output's contiguous
+// dimension, so each step of a fold is a coalesced read (the reference
+// instead gives every output its own 256-thread block,
+// src/tensor.cpp:896-962).  When there are fewer than 64 output groups per
+// workgroup, the spare lanes become strands that fold interleaved rows of
+// the same outputs, and the strands' partials are combined through LDS.
+// When the outputs alone cannot fill the machine, the axis is split into
+// chunks folded by separate workgroups (grid y) into partial results,
+// which a second pass combines.
 
 #include "codegen.hpp"
 #include "emit_expr.hpp"
@@ -53,13 +55,29 @@ namespace porch::cg {
         }
     } // namespace
 
+    namespace {
+        // Workgroup layout: `cols` lanes along the output groups (a power of
+        // two up to 64, fewer when there are fewer groups) times
+        // 256 / cols strands, each strand folding every strands-th row of
+        // the axis.
+        int layout_cols(int64_t groups) {
+            int cols = 1;
+            while (cols < 64 && cols < groups) cols *= 2;
+            return cols;
+        }
+    } // namespace
+
     int64_t column_reduce_parts(const column_reduce_request& r, int compute_units) {
         const int64_t extent = r.shape[r.axis];
         const int64_t outputs = ir::numel(r.shape) / std::max<int64_t>(extent, 1);
         if (extent < 256 || outputs * extent < (int64_t{1} << 20)) return 1;
-        const int64_t groups = (outputs / lanes_width(r) + 255) / 256;
+        const int64_t groups = outputs / lanes_width(r);
+        const int cols = layout_cols(groups);
+        const int64_t strands = 256 / cols;
+        const int64_t workgroups = (groups + cols - 1) / cols;
         const int64_t target = static_cast<int64_t>(compute_units) * 4;
-        const int64_t parts = std::min(target / std::max<int64_t>(groups, 1), extent / 32);
+        // at least 4 rows per strand in each part
+        const int64_t parts = std::min(target / std::max<int64_t>(workgroups, 1), extent / (4 * strands));
         return std::max<int64_t>(parts, 1);
     }
 
@@ -76,17 +94,19 @@ namespace porch::cg {
         const int64_t outputs = ir::numel(out_shape);
         const int64_t extent = r.shape[r.axis];
         // 4 outputs per lane (128-bit loads and stores) where the leaves
-        // allow; the fold order per output is unchanged.
+        // allow.
         const size_t inner = inner_dim(r);
         const int width = lanes_width(r);
         const int64_t groups = outputs / width;
+        const int cols = layout_cols(groups);
+        const int strands = 256 / cols;
         kernel_code kc;
         kc.kind = "reduce.column";
         kc.name = "porch_reduce";
         kc.n_slots = r.n_slots;
         kc.block = 256;
         kc.grid_x = static_cast<unsigned>(
-            std::clamp<int64_t>((groups + 255) / 256, 1, int64_t{1} << 22)
+            std::clamp<int64_t>((groups + cols - 1) / cols, 1, int64_t{1} << 22)
         );
         const int64_t parts = std::max<int64_t>(r.parts, 1);
         const int64_t chunk = (extent + parts - 1) / parts;
@@ -94,14 +114,24 @@ namespace porch::cg {
         const char* T = r.width.type();
         std::vector<std::string> names;
         for (size_t d = 0; d < rank; ++d) names.push_back("q" + std::to_string(d));
+        const std::string W = std::to_string(width);
+        const std::string C = std::to_string(cols);
+        const std::string S = std::to_string(strands);
 
         std::string& s = kc.source;
         s = kernel_prologue(r.n_slots, T);
         s += "extern \"C\" __global__ void __launch_bounds__(256) porch_reduce(" +
              kernel_params(r.n_slots) + ") {\n";
-        s += "    for (idx_t g = (idx_t)blockIdx.x * 256 + threadIdx.x; g < " +
-             std::to_string(groups) + "; g += (idx_t)gridDim.x * 256) {\n";
-        s += "        const idx_t o = g * " + std::to_string(width) + ";\n";
+        if (strands > 1) s += "    __shared__ float partial[" + S + "][" + C + "][" + W + "];\n";
+        s += "    const int cl = threadIdx.x % " + C + ";\n";
+        s += "    const int strand = threadIdx.x / " + C + ";\n";
+        // The group loop is uniform across the workgroup (barriers inside);
+        // `live` marks lanes past the last group.
+        s += "    for (idx_t base = (idx_t)blockIdx.x * " + C + "; base < " + std::to_string(groups) +
+             "; base += (idx_t)gridDim.x * " + C + ") {\n";
+        s += "        const idx_t g = base + cl;\n";
+        s += "        const bool live = g < " + std::to_string(groups) + ";\n";
+        s += "        const idx_t o = g * " + W + ";\n";
         const std::vector<int64_t> ostr = ir::contiguous_strides(out_shape);
         for (size_t i = 0; i < out_dims.size(); ++i) {
             std::string value;
@@ -115,26 +145,26 @@ namespace porch::cg {
                  " = " + value + ";\n";
         }
         const std::string init = r.is_max ? "-PORCH_FLT_MAX" : "0.0f";
-        s += "        float acc[" + std::to_string(width) + "];\n";
-        s += "        #pragma unroll\n        for (int e = 0; e < " + std::to_string(width) +
-             "; ++e) acc[e] = " + init + ";\n";
-        // Unrolled so that several rows' loads are in flight at once; the
-        // fold itself stays in row order.
+        s += "        float acc[" + W + "];\n";
+        s += "        #pragma unroll\n        for (int e = 0; e < " + W + "; ++e) acc[e] = " + init + ";\n";
+        // Each strand folds rows strand, strand + strands, ... of its chunk
+        // in order; unrolled so that several rows' loads are in flight.
         const std::string qa = "q" + std::to_string(r.axis);
+        const std::string first = parts > 1 ? "(" + std::string(T) + ")blockIdx.y * " + std::to_string(chunk) : "0";
         if (parts > 1) {
-            s += std::string("        const ") + T + " first = (" + T + ")blockIdx.y * " +
-                 std::to_string(chunk) + ";\n";
+            s += std::string("        const ") + T + " first = " + first + ";\n";
             s += std::string("        const ") + T + " last = first + " + std::to_string(chunk) + " < " +
                  std::to_string(extent) + " ? first + " + std::to_string(chunk) + " : " +
                  std::to_string(extent) + ";\n";
-            s += "        #pragma unroll 8\n";
-            s += std::string("        for (") + T + " " + qa + " = first; " + qa + " < last; ++" + qa + ") {\n";
         }
         else {
-            s += "        #pragma unroll 8\n";
-            s += std::string("        for (") + T + " " + qa + " = 0; " + qa + " < " +
-                 std::to_string(extent) + "; ++" + qa + ") {\n";
+            s += std::string("        const ") + T + " first = 0;\n";
+            s += std::string("        const ") + T + " last = " + std::to_string(extent) + ";\n";
         }
+        s += "        if (live) {\n";
+        s += "        #pragma unroll 4\n";
+        s += std::string("        for (") + T + " " + qa + " = first + strand; " + qa + " < last; " + qa +
+             " += " + S + ") {\n";
         std::string body;
         emitter em(k, body, width);
         em.indent = "            ";
@@ -161,17 +191,37 @@ namespace porch::cg {
         };
         const std::vector<std::string> v = em.emit(r.producer);
         s += body;
+        auto combine = [&](const std::string& a, const std::string& b) {
+            return r.is_max ? a + " > " + b + " ? " + a + " : " + b : a + " + " + b;
+        };
         for (int e = 0; e < width; ++e) {
             const std::string a = "acc[" + std::to_string(e) + "]";
-            if (r.is_max) s += "            " + a + " = " + a + " > " + v[e] + " ? " + a + " : " + v[e] + ";\n";
-            else s += "            " + a + " += " + v[e] + ";\n";
+            s += "            " + a + " = " + combine(a, v[e]) + ";\n";
         }
-        s += "        }\n";
+        s += "        }\n        }\n";
         const std::string dst = parts > 1 ? "(idx_t)blockIdx.y * " + std::to_string(outputs) + " + o" : "o";
+        std::string result = "acc";
+        if (strands > 1) {
+            // Strand partials combined pairwise through LDS, in a fixed order.
+            s += "        #pragma unroll\n        for (int e = 0; e < " + W + "; ++e) partial[strand][cl][e] = acc[e];\n";
+            s += "        __syncthreads();\n";
+            s += "        #pragma unroll\n";
+            s += "        for (int h = " + std::to_string(strands / 2) + "; h >= 1; h >>= 1) {\n";
+            s += "            if (strand < h) {\n";
+            s += "                #pragma unroll\n                for (int e = 0; e < " + W + "; ++e)\n";
+            s += "                    partial[strand][cl][e] = " +
+                 combine("partial[strand][cl][e]", "partial[strand + h][cl][e]") + ";\n";
+            s += "            }\n            __syncthreads();\n        }\n";
+            result = "partial[0][cl]";
+        }
+        s += std::string("        if (") + (strands > 1 ? "strand == 0 && " : "") + "live) {\n";
         if (width == 4)
-            s += "        *reinterpret_cast<float4*>(out + " + dst + ") = make_float4(acc[0], acc[1], acc[2], acc[3]);\n";
+            s += "            *reinterpret_cast<float4*>(out + " + dst + ") = make_float4(" + result + "[0], " +
+                 result + "[1], " + result + "[2], " + result + "[3]);\n";
         else
-            s += "        out[" + dst + "] = acc[0];\n";
+            s += "            out[" + dst + "] = " + result + "[0];\n";
+        s += "        }\n";
+        if (strands > 1) s += "        __syncthreads();\n";
         s += "    }\n}\n";
         return kc;
     }
