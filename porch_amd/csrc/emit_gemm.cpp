@@ -233,23 +233,59 @@ namespace porch::cg {
             // LDS reads per MFMA and the B re-reads; used while they still
             // give every compute unit a tile (measured 2.7% faster at 4096^3).
             const int64_t tiles_n = (r.n + BN - 1) / BN;
-            const int bm =
-                (r.m >= 256 && ((r.m + 255) / 256) * tiles_n * r.batch >= r.compute_units) ? 256 : BM;
+            const int64_t steps = (r.k + BK - 1) / BK;
+            const operand_layout la = layout_of(r.a, true, r.m, r.k);
+            const operand_layout lb = layout_of(r.b, false, r.n, r.k);
+            const bool scheduled = la.vector && lb.vector;
+            // LDS stores of the next K-slice per wave, and whether they and
+            // the global loads fit between a step's MFMAs
+            auto ds_writes_of = [&](int rows) {
+                return (la.k_major ? 2 : 4) * (rows / 64) + (lb.k_major ? 2 : 4) * (BN / 64);
+            };
+            auto interleaves = [&](int rows) {
+                return scheduled && 4 * (rows / 64 + BN / 64) + 4 + ds_writes_of(rows) <= (BK / 2) * (rows / 64) * 2;
+            };
+            // A short K (at most 3 steps, K <= 48) with more tiles than
+            // resident workgroups (two per compute unit): the output stores
+            // cost more than the MFMAs, and a workgroup that computes, then
+            // stores, leaves the MFMA units idle while its stores drain.
+            // Persistent workgroups walk the tiles instead, keep the previous
+            // tile's accumulators and store one slice of them during each
+            // K-step of the current tile (the last step also loads the next
+            // tile's first K-slice), so the stores overlap the MFMAs
+            // (measured 11-20% faster at K = 16, 32 and 48).  From 4 steps
+            // on it stops paying: the next slice's loads wait (in order)
+            // behind the slice stores issued before them, and the 128-row
+            // tiles it needs cost more LDS reads per MFMA (K = 64: -4% to
+            // +6%; K = 128: +25%).  The stores go through a buffer resource
+            // whose range check drops out-of-range lanes (offset 2^31),
+            // which keeps them branch-free.
+            // Two accumulator sets need 128-row tiles (a wave's 64 x 64 block)
+            // to stay within the register budget of two workgroups per
+            // compute unit.
+            const int64_t resident = static_cast<int64_t>(std::max(r.compute_units, 1)) * 2;
+            const int64_t out_elems = r.batch * r.m * r.n;
+            const bool persistent = interleaves(BM) && ((r.m + BM - 1) / BM) * tiles_n * r.batch > resident &&
+                                    steps <= 3 && out_elems < (int64_t{1} << 29);
+            const int bm = persistent ? BM
+                           : (r.m >= 256 && ((r.m + 255) / 256) * tiles_n * r.batch >= r.compute_units) ? 256
+                                                                                                        : BM;
             const int ib = bm / 64; // 32-row MFMA blocks per wave
             const int64_t tiles_m = (r.m + bm - 1) / bm;
             const int64_t tiles = tiles_m * tiles_n;
             const int64_t total = tiles * r.batch; // workgroups: (batch entry, tile) pairs
-            const int64_t steps = (r.k + BK - 1) / BK;
-            const operand_layout la = layout_of(r.a, true, r.m, r.k);
-            const operand_layout lb = layout_of(r.b, false, r.n, r.k);
             const std::string IB = std::to_string(ib);
             const std::string HALF = std::to_string(bm / 2);
+            const int vmem = bm / 64 + BN / 64;
+            const int mfmas = (BK / 2) * ib * 2;
+            const int ds_writes = ds_writes_of(bm);
+            const bool interleave = interleaves(bm);
             kernel_code kc;
             kc.kind = "gemm.mfma";
             kc.name = "porch_gemm";
             kc.n_slots = r.n_slots;
             kc.block = 256;
-            kc.grid_x = static_cast<unsigned>(total);
+            kc.grid_x = static_cast<unsigned>(persistent ? resident : total);
             const char* T = r.width.type();
             std::string& s = kc.source;
             s = kernel_prologue(r.n_slots, T);
@@ -270,89 +306,191 @@ namespace porch::cg {
             // each XCD a contiguous band of tile rows so its L2 holds them.
             // (For a batched product the bands run over (entry, tile) pairs,
             // entry-major, so an XCD holds whole entries where it can.)
-            const std::string lin = r.batched ? "lin" : "tile";
-            if (total % 8 == 0) {
-                s += "    const int " + lin + " = (blockIdx.x % 8) * " + std::to_string(total / 8) +
-                     " + blockIdx.x / 8;\n";
-            }
-            else {
-                s += "    const int " + lin + " = blockIdx.x;\n";
-            }
-            if (r.batched) {
-                s += "    const idx_t qb = lin / " + std::to_string(tiles) + ";\n";
-                s += "    const int tile = lin % " + std::to_string(tiles) + ";\n";
-            }
-            s += "    const idx_t m0 = (idx_t)(tile / " + std::to_string(tiles_n) + ") * " +
-                 std::to_string(bm) + ";\n";
-            s += "    const idx_t n0 = (idx_t)(tile % " + std::to_string(tiles_n) + ") * " +
-                 std::to_string(BN) + ";\n";
-            auto base = [&r](const gemm_operand& op) {
-                std::string b = "a" + std::to_string(op.slot) + " + " + std::to_string(op.offset);
-                if (r.batched && op.stride_batch != 0)
-                    b += " + qb * " + std::to_string(op.stride_batch);
-                return b;
+            // Tile `raw` (a workgroup index, or a persistent workgroup's
+            // running index) -> m0, n0 (and qb), A, B with name suffix `sx`.
+            // With a grid that is a multiple of 8, raw % 8 is the XCD.
+            auto decode = [&](const std::string& raw, const std::string& sx, const std::string& ind) {
+                std::string d;
+                const std::string lin = r.batched ? "lin" + sx : "tile" + sx;
+                const std::string cast = raw != "blockIdx.x" ? "(int)" : ""; // an idx_t running index
+                if (total % 8 == 0)
+                    d += ind + "const int " + lin + " = " + cast + "(" + raw + " % 8) * " +
+                         std::to_string(total / 8) + " + " + (cast.empty() ? raw + " / 8" : cast + "(" + raw + " / 8)") +
+                         ";\n";
+                else
+                    d += ind + "const int " + lin + " = " + cast + raw + ";\n";
+                if (r.batched) {
+                    d += ind + "const idx_t qb" + sx + " = " + lin + " / " + std::to_string(tiles) + ";\n";
+                    d += ind + "const int tile" + sx + " = " + lin + " % " + std::to_string(tiles) + ";\n";
+                }
+                d += ind + "const idx_t m0" + sx + " = (idx_t)(tile" + sx + " / " + std::to_string(tiles_n) +
+                     ") * " + std::to_string(bm) + ";\n";
+                d += ind + "const idx_t n0" + sx + " = (idx_t)(tile" + sx + " % " + std::to_string(tiles_n) +
+                     ") * " + std::to_string(BN) + ";\n";
+                auto base = [&](const gemm_operand& op) {
+                    std::string b = "a" + std::to_string(op.slot) + " + " + std::to_string(op.offset);
+                    if (r.batched && op.stride_batch != 0)
+                        b += " + qb" + sx + " * " + std::to_string(op.stride_batch);
+                    return b;
+                };
+                d += ind + "const float* __restrict__ A" + sx + " = " + base(r.a) + ";\n";
+                d += ind + "const float* __restrict__ B" + sx + " = " + base(r.b) + ";\n";
+                return d;
             };
-            s += "    const float* __restrict__ A = " + base(r.a) + ";\n";
-            s += "    const float* __restrict__ B = " + base(r.b) + ";\n";
+            if (!persistent) s += decode("blockIdx.x", "", "    ");
             s += "    float rA[" + std::to_string(4 * (bm / 64)) + "];\n    float rB[8];\n";
             s += "    floatx16 acc[" + IB + "][2];\n";
-            s += "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n";
-            s += "        #pragma unroll\n        for (int j = 0; j < 2; ++j)\n";
-            s += "            #pragma unroll\n            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;\n";
+            const std::string zero_acc =
+                "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n"
+                "        #pragma unroll\n        for (int j = 0; j < 2; ++j)\n"
+                "            #pragma unroll\n            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;\n";
             std::string load_a, store_a, load_b, store_b;
             operand_code(load_a, store_a, "A", r.a, true, r.m, r.k, la, bm);
             operand_code(load_b, store_b, "B", r.b, false, r.n, r.k, lb, BN);
-            // prologue: tile 0
-            s += "    {\n        const idx_t k0 = 0;\n        const int nb = 0;\n";
+            if (!persistent) s += zero_acc;
+            // prologue: the first K-slice of the (first) tile
+            s += "    {\n";
+            if (persistent) s += decode("blockIdx.x", "", "        ");
+            s += "        const idx_t k0 = 0;\n        const int nb = 0;\n";
             s += load_a + load_b + store_a + store_b;
             s += "    }\n    __syncthreads();\n";
+            // Epilogue for the accumulator blocks u = 2 bi + bj in [lo, hi)
+            // of `accn` at tile origin (m0n, n0n, qbn).  Buffered: branch-free,
+            // with clamped coordinates for the epilogue's own loads and the
+            // store offset set out of the buffer's range for lanes outside
+            // the output.
+            auto epilogue = [&](const std::string& accn, const std::string& m0n, const std::string& n0n,
+                                const std::string& qbn, int lo, int hi, bool buffered) {
+                std::string e;
+                if (lo >= hi) return e;
+                const std::string M = std::to_string(r.m), N = std::to_string(r.n);
+                if (buffered) {
+                    e += "    #pragma unroll\n    for (int u = " + std::to_string(lo) + "; u < " + std::to_string(hi) +
+                         "; ++u)\n";
+                    e += "    #pragma unroll\n    for (int v = 0; v < 16; ++v) {\n";
+                    e += "        const int bi = u >> 1;\n        const int bj = u & 1;\n";
+                }
+                else {
+                    e += "    #pragma unroll\n    for (int bi = 0; bi < " + IB + "; ++bi)\n";
+                    e += "    #pragma unroll\n    for (int bj = 0; bj < 2; ++bj)\n";
+                    e += "    #pragma unroll\n    for (int v = 0; v < 16; ++v) {\n";
+                }
+                e += "        const idx_t q0 = " + m0n + " + wm * " + HALF +
+                     " + bi * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);\n";
+                e += "        const idx_t q1 = " + n0n + " + wn * 64 + bj * 32 + (lane & 31);\n";
+                std::string body;
+                emitter em(*r.expr, body, 1);
+                std::vector<std::string> names;
+                if (buffered) {
+                    e += "        const bool inb = q0 < " + M + " && q1 < " + N + ";\n";
+                    e += "        const idx_t e0 = inb ? q0 : (idx_t)0;\n";
+                    e += "        const idx_t e1 = inb ? q1 : (idx_t)0;\n";
+                    e += "        const float acc_v = " + accn + "[bi][bj][v];\n";
+                    em.indent = "        ";
+                    names = r.batched ? std::vector<std::string>{qbn, "e0", "e1"}
+                                      : std::vector<std::string>{"e0", "e1"};
+                }
+                else {
+                    e += "        if (q0 < " + M + " && q1 < " + N + ") {\n";
+                    e += "            const float acc_v = " + accn + "[bi][bj][v];\n";
+                    em.indent = "            ";
+                    names = r.batched ? std::vector<std::string>{qbn, "q0", "q1"}
+                                      : std::vector<std::string>{"q0", "q1"};
+                }
+                em.declare_roots({r.epilogue});
+                epilogue_emitter(em, r, names, "acc_v");
+                const std::string v = em.emit(r.epilogue)[0];
+                e += body;
+                const std::string i0 = buffered ? "e0" : "q0", i1 = buffered ? "e1" : "q1";
+                const std::string at = r.batched ? "(" + qbn + " * " + M + " + " + i0 + ") * " + N + " + " + i1
+                                                 : i0 + " * " + N + " + " + i1;
+                if (buffered) {
+                    e += "        const int off = inb ? (int)((" + at + ") * 4) : (int)0x80000000;\n";
+                    e += "        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, " + v +
+                         "), orsrc, off, 0, 0);\n";
+                    e += "    }\n";
+                }
+                else {
+                    e += "            out[" + at + "] = " + v + ";\n        }\n    }\n";
+                }
+                return e;
+            };
+            if (persistent) {
+                s += "    const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(out, 0, " +
+                     std::to_string(out_elems * 4) + ", 0x00020000);\n";
+                s += "    floatx16 accP[" + IB + "][2];\n";
+                s += "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n";
+                s += "        #pragma unroll\n        for (int j = 0; j < 2; ++j)\n";
+                s += "            #pragma unroll\n            for (int v = 0; v < 16; ++v) accP[i][j][v] = 0.0f;\n";
+                // the first tile has no predecessor: a row origin past the
+                // output masks every lane of its slices
+                s += "    idx_t m0p = " + std::to_string(r.m) + ";\n    idx_t n0p = 0;\n";
+                if (r.batched) s += "    idx_t qbp = 0;\n";
+                if (steps % 2 != 0) s += "    int phase = 0;\n";
+                s += "    for (idx_t rr = blockIdx.x; rr < " + std::to_string(total) + "; rr += gridDim.x) {\n";
+                s += decode("rr", "c", "    ");
+                s += "    const idx_t rn = rr + gridDim.x < " + std::to_string(total) + " ? rr + gridDim.x : rr;\n";
+                s += decode("rn", "x", "    ");
+            }
+            if (persistent) s += zero_acc;
             // With both operands on the 128-bit path the next tile's global
             // loads and LDS stores are issued in the same block as the
             // MFMAs, so the scheduler can interleave both with them (the last
-            // step reloads its own tile, in bounds, into the idle buffer);
-            // otherwise they are skipped on the last step.
-            const int vmem = bm / 64 + BN / 64;
-            const int mfmas = (BK / 2) * ib * 2;
-            const int ds_writes = (la.k_major ? 2 : 4) * (bm / 64) + (lb.k_major ? 2 : 4) * (BN / 64);
-            const bool scheduled = la.vector && lb.vector;
-            const bool interleave = scheduled && 4 * vmem + 4 + ds_writes <= mfmas;
-            s += "    for (int t = 0; t < " + std::to_string(steps) + "; ++t) {\n";
-            s += "        const int cb = t & 1;\n";
-            s += "        const int nb = cb ^ 1;\n";
-            if (interleave) {
-                s += "        const idx_t k0 = (idx_t)(t + 1 < " + std::to_string(steps) + " ? t + 1 : t) * " +
-                     std::to_string(BK) + ";\n";
-                s += "        {\n" + load_a + load_b + "        }\n";
+            // step reloads its own tile, in bounds, into the idle buffer, or
+            // loads a persistent workgroup's next tile); otherwise they are
+            // skipped on the last step.
+            std::string head;
+            if (persistent) {
+                head += steps % 2 != 0 ? "        const int cb = (phase + t) & 1;\n" : "        const int cb = t & 1;\n";
+                head += "        const int nb = cb ^ 1;\n";
+                head += "        const bool to_next = t + 1 == " + std::to_string(steps) + ";\n";
+                head += "        const idx_t k0 = to_next ? (idx_t)0 : (idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
+                head += "        {\n";
+                head += "        const idx_t m0 = to_next ? m0x : m0c;\n";
+                head += "        const idx_t n0 = to_next ? n0x : n0c;\n";
+                head += "        const float* __restrict__ A = to_next ? Ax : Ac;\n";
+                head += "        const float* __restrict__ B = to_next ? Bx : Bc;\n";
+                head += load_a + load_b + "        }\n";
             }
             else {
-                s += "        const idx_t k0 = (idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
-                s += "        const bool more = t + 1 < " + std::to_string(steps) + ";\n";
-                s += "        if (more) {\n" + load_a + load_b + "        }\n";
+                head += "        const int cb = t & 1;\n";
+                head += "        const int nb = cb ^ 1;\n";
+                if (interleave) {
+                    head += "        const idx_t k0 = (idx_t)(t + 1 < " + std::to_string(steps) + " ? t + 1 : t) * " +
+                            std::to_string(BK) + ";\n";
+                    head += "        {\n" + load_a + load_b + "        }\n";
+                }
+                else {
+                    head += "        const idx_t k0 = (idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
+                    head += "        const bool more = t + 1 < " + std::to_string(steps) + ";\n";
+                    head += "        if (more) {\n" + load_a + load_b + "        }\n";
+                }
             }
+            std::string step;
             // this lane's k parity and row inside each 32-row block
-            s += "        const int h = lane >> 5;\n";
-            s += "        const int li = lane & 31;\n";
-            s += "        float av[" + IB + "][8];\n        float bv[2][8];\n";
-            s += "        #pragma unroll\n        for (int b = 0; b < " + IB + "; ++b) {\n";
-            s += "            const float4 al = *reinterpret_cast<const float4*>(&As[cb][h][wm * " + HALF +
-                 " + b * 32 + li][0]);\n";
-            s += "            const float4 ah = *reinterpret_cast<const float4*>(&As[cb][h][wm * " + HALF +
-                 " + b * 32 + li][4]);\n";
-            s += "            av[b][0] = al.x; av[b][1] = al.y; av[b][2] = al.z; av[b][3] = al.w;\n";
-            s += "            av[b][4] = ah.x; av[b][5] = ah.y; av[b][6] = ah.z; av[b][7] = ah.w;\n";
-            s += "        }\n";
-            s += "        #pragma unroll\n        for (int b = 0; b < 2; ++b) {\n";
-            s += "            const float4 bl = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][0]);\n";
-            s += "            const float4 bh = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][4]);\n";
-            s += "            bv[b][0] = bl.x; bv[b][1] = bl.y; bv[b][2] = bl.z; bv[b][3] = bl.w;\n";
-            s += "            bv[b][4] = bh.x; bv[b][5] = bh.y; bv[b][6] = bh.z; bv[b][7] = bh.w;\n";
-            s += "        }\n";
-            s += "        #pragma unroll\n";
-            s += "        for (int st = 0; st < " + std::to_string(BK / 2) + "; ++st)\n";
-            s += "            #pragma unroll\n            for (int i = 0; i < " + IB + "; ++i)\n";
-            s += "                #pragma unroll\n                for (int j = 0; j < 2; ++j)\n";
-            s += "                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][st], bv[j][st], acc[i][j], 0, 0, 0);\n";
-            if (interleave) s += "        {\n" + store_a + store_b + "        }\n";
+            step += "        const int h = lane >> 5;\n";
+            step += "        const int li = lane & 31;\n";
+            step += "        float av[" + IB + "][8];\n        float bv[2][8];\n";
+            step += "        #pragma unroll\n        for (int b = 0; b < " + IB + "; ++b) {\n";
+            step += "            const float4 al = *reinterpret_cast<const float4*>(&As[cb][h][wm * " + HALF +
+                    " + b * 32 + li][0]);\n";
+            step += "            const float4 ah = *reinterpret_cast<const float4*>(&As[cb][h][wm * " + HALF +
+                    " + b * 32 + li][4]);\n";
+            step += "            av[b][0] = al.x; av[b][1] = al.y; av[b][2] = al.z; av[b][3] = al.w;\n";
+            step += "            av[b][4] = ah.x; av[b][5] = ah.y; av[b][6] = ah.z; av[b][7] = ah.w;\n";
+            step += "        }\n";
+            step += "        #pragma unroll\n        for (int b = 0; b < 2; ++b) {\n";
+            step += "            const float4 bl = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][0]);\n";
+            step += "            const float4 bh = *reinterpret_cast<const float4*>(&Bs[cb][h][wn * 64 + b * 32 + li][4]);\n";
+            step += "            bv[b][0] = bl.x; bv[b][1] = bl.y; bv[b][2] = bl.z; bv[b][3] = bl.w;\n";
+            step += "            bv[b][4] = bh.x; bv[b][5] = bh.y; bv[b][6] = bh.z; bv[b][7] = bh.w;\n";
+            step += "        }\n";
+            step += "        #pragma unroll\n";
+            step += "        for (int st = 0; st < " + std::to_string(BK / 2) + "; ++st)\n";
+            step += "            #pragma unroll\n            for (int i = 0; i < " + IB + "; ++i)\n";
+            step += "                #pragma unroll\n                for (int j = 0; j < 2; ++j)\n";
+            step += "                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][st], bv[j][st], acc[i][j], 0, 0, 0);\n";
+            if (interleave) step += "        {\n" + store_a + store_b + "        }\n";
             if (scheduled) {
                 // Instruction order for the scheduler: the 128-bit LDS reads
                 // first, then one of the next tile's global loads after every
@@ -362,54 +500,55 @@ namespace porch::cg {
                 // after nearly all MFMAs).  Then, after a gap of MFMAs that
                 // covers the loads' latency, one LDS store of the next tile
                 // after each MFMA, instead of all of them after the last
-                // MFMA (another 4% at 4096^3).
+                // MFMA (another 4% at 4096^3).  With the previous tile's
+                // stores in the same block the load groups name reads only
+                // (0x040); the stores fill in around them.
                 const int ds_reads = 2 * ib + 4;
-                s += "        __builtin_amdgcn_sched_group_barrier(0x100, " + std::to_string(ds_reads) + ", 0);\n";
+                const std::string vmem_mask = persistent ? "0x040" : "0x020";
+                step += "        __builtin_amdgcn_sched_group_barrier(0x100, " + std::to_string(ds_reads) + ", 0);\n";
                 for (int g = 0; g < vmem; ++g) {
-                    s += "        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);\n";
-                    s += "        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);\n";
+                    step += "        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);\n";
+                    step += "        __builtin_amdgcn_sched_group_barrier(" + vmem_mask + ", 1, 0);\n";
                 }
                 int rest = mfmas - 4 * vmem;
                 if (interleave) {
                     const int gap = std::min(16, rest - ds_writes);
-                    s += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(gap) + ", 0);\n";
+                    step += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(gap) + ", 0);\n";
                     for (int g = 0; g < ds_writes; ++g) {
-                        s += "        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);\n";
-                        s += "        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);\n";
+                        step += "        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);\n";
+                        step += "        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);\n";
                     }
                     rest -= gap + ds_writes;
                 }
                 if (rest > 0)
-                    s += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(rest) + ", 0);\n";
+                    step += "        __builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(rest) + ", 0);\n";
             }
-            if (!interleave) s += "        if (more) {\n" + store_a + store_b + "        }\n";
-            s += "        __syncthreads();\n";
-            s += "    }\n";
-            // epilogue
-            s += "    #pragma unroll\n    for (int bi = 0; bi < " + IB + "; ++bi)\n";
-            s += "    #pragma unroll\n    for (int bj = 0; bj < 2; ++bj)\n";
-            s += "    #pragma unroll\n    for (int v = 0; v < 16; ++v) {\n";
-            s += "        const idx_t q0 = m0 + wm * " + HALF +
-                 " + bi * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);\n";
-            s += "        const idx_t q1 = n0 + wn * 64 + bj * 32 + (lane & 31);\n";
-            s += "        if (q0 < " + std::to_string(r.m) + " && q1 < " + std::to_string(r.n) + ") {\n";
-            s += "            const float acc_v = acc[bi][bj][v];\n";
-            std::string body;
-            emitter em(*r.expr, body, 1);
-            em.indent = "            ";
-            em.declare_roots({r.epilogue});
-            const std::vector<std::string> names =
-                r.batched ? std::vector<std::string>{"qb", "q0", "q1"}
-                          : std::vector<std::string>{"q0", "q1"};
-            epilogue_emitter(em, r, names, "acc_v");
-            const std::string v = em.emit(r.epilogue)[0];
-            s += body;
-            if (r.batched)
-                s += "            out[(qb * " + std::to_string(r.m) + " + q0) * " + std::to_string(r.n) +
-                     " + q1] = " + v + ";\n";
-            else
-                s += "            out[q0 * " + std::to_string(r.n) + " + q1] = " + v + ";\n";
-            s += "        }\n    }\n}\n";
+            if (!interleave) step += "        if (more) {\n" + store_a + store_b + "        }\n";
+            step += "        __syncthreads();\n";
+            if (persistent) {
+                // steps unrolled, so each stores a fixed slice of the
+                // previous tile's accumulator blocks
+                for (int64_t t = 0; t < steps; ++t) {
+                    const int lo = static_cast<int>(t * 2 * ib / steps);
+                    const int hi = static_cast<int>((t + 1) * 2 * ib / steps);
+                    s += "    {\n        const int t = " + std::to_string(t) + ";\n" + head;
+                    s += epilogue("accP", "m0p", "n0p", "qbp", lo, hi, true);
+                    s += step + "    }\n";
+                }
+                if (steps % 2 != 0) s += "    phase += " + std::to_string(steps) + ";\n";
+                s += "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n";
+                s += "        #pragma unroll\n        for (int j = 0; j < 2; ++j) accP[i][j] = acc[i][j];\n";
+                s += "    m0p = m0c;\n    n0p = n0c;\n";
+                if (r.batched) s += "    qbp = qbc;\n";
+                s += "    }\n";
+                // the last tile's accumulators
+                s += epilogue("accP", "m0p", "n0p", "qbp", 0, 2 * ib, true);
+            }
+            else {
+                s += "    for (int t = 0; t < " + std::to_string(steps) + "; ++t) {\n" + head + step + "    }\n";
+                s += epilogue("acc", "m0", "n0", "qb", 0, 2 * ib, false);
+            }
+            s += "}\n";
             return kc;
         }
 

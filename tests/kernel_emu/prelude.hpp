@@ -9,7 +9,8 @@
 //
 // Emulated: thread/block indices, __syncthreads (a barrier over the
 // block's threads), wave64 __shfl_xor and v_mfma_f32_32x32x2f32 (barriers
-// over the wave's 64 threads, operand layouts as on gfx950), LDS arrays
+// over the wave's 64 threads, operand layouts as on gfx950), raw buffer
+// stores (range-checked against the resource's size), LDS arrays
 // (function-local statics, shared by the block's threads; blocks run one
 // after another).  The rest of the device builtins map to host math.
 #pragma once
@@ -67,6 +68,18 @@ namespace emu {
         wave_barrier[w]->arrive_and_wait();
         return out;
     }
+
+    // A raw buffer resource (stride 0): stores at byte offsets at or past
+    // num_records are dropped, as the hardware's range check does.
+    struct buffer_rsrc {
+        char* base;
+        uint32_t num_records;
+    };
+    inline void buffer_store_b32(unsigned int value, buffer_rsrc r, int offset) {
+        const uint32_t at = static_cast<uint32_t>(offset);
+        if (at >= r.num_records) return;
+        __builtin_memcpy(r.base + at, &value, 4);
+    }
 } // namespace emu
 
 #define threadIdx (emu::thread_idx)
@@ -85,6 +98,9 @@ namespace emu {
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu::mfma_32x32x2((a), (b), (c))
+#define __builtin_amdgcn_make_buffer_rsrc(p, stride, num, flags) \
+    emu::buffer_rsrc{reinterpret_cast<char*>(p), static_cast<uint32_t>(num)}
+#define __builtin_amdgcn_raw_buffer_store_b32(v, r, off, soff, aux) emu::buffer_store_b32((v), (r), (off) + (soff))
 
 struct __attribute__((aligned(16))) float4 {
     float x, y, z, w;

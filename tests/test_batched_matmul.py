@@ -137,6 +137,20 @@ def test_large_products_use_mfma_over_every_entry():
     assert kernel["grid"][0] == 16 * 4 * 4  # (entry, 128x128 tile) pairs
 
 
+def test_many_tiles_use_persistent_workgroups():
+    # more (entry, tile) pairs than two per compute unit: each workgroup
+    # walks tiles, prefetching its next tile during the current one's last step
+    for b, m, k, n in [(32, 1024, 32, 1024), (18, 1024, 40, 1024), (8, 2048, 16, 2048)]:
+        plan = porch.plan(plain(placeholder, b, m, k, n))
+        (kernel,) = plan["kernels"]
+        assert kernel["kind"] == "gemm.mfma" and kernel["grid"][0] == 512, (b, m, k, n)
+        assert "rr += gridDim.x" in porch.kernel_source(plain(placeholder, b, m, k, n), 0)
+    # exactly 512 tiles, or a K of 4 steps and more, keep one workgroup per tile
+    for expr in (porch.matmul(placeholder([2048, 32]), placeholder([32, 4096])),
+                 plain(placeholder, 32, 1024, 64, 1024)):
+        assert "rr += gridDim.x" not in porch.kernel_source(expr, 0)
+
+
 def test_shared_weight_has_no_batch_offset():
     source = porch.kernel_source(shared_weight(placeholder, 4, 256, 256, 256), 0)
     assert "const float* __restrict__ B = a1 + 0;" in source
@@ -176,6 +190,37 @@ def test_batched_real_values_within_float64_bound(gpu):
     # |sum error| <= k * eps * sum |x||y| for any summation order
     bound = k * np.finfo(np.float32).eps * np.matmul(np.abs(x).astype(np.float64), np.abs(y).astype(np.float64))
     assert np.all(np.abs(out - exact) <= bound)
+
+
+# shapes with more tiles than resident workgroups and a short K: even and
+# odd K-step counts (the LDS buffer parity carried across tiles), a ragged
+# K, ragged rows, a single step, and the rank-2 product with a transposed
+# operand
+PERSISTENT = [
+    (lambda make: with_epilogue(make, 18, 1024, 40, 1024)),
+    (lambda make: plain(make, 20, 1020, 36, 1024)),
+    (lambda make: shared_weight(make, 24, 1024, 32, 768)),
+    (lambda make: with_epilogue(make, 40, 512, 16, 516)),
+    (lambda make: porch.matmul(make([5116, 20]), porch.transpose(make([5120, 20]))) * 2.0),
+]
+
+
+@pytest.mark.gpu
+def test_persistent_products_bit_exact(gpu):
+    rng = np.random.default_rng(11)
+
+    def make(shape):
+        return gpu.tensor(list(shape), ints(shape, rng).reshape(-1))
+
+    for i, build in enumerate(PERSISTENT):
+        print("persistent case", i, flush=True)
+        expr = build(make)
+        kernel = gpu.plan(expr)["kernels"][-1]
+        assert kernel["kind"] == "gemm.mfma"
+        assert "rr += gridDim.x" in gpu.kernel_source(expr, len(gpu.plan(expr)["kernels"]) - 1), i
+        ref = host.evaluate(expr)
+        out = gpu.materialize(expr).cpu().reshape(expr.shape())
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), i
 
 
 @pytest.mark.gpu
