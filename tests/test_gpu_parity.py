@@ -80,6 +80,18 @@ def test_softmax_within_1e6(gpu, size):
     assert np.allclose(out.sum(axis=1), 1.0, atol=2e-5)
 
 
+def test_softmax_full_size_ulp_histogram(gpu):
+    # the workload's size: per-element distance to the oracle in ulp (the
+    # oracle's exp is std::exp, the kernel's a polynomial within 1 ulp)
+    out, ref, _ = gpu_and_oracle(gpu, "softmax", CONFIG_SIZES["softmax"])
+    d = ulp_distance(out, ref)
+    counts = {u: int((d == u).sum()) for u in range(4)}
+    counts[">3"] = int((d > 3).sum())
+    print("softmax [8192,4096] ulp histogram vs oracle:", counts, flush=True)
+    assert sum(counts.values()) == out.size
+    assert d.max() <= 8
+
+
 # short rows: several rows per wave (lane segments of 1 to 32), row counts
 # that leave the last wave's segments partly empty
 @pytest.mark.parametrize("cols", [1, 2, 3, 5, 8, 31, 32, 33, 64, 100, 128, 200, 255])
@@ -141,6 +153,26 @@ def test_matmul_epilogue_full_size_on_a_row_sample(gpu):
     assert_close(out[rows], ref, 1e-4)
     exact = np.maximum(a.reshape(m, k)[rows].astype(np.float64) @ b.reshape(k, n) + bias, 0.0) - 0.5
     assert np.abs(out[rows] - exact).max() < 5e-6
+
+
+def test_matmul_full_size_product_against_float64(gpu):
+    # the workload's A @ B before its epilogue, on a row sample, against a
+    # float64 GEMM: the largest absolute difference, and the largest as a
+    # fraction of the accumulation bound K * eps * sum |a| |b|
+    porch = gpu
+    size = CONFIG_SIZES["matmul_epilogue"]
+    a, b, _ = config_inputs("matmul_epilogue")
+    m, k, n = size["m"], size["k"], size["n"]
+    am, bm = a.reshape(m, k), b.reshape(k, n)
+    out = porch.materialize(porch.matmul(porch.tensor([m, k], a), porch.tensor([k, n], b))).cpu().reshape(m, n)
+    rows = np.array([0, 1, 2, 511, 777, 2048, 3333, 4000, 4095])
+    exact = am[rows].astype(np.float64) @ bm.astype(np.float64)
+    bound = k * np.finfo(np.float32).eps * (np.abs(am[rows]).astype(np.float64) @ np.abs(bm).astype(np.float64))
+    delta = np.abs(out[rows] - exact)
+    print(f"matmul 4096^3 pre-epilogue: max |delta| = {delta.max():.3e}, "
+          f"max |delta| / bound = {(delta / bound).max():.3e}", flush=True)
+    assert delta.max() < 5e-6
+    assert np.all(delta <= bound)
 
 
 # -- edge cases the reference's tests touch: empty, ragged, rank-3 ----------
