@@ -245,28 +245,27 @@ namespace porch::cg {
             auto interleaves = [&](int rows) {
                 return scheduled && 4 * (rows / 64 + BN / 64) + 4 + ds_writes_of(rows) <= (BK / 2) * (rows / 64) * 2;
             };
-            // A short K (at most 3 steps, K <= 48) with more tiles than
+            // A short K (at most 4 steps, K <= 64) with more tiles than
             // resident workgroups (two per compute unit): the output stores
-            // cost more than the MFMAs, and a workgroup that computes, then
-            // stores, leaves the MFMA units idle while its stores drain.
+            // cost about as much as the MFMAs, and a workgroup that computes,
+            // then stores, leaves the MFMA units idle while its stores drain.
             // Persistent workgroups walk the tiles instead, keep the previous
             // tile's accumulators and store one slice of them during each
-            // K-step of the current tile (the last step also loads the next
-            // tile's first K-slice), so the stores overlap the MFMAs
-            // (measured 11-20% faster at K = 16, 32 and 48).  From 4 steps
-            // on it stops paying: the next slice's loads wait (in order)
-            // behind the slice stores issued before them, and the 128-row
-            // tiles it needs cost more LDS reads per MFMA (K = 64: -4% to
-            // +6%; K = 128: +25%).  The stores go through a buffer resource
-            // whose range check drops out-of-range lanes (offset 2^31),
-            // which keeps them branch-free.
+            // K-step of the current tile (the last steps also load the next
+            // tile's first K-slices), so the stores overlap the MFMAs
+            // (measured 9-20% faster at K = 16 to 64).  From 6 steps on it
+            // stops paying (K = 96 and 128: 5-8% slower): the 128-row tiles
+            // it needs cost more LDS reads per MFMA, and the stores are a
+            // smaller share of the time.  The stores go through a buffer
+            // resource whose range check drops out-of-range lanes (offset
+            // 2^31), which keeps them branch-free.
             // Two accumulator sets need 128-row tiles (a wave's 64 x 64 block)
             // to stay within the register budget of two workgroups per
             // compute unit.
             const int64_t resident = static_cast<int64_t>(std::max(r.compute_units, 1)) * 2;
             const int64_t out_elems = r.batch * r.m * r.n;
             const bool persistent = interleaves(BM) && ((r.m + BM - 1) / BM) * tiles_n * r.batch > resident &&
-                                    steps <= 3 && out_elems < (int64_t{1} << 29);
+                                    steps <= 4 && out_elems < (int64_t{1} << 29);
             const int bm = persistent ? BM
                            : (r.m >= 256 && ((r.m + 255) / 256) * tiles_n * r.batch >= r.compute_units) ? 256
                                                                                                         : BM;
@@ -338,7 +337,26 @@ namespace porch::cg {
                 return d;
             };
             if (!persistent) s += decode("blockIdx.x", "", "    ");
-            s += "    float rA[" + std::to_string(4 * (bm / 64)) + "];\n    float rB[8];\n";
+            // Even step counts of a persistent kernel load two K-slices
+            // ahead, through two register sets: a slice's LDS store then
+            // waits only for loads issued a step earlier, behind the output
+            // stores of two steps before, not of the step before.
+            const bool ahead2 = persistent && steps % 2 == 0;
+            auto in_set = [](std::string code, int set) {
+                for (const char* name : {"rA[", "rB["}) {
+                    const std::string from{name};
+                    const std::string to = from.substr(0, 2) + std::to_string(set) + "[";
+                    for (size_t at = code.find(from); at != std::string::npos; at = code.find(from, at + to.size()))
+                        code.replace(at, from.size(), to);
+                }
+                return code;
+            };
+            if (ahead2)
+                for (int set = 0; set < 2; ++set)
+                    s += "    float rA" + std::to_string(set) + "[" + std::to_string(4 * (bm / 64)) + "];\n    float rB" +
+                         std::to_string(set) + "[8];\n";
+            else
+                s += "    float rA[" + std::to_string(4 * (bm / 64)) + "];\n    float rB[8];\n";
             s += "    floatx16 acc[" + IB + "][2];\n";
             const std::string zero_acc =
                 "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n"
@@ -352,7 +370,15 @@ namespace porch::cg {
             s += "    {\n";
             if (persistent) s += decode("blockIdx.x", "", "        ");
             s += "        const idx_t k0 = 0;\n        const int nb = 0;\n";
-            s += load_a + load_b + store_a + store_b;
+            if (ahead2) {
+                s += in_set(load_a + load_b + store_a + store_b, 0);
+                // and its second, held in registers
+                s += "        {\n        const idx_t k0 = " + std::to_string(BK) + ";\n";
+                s += in_set(load_a + load_b, 1) + "        }\n";
+            }
+            else {
+                s += load_a + load_b + store_a + store_b;
+            }
             s += "    }\n    __syncthreads();\n";
             // Epilogue for the accumulator blocks u = 2 bi + bj in [lo, hi)
             // of `accn` at tile origin (m0n, n0n, qbn).  Buffered: branch-free,
@@ -490,7 +516,11 @@ namespace porch::cg {
             step += "            #pragma unroll\n            for (int i = 0; i < " + IB + "; ++i)\n";
             step += "                #pragma unroll\n                for (int j = 0; j < 2; ++j)\n";
             step += "                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][st], bv[j][st], acc[i][j], 0, 0, 0);\n";
-            if (interleave) step += "        {\n" + store_a + store_b + "        }\n";
+            // the LDS stores of the next slice, then the schedule; the
+            // two-ahead persistent form picks its register set per step
+            const std::string step_compute = step;
+            step.clear();
+            const int stores_per_step = static_cast<int>((2 * ib + steps - 1) / steps) * 16;
             if (scheduled) {
                 // Instruction order for the scheduler: the 128-bit LDS reads
                 // first, then one of the next tile's global loads after every
@@ -510,6 +540,10 @@ namespace porch::cg {
                     step += "        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);\n";
                     step += "        __builtin_amdgcn_sched_group_barrier(" + vmem_mask + ", 1, 0);\n";
                 }
+                // the previous tile's output stores after this step's loads
+                if (ahead2)
+                    step += "        __builtin_amdgcn_sched_group_barrier(0x080, " + std::to_string(stores_per_step) +
+                            ", 0);\n";
                 int rest = mfmas - 4 * vmem;
                 if (interleave) {
                     const int gap = std::min(16, rest - ds_writes);
@@ -525,15 +559,38 @@ namespace porch::cg {
             }
             if (!interleave) step += "        if (more) {\n" + store_a + store_b + "        }\n";
             step += "        __syncthreads();\n";
+            const std::string step_schedule = step;
+            auto step_of = [&](const std::string& lds_stores) {
+                return step_compute + (interleave ? "        {\n" + lds_stores + "        }\n" : std::string()) +
+                       step_schedule;
+            };
+            step = step_of(store_a + store_b);
             if (persistent) {
                 // steps unrolled, so each stores a fixed slice of the
                 // previous tile's accumulator blocks
                 for (int64_t t = 0; t < steps; ++t) {
                     const int lo = static_cast<int>(t * 2 * ib / steps);
                     const int hi = static_cast<int>((t + 1) * 2 * ib / steps);
-                    s += "    {\n        const int t = " + std::to_string(t) + ";\n" + head;
-                    s += epilogue("accP", "m0p", "n0p", "qbp", lo, hi, true);
-                    s += step + "    }\n";
+                    s += "    {\n        const int t = " + std::to_string(t) + ";\n";
+                    if (ahead2) {
+                        // load slice t + 2 (of this tile or the next) into
+                        // set t % 2; store slice t + 1 from the other set
+                        const bool next = t + 2 >= steps;
+                        const std::string sx = next ? "x" : "c";
+                        s += "        const int cb = t & 1;\n        const int nb = cb ^ 1;\n        {\n";
+                        s += "        const idx_t k0 = " + std::to_string(((t + 2) % steps) * BK) + ";\n";
+                        s += "        const idx_t m0 = m0" + sx + ";\n        const idx_t n0 = n0" + sx + ";\n";
+                        s += "        const float* __restrict__ A = A" + sx + ";\n";
+                        s += "        const float* __restrict__ B = B" + sx + ";\n";
+                        s += in_set(load_a + load_b, static_cast<int>(t % 2)) + "        }\n";
+                        s += epilogue("accP", "m0p", "n0p", "qbp", lo, hi, true);
+                        s += step_of(in_set(store_a + store_b, static_cast<int>((t + 1) % 2))) + "    }\n";
+                    }
+                    else {
+                        s += head;
+                        s += epilogue("accP", "m0p", "n0p", "qbp", lo, hi, true);
+                        s += step + "    }\n";
+                    }
                 }
                 if (steps % 2 != 0) s += "    phase += " + std::to_string(steps) + ";\n";
                 s += "    #pragma unroll\n    for (int i = 0; i < " + IB + "; ++i)\n";

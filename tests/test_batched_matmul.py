@@ -140,14 +140,14 @@ def test_large_products_use_mfma_over_every_entry():
 def test_many_tiles_use_persistent_workgroups():
     # more (entry, tile) pairs than two per compute unit: each workgroup
     # walks tiles, prefetching its next tile during the current one's last step
-    for b, m, k, n in [(32, 1024, 32, 1024), (18, 1024, 40, 1024), (8, 2048, 16, 2048)]:
+    for b, m, k, n in [(32, 1024, 32, 1024), (18, 1024, 40, 1024), (8, 2048, 16, 2048), (16, 1024, 64, 1024)]:
         plan = porch.plan(plain(placeholder, b, m, k, n))
         (kernel,) = plan["kernels"]
         assert kernel["kind"] == "gemm.mfma" and kernel["grid"][0] == 512, (b, m, k, n)
         assert "rr += gridDim.x" in porch.kernel_source(plain(placeholder, b, m, k, n), 0)
-    # exactly 512 tiles, or a K of 4 steps and more, keep one workgroup per tile
+    # exactly 512 tiles, or a K of 5 steps and more, keep one workgroup per tile
     for expr in (porch.matmul(placeholder([2048, 32]), placeholder([32, 4096])),
-                 plain(placeholder, 32, 1024, 64, 1024)):
+                 plain(placeholder, 32, 1024, 80, 1024)):
         assert "rr += gridDim.x" not in porch.kernel_source(expr, 0)
 
 
@@ -192,11 +192,12 @@ def test_batched_real_values_within_float64_bound(gpu):
     assert np.all(np.abs(out - exact) <= bound)
 
 
-# shapes with more tiles than resident workgroups and a short K: even and
-# odd K-step counts (the LDS buffer parity carried across tiles), a ragged
-# K, ragged rows, a single step, and the rank-2 product with a transposed
-# operand
+# shapes with more tiles than resident workgroups and a short K: even K-step
+# counts (loads two slices ahead) and odd ones (the LDS buffer parity
+# carried across tiles), a ragged K, ragged rows, a single step, and the
+# rank-2 product with a transposed operand
 PERSISTENT = [
+    (lambda make: plain(make, 12, 1024, 64, 1024)),
     (lambda make: with_epilogue(make, 18, 1024, 40, 1024)),
     (lambda make: plain(make, 20, 1020, 36, 1024)),
     (lambda make: shared_weight(make, 24, 1024, 32, 768)),
