@@ -229,9 +229,6 @@ namespace porch::cg {
         }
 
         kernel_code emit_gemm_mfma(const gemm_request& r) {
-            // 256-row tiles (each wave 128 x 64: 4 x 2 MFMA blocks) halve the
-            // LDS reads per MFMA and the B re-reads; used while they still
-            // give every compute unit a tile (measured 2.7% faster at 4096^3).
             const int64_t tiles_n = (r.n + BN - 1) / BN;
             const int64_t steps = (r.k + BK - 1) / BK;
             const operand_layout la = layout_of(r.a, true, r.m, r.k);
@@ -266,6 +263,10 @@ namespace porch::cg {
             const int64_t out_elems = r.batch * r.m * r.n;
             const bool persistent = interleaves(BM) && ((r.m + BM - 1) / BM) * tiles_n * r.batch > resident &&
                                     steps <= 4 && out_elems < (int64_t{1} << 29);
+            // Otherwise 256-row tiles (each wave 128 x 64: 4 x 2 MFMA blocks)
+            // halve the LDS reads per MFMA and the B re-reads; used while
+            // they still give every compute unit a tile (measured 2.7%
+            // faster at 4096^3).
             const int bm = persistent ? BM
                            : (r.m >= 256 && ((r.m + 255) / 256) * tiles_n * r.batch >= r.compute_units) ? 256
                                                                                                         : BM;

@@ -33,24 +33,26 @@ def _input_floats(t) -> int:
     return t.layout().span()
 
 
-def _program(source: str, name: str, sizes: list[int], grid, block: int) -> str:
+def _program(source: str, name: str, sizes: list[int], grid, block: int, only=None) -> str:
     args = ", ".join(f"b{i}" for i in range(len(sizes)))
+    subset = ", {" + ", ".join(str(int(x)) for x in only) + "}" if only else ""
     decls = "".join(f"    float* b{i} = emu::guarded({n}, tail);\n" for i, n in enumerate(sizes))
     return (
         '#include "prelude.hpp"\n#include "runner.hpp"\n' + source +
         "\nint main(int argc, char** argv) {\n"
         "    const bool tail = argc > 1 && argv[1][0] == '1';\n" + decls +
-        f"    emu::run({{{grid[0]}, {grid[1]}, {grid[2]}}}, {block}, [&] {{ {name}({args}); }});\n"
+        f"    emu::run({{{grid[0]}, {grid[1]}, {grid[2]}}}, {block}, [&] {{ {name}({args}); }}{subset});\n"
         '    std::puts("ok");\n    return 0;\n}\n'
     )
 
 
 def run_kernel(source: str, name: str, sizes: list[int], grid, block: int = 256,
-               timeout: float = 120.0) -> tuple[bool, str]:
-    """Builds and runs one kernel over `grid` with guarded buffers of
-    `sizes` floats (its parameters in order); (stayed in bounds, detail)."""
+               timeout: float = 120.0, only=None) -> tuple[bool, str]:
+    """Builds and runs one kernel over `grid` (or only the block x indices
+    in `only`) with guarded buffers of `sizes` floats (its parameters in
+    order); (stayed in bounds, detail)."""
     os.makedirs(BUILD, exist_ok=True)
-    program = _program(source, name, sizes, grid, block)
+    program = _program(source, name, sizes, grid, block, only)
     key = hashlib.sha1(program.encode()).hexdigest()[:16]
     cpp = os.path.join(BUILD, f"k_{key}.cpp")
     exe = os.path.join(BUILD, f"k_{key}")
@@ -72,8 +74,10 @@ def run_kernel(source: str, name: str, sizes: list[int], grid, block: int = 256,
     return True, ""
 
 
-def emulate(expr, timeout: float = 120.0) -> list[dict]:
-    """Per kernel of the plan: {"kind", "ok", "detail"}."""
+def emulate(expr, timeout: float = 120.0, only=None) -> list[dict]:
+    """Per kernel of the plan: {"kind", "ok", "detail"}.  `only`: run just
+    these block x indices of each kernel (for persistent grids whose
+    workgroups each walk many tiles)."""
     expr = porch.tensor_expr(expr)
     plan = porch.plan(expr)
     _, _, _, inputs, _ = porch.serialize(expr._root)
@@ -85,6 +89,6 @@ def emulate(expr, timeout: float = 120.0) -> list[dict]:
         slots = input_floats + temps
         dest = out_floats if k["dest"] == "output" else temps[int(k["dest"][4:])]
         ok, detail = run_kernel(porch.kernel_source(expr, i), k["name"], slots[: k["slots"]] + [dest],
-                                k["grid"], k["block"], timeout)
+                                k["grid"], k["block"], timeout, only)
         results.append({"kind": k["kind"], "ok": ok, "detail": detail})
     return results

@@ -45,7 +45,10 @@ namespace emu {
         return f;
     }
 
-    inline void run(dim3 grid, unsigned block, const std::function<void()>& kernel) {
+    // Runs every block of `grid`, or only the x indices in `only` (the
+    // grid size seen by the kernel stays `grid`).
+    inline void run(dim3 grid, unsigned block, const std::function<void()>& kernel,
+                    std::vector<unsigned> only = {}) {
         grid_dim = grid;
         block_dim = {block, 1, 1};
         std::barrier<> blocks(static_cast<std::ptrdiff_t>(block));
@@ -62,8 +65,8 @@ namespace emu {
                 thread_idx = {t, 0, 0};
                 for (unsigned z = 0; z < grid.z; ++z)
                     for (unsigned y = 0; y < grid.y; ++y)
-                        for (unsigned x = 0; x < grid.x; ++x) {
-                            block_idx = {x, y, z};
+                        for (unsigned i = 0; i < (only.empty() ? grid.x : only.size()); ++i) {
+                            block_idx = {only.empty() ? i : only[i], y, z};
                             kernel();
                             blocks.arrive_and_wait();
                         }

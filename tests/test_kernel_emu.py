@@ -5,12 +5,14 @@ inaccessible guard regions (tests/kernel_emu).  An out-of-bounds read or
 write faults the emulation process instead of a GPU.
 
 Covers the benchmark graphs at small sizes, the tiled, permute, batched and
-strided cases of the other tests, seeded random graphs (views, concat,
+strided cases of the other tests, the persistent short-K products (on a
+subset of their workgroups), seeded random graphs (views, concat,
 reductions, products, strided leaves), and a regression: a transposed leaf
 in one branch of a concat is staged by the LDS-transpose kernel ahead of the
 select, and must be loaded only where the select takes its branch.
 """
 
+import re
 from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
@@ -19,6 +21,7 @@ import pytest
 import porch_amd as porch
 from tests.helpers import config_graph, config_shapes, placeholder, strided_placeholder
 from tests.kernel_emu import emulate as emu
+from tests.test_batched_matmul import PERSISTENT
 from tests.test_gpu_fuzz import random_graph, random_product
 from tests.test_permute import CASES as PERMUTE_CASES
 from tests.test_tiled import CASES as TILED_CASES, build_case
@@ -84,6 +87,36 @@ def test_tiled_and_permute_cases():
     with ThreadPoolExecutor(6) as pool:
         for results in pool.map(emu.emulate, exprs):
             assert all(r["ok"] for r in results), results
+
+
+def test_persistent_products_on_a_subset_of_workgroups():
+    # each persistent workgroup walks several tiles; the first and last
+    # workgroups (by index) reach the first tiles and the ragged last ones
+    # through the XCD mapping, and the loop's hand-over between tiles
+    exprs = [build(placeholder) for build in PERSISTENT]
+    for expr in exprs:
+        assert porch.plan(expr)["kernels"][-1]["grid"][0] == 512
+    with ThreadPoolExecutor(5) as pool:
+        for i, results in enumerate(pool.map(lambda e: emu.emulate(e, only=[0, 1, 7, 256, 505, 510, 511]), exprs)):
+            assert all(r["ok"] for r in results), (i, results)
+
+
+def test_subset_emulation_catches_a_planted_overrun():
+    # the last tile's prefetch of "the next tile" without its clamp reads
+    # past the operands, in the last workgroup only
+    expr = porch.tensor_expr(PERSISTENT[0](placeholder))
+    plan = porch.plan(expr)
+    kernel = plan["kernels"][0]
+    source = porch.kernel_source(expr, 0)
+    planted = re.sub(r"const idx_t rn = rr \+ gridDim\.x < \d+ \? rr \+ gridDim\.x : rr;",
+                     "const idx_t rn = rr + gridDim.x;", source)
+    assert planted != source
+    _, _, _, inputs, _ = porch.serialize(expr._root)
+    sizes = [int(np.prod(t.shape())) for t in inputs] + [int(np.prod(plan["out_shape"]))]
+    ok, _ = emu.run_kernel(planted, kernel["name"], sizes, kernel["grid"], kernel["block"], only=[511])
+    assert not ok
+    ok, detail = emu.run_kernel(source, kernel["name"], sizes, kernel["grid"], kernel["block"], only=[511])
+    assert ok, detail
 
 
 def strided_or_dense(shape, rng):
