@@ -224,6 +224,64 @@ def test_persistent_products_bit_exact(gpu):
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), i
 
 
+def random_persistent_product(rng, make):
+    """A product with more than 512 tiles and K of 4 to 64 (the persistent
+    kernel, which needs 128-bit operand loads: K and the contiguous extent
+    of each operand multiples of 4), ragged row counts, operands that are
+    plain, transposed or permuted views or shared weights, and a random
+    epilogue."""
+    k = 4 * int(rng.integers(1, 17))
+    if rng.integers(0, 3):
+        b, m, n = int(rng.integers(6, 40)), int(rng.integers(400, 1100)), 4 * int(rng.integers(100, 275))
+        b = max(b, 600 // (((m + 127) // 128) * ((n + 127) // 128)) + 1)
+        form = int(rng.integers(0, 3))
+        if form == 0:
+            expr = plain(make, b, m, k, n)
+        elif form == 1:
+            expr = shared_weight(make, b, m, k, n)
+        else:
+            expr = permuted_operands(make, b, m, k, n)
+    else:
+        transposed_a = bool(rng.integers(0, 2))
+        m = int(rng.integers(2900, 5200)) // (4 if transposed_a else 1) * (4 if transposed_a else 1)
+        n = 4 * int(rng.integers(725, 1300))
+        a = porch.transpose(make([k, m])) if transposed_a else make([m, k])
+        bt = porch.transpose(make([n, k])) if rng.integers(0, 2) else make([k, n])
+        expr = porch.matmul(a, bt)
+    if rng.integers(0, 2):
+        shape = expr.shape()
+        bias = porch.broadcast_to(make([1] * (len(shape) - 1) + [shape[-1]]), shape)
+        expr = porch.relu(expr + bias) - 2.0
+    return expr
+
+
+def test_random_persistent_products_plan_as_persistent():
+    rng = np.random.default_rng(12)
+    count = 0
+    for _ in range(16):
+        expr = random_persistent_product(rng, placeholder)
+        kernel = porch.plan(expr)["kernels"][-1]
+        if kernel["kind"] == "gemm.mfma" and "rr += gridDim.x" in porch.kernel_source(expr, len(porch.plan(expr)["kernels"]) - 1):
+            count += 1
+    assert count >= 10
+
+
+@pytest.mark.gpu
+def test_random_persistent_products_bit_exact(gpu):
+    rng = np.random.default_rng(13)
+
+    def make(shape):
+        return gpu.tensor(list(shape), ints(shape, rng).reshape(-1))
+
+    for trial in range(12):
+        expr = random_persistent_product(rng, make)
+        plan = gpu.plan(expr)
+        print("persistent fuzz", trial, expr.shape(), [k["grid"][0] for k in plan["kernels"]], flush=True)
+        ref = host.evaluate(expr)
+        out = gpu.materialize(expr).cpu().reshape(expr.shape())
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, plan)
+
+
 @pytest.mark.gpu
 def test_softmax_of_batched_scores(gpu):
     rng = np.random.default_rng(10)
