@@ -133,7 +133,11 @@ namespace porch::cg {
         // Row-invariant, column-varying loads are hoisted out of the row loop.
         std::vector<int> hoisted;
         const int64_t per_value = chunks * width;
-        const int64_t budget = 128; // cached floats per lane
+        // Cached floats per lane.  With 16-wave workgroups (128 VGPRs in
+        // all) a full cache spills: softmax [1024, 131072] spills 49 VGPRs,
+        // and still runs faster (305 us) than three uncached passes over
+        // HBM (362 us).
+        const int64_t budget = 128;
         if (rows > 1) {
             std::set<int> seen;
             for (const int root : pass_roots) {
@@ -258,8 +262,13 @@ namespace porch::cg {
             s += "    float c" + std::to_string(id) + "[" + NC + "][" + W + "];\n";
         }
 
+        // Chunk loops unroll fully when values live in per-chunk register
+        // arrays (cached or hoisted); otherwise by 8: a fully unrolled loop
+        // over many chunks issues all its loads at once and spills (softmax
+        // [512, 262144], 64 chunks: 68 VGPRs spilled).
+        const bool partial_unroll = cached.empty() && hoisted.empty() && chunks > 16;
         auto chunk_open = [&](std::string& code, const std::string& indent) {
-            code += indent + "#pragma unroll\n";
+            code += indent + (partial_unroll ? "#pragma unroll 8\n" : "#pragma unroll\n");
             code += indent + "for (int j = 0; j < " + NC + "; ++j) {\n";
             code += indent + "    const " + T + " " + qc + " = (" + T + ")(j * " +
                     std::to_string(lanes) + " + tl) * " + W + ";\n";
@@ -277,14 +286,23 @@ namespace porch::cg {
         };
 
         // A leaf whose every element is read exactly once by this kernel
-        // (no broadcast dimension) streams past the caches: non-temporal
-        // loads keep it from evicting data that is reused.
-        auto streaming = [&](const knode& n) {
+        // (no broadcast dimension, and held in registers or read by one
+        // pass only) streams past the caches: non-temporal loads keep it
+        // from evicting data that is reused.  A leaf that several passes
+        // read again (a row too long for the register cache) uses ordinary
+        // loads, so the later passes can hit L2 and the Infinity Cache.
+        std::vector<int> passes_reading(k.nodes.size(), 0);
+        for (const row_reduction& red : r.reductions)
+            for (const int id : k.postorder(red.producer)) ++passes_reading[id];
+        if (r.output >= 0)
+            for (const int id : k.postorder(r.output)) ++passes_reading[id];
+        auto streaming = [&](int id) {
+            const knode& n = k.at(id);
             if (!n.index.is_affine) return false;
             for (size_t d = 0; d < rank; ++d) {
                 if (r.shape[d] > 1 && n.index.w[d] == 0) return false;
             }
-            return true;
+            return passes_reading[id] <= 1 || std::find(cached.begin(), cached.end(), id) != cached.end();
         };
         // Outputs use ordinary stores: with non-temporal loads already
         // keeping the inputs out of the way, non-temporal stores measured
@@ -312,7 +330,7 @@ namespace porch::cg {
             }
             if (aligned) {
                 const std::string v = em.fresh("w");
-                if (streaming(n)) {
+                if (streaming(id)) {
                     em.line("const porch_v4f " + v + " = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" +
                             base + " + " + idx + "));");
                 }
