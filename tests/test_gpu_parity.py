@@ -71,9 +71,11 @@ def test_view_chain_bit_exact(gpu, n):
                                   {"rows": 64, "cols": 4100}, {"rows": 8, "cols": 12288},
                                   {"rows": 300, "cols": 2048}, {"rows": 50, "cols": 3000},
                                   {"rows": 7, "cols": 2050}, {"rows": 8192, "cols": 4096},
-                                  # workgroups of 8 and 16 waves; 131072 exceeds the register cache
+                                  # workgroups of 8 and 16 waves; from 131072 on the row exceeds the
+                                  # register cache and max and sum run as one online pass
                                   {"rows": 5, "cols": 33000}, {"rows": 3, "cols": 65536},
-                                  {"rows": 2, "cols": 131072}])
+                                  {"rows": 2, "cols": 131072}, {"rows": 3, "cols": 262147},
+                                  {"rows": 40, "cols": 200004}])
 def test_softmax_within_1e6(gpu, size):
     out, ref, _ = gpu_and_oracle(gpu, "softmax", size)
     assert_close(out, ref, 1e-6)
