@@ -139,3 +139,17 @@ def test_scalars_are_emitted_exactly():
         assert "f" in source
     inf_source = porch.kernel_source(x * float("inf"))
     assert "__uint_as_float(0x7f800000u)" in inf_source
+
+
+def test_long_softmax_rows_read_twice():
+    # rows within the register cache: one read of x; beyond it, max and sum
+    # share one pass, so two reads (not three), with ordinary loads
+    def reads(cols):
+        source = porch.kernel_source(porch.softmax(placeholder([4, cols]), 1))
+        return source.count("a0 + ("), "__builtin_nontemporal_load" in source, "acc_a" in source
+
+    assert reads(65536) == (1, True, False)
+    assert reads(262144) == (2, False, True)
+    # a plain sum of exp over such rows stays one streaming pass
+    source = porch.kernel_source(porch.sum(porch.exp(placeholder([4, 262144])), 1))
+    assert source.count("a0 + (") == 1 and "acc_a" not in source
