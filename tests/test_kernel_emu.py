@@ -73,6 +73,7 @@ def test_staged_leaf_under_a_concat_branch_is_guarded():
     ("logistic_rowsum", {"rows": 999, "cols": 1}),
     ("logistic_rowsum", {"rows": 35, "cols": 40}),
     ("softmax", {"rows": 3, "cols": 65536}),
+    ("softmax", {"rows": 2, "cols": 262148}),  # beyond the register cache: one online pass
     ("logistic_rowsum", {"rows": 9, "cols": 2052}),
     ("matmul_epilogue", {"m": 200, "k": 70, "n": 136}),
 ])
