@@ -390,14 +390,24 @@ namespace porch::cg {
         }
 
         size_t next_slot = 0;
+        // Lane reduction, lowest distance first: within a row of 16 lanes
+        // by DPP (quad permutations for distances 1 and 2, then the half-row
+        // and row mirrors, which pair lanes across groups that already hold
+        // one value each), across rows by ds_bpermute (__shfl_xor).  Every
+        // lane ends with the same value, as a + b == b + a.
         auto reduce_lanes = [&](const std::string& acc, bool is_max) {
             std::string code;
-            const std::string op = is_max ? "porch_max(" + acc + ", __shfl_xor(" + acc + ", m, 64))"
-                                          : acc + " + __shfl_xor(" + acc + ", m, 64)";
-            if (lanes > 1) {
-                code += "        #pragma unroll\n";
-                code += "        for (int m = " + std::to_string(std::min(lanes, 64) / 2) + "; m >= 1; m >>= 1) " +
-                        acc + " = " + op + ";\n";
+            auto combine = [&](const std::string& partner) {
+                return is_max ? "porch_max(" + acc + ", " + partner + ")" : acc + " + " + partner;
+            };
+            const int span = std::min(lanes, 64);
+            const char* dpp[] = {"0xB1", "0x4E", "0x141", "0x140"}; // distances 1, 2, 4, 8
+            for (int m = 1, i = 0; m < span; m *= 2, ++i) {
+                const std::string partner =
+                    m <= 8 ? "__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, " + acc +
+                                 "), " + dpp[i] + ", 0xF, 0xF, false))"
+                           : "__shfl_xor(" + acc + ", " + std::to_string(m) + ", 64)";
+                code += "        " + acc + " = " + combine(partner) + ";\n";
             }
             if (block_mode) {
                 const std::string slot = "red[it & 1][" + std::to_string(next_slot++) + "]";

@@ -8,7 +8,8 @@
 // not the point (the oracle checks those); addresses are.
 //
 // Emulated: thread/block indices, __syncthreads (a barrier over the
-// block's threads), wave64 __shfl_xor and v_mfma_f32_32x32x2f32 (barriers
+// block's threads), wave64 __shfl_xor, DPP row patterns and
+// v_mfma_f32_32x32x2f32 (barriers
 // over the wave's 64 threads, operand layouts as on gfx950), raw buffer
 // stores (range-checked against the resource's size), LDS arrays
 // (function-local statics, shared by the block's threads; blocks run one
@@ -19,6 +20,7 @@
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
 
 namespace emu {
     struct dim3 {
@@ -46,6 +48,24 @@ namespace emu {
         const float r = wave_a[w][src];
         wave_barrier[w]->arrive_and_wait();
         return r;
+    }
+
+    // DPP row patterns used by the kernels: quad_perm [1,0,3,2] and
+    // [2,3,0,1], row_half_mirror, row_mirror.
+    inline int update_dpp(int src, int ctrl) {
+        const int w = wave();
+        const int l = lane();
+        int from = l;
+        if (ctrl == 0xB1) from = l ^ 1;
+        else if (ctrl == 0x4E) from = l ^ 2;
+        else if (ctrl == 0x141) from = (l & ~7) | (7 - (l & 7));
+        else if (ctrl == 0x140) from = (l & ~15) | (15 - (l & 15));
+        else std::abort();
+        wave_a[w][l] = __builtin_bit_cast(float, src);
+        wave_barrier[w]->arrive_and_wait();
+        const float r = wave_a[w][from];
+        wave_barrier[w]->arrive_and_wait();
+        return __builtin_bit_cast(int, r);
     }
 
     typedef float v16 __attribute__((ext_vector_type(16)));
@@ -98,6 +118,7 @@ namespace emu {
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu::mfma_32x32x2((a), (b), (c))
+#define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu::update_dpp((src), (ctrl))
 #define __builtin_amdgcn_make_buffer_rsrc(p, stride, num, flags) \
     emu::buffer_rsrc{reinterpret_cast<char*>(p), static_cast<uint32_t>(num)}
 #define __builtin_amdgcn_raw_buffer_store_b32(v, r, off, soff, aux) emu::buffer_store_b32((v), (r), (off) + (soff))
