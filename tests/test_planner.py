@@ -153,3 +153,14 @@ def test_long_softmax_rows_read_twice():
     # a plain sum of exp over such rows stays one streaming pass
     source = porch.kernel_source(porch.sum(porch.exp(placeholder([4, 262144])), 1))
     assert source.count("a0 + (") == 1 and "acc_a" not in source
+
+
+def test_lane_reductions_use_dpp_within_rows_and_bpermute_across():
+    # a 32-column row takes an 8-lane segment: three DPP steps, no bpermute
+    short = porch.kernel_source(porch.sum(placeholder([1000, 32]), 1))
+    assert [c for c in ("0xB1", "0x4E", "0x141", "0x140") if c in short] == ["0xB1", "0x4E", "0x141"]
+    assert "__shfl_xor" not in short
+    # a full wave: four DPP steps, then distances 16 and 32 across rows
+    full = porch.kernel_source(porch.sum(placeholder([1000, 2048]), 1))
+    assert all(c in full for c in ("0xB1", "0x4E", "0x141", "0x140"))
+    assert "__shfl_xor(acc_out, 16, 64)" in full and "__shfl_xor(acc_out, 32, 64)" in full
