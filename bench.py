@@ -63,6 +63,8 @@ WORK = {
     "batched_transpose": ("hbm", 2 * 64 * 512 * 512 * 4),
     "heads_permute": ("hbm", 2 * 32 * 1024 * 16 * 128 * 4),
     "batched_matmul": ("mfma", 2 * 32 * 1024 ** 3),
+    "attention_scores": ("mfma", 2 * 16 * 4096 * 64 * 4096),
+    "vocab_softmax": ("hbm", 2 * 512 * 262144 * 4),
 }
 DESCRIPTION = {
     "elementwise": "(a + b) * 2 - 1, a, b fp32 [1048576]",
@@ -74,11 +76,13 @@ DESCRIPTION = {
     "batched_transpose": "permute(x, [0,2,1]), x fp32 [64,512,512]",
     "heads_permute": "permute(x, [0,2,1,3]), x fp32 [32,1024,16,128]",
     "batched_matmul": "relu(batched_matmul(A, B) + bcast(bias)) - 0.5, A, B fp32 [32,1024,1024]",
+    "attention_scores": "batched_matmul(q, k) * 0.125, q fp32 [16,4096,64], k fp32 [16,64,4096]",
+    "vocab_softmax": "softmax(x, 1), x fp32 [512,262144]",
 }
 # Input copies rotated through so that a step never re-reads cached data.
 ROTATION = {"elementwise": 48, "view_chain": 8, "softmax": 4, "logistic_rowsum": 6,
             "matmul_epilogue": 1, "copy": 2, "batched_transpose": 4, "heads_permute": 2,
-            "batched_matmul": 1}
+            "batched_matmul": 1, "attention_scores": 1, "vocab_softmax": 1}
 # Counter summaries (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) per workload.
 PROFILES = os.path.join(ROOT, "profiles")
 
@@ -287,6 +291,16 @@ def cpu_baseline(name: str, min_seconds: float = 10.0) -> dict:
                           porch.broadcast_to(tensors[2], [entries, 1024, 1024])) - 0.5
         sample = f"{entries} of the 32 batch entries per run (time x {32 // entries})"
         scale = 32 / entries
+    elif name == "attention_scores":
+        rows = 256  # 256 of the 4096 rows of one of the 16 entries; time scaled by 256
+        q, k = values
+        tensors[0]._state = porch._State([1, rows, 64], porch.device())
+        tensors[0]._state.storage = porch._Storage(None, q[: rows * 64])
+        tensors[1]._state = porch._State([1, 64, 4096], porch.device())
+        tensors[1]._state.storage = porch._Storage(None, k[: 64 * 4096])
+        expr = porch.batched_matmul(tensors[0], tensors[1]) * 0.125
+        sample = f"{rows} rows of 1 of the 16 entries per run (time x {16 * 4096 // rows})"
+        scale = 16 * 4096 / rows
     else:
         expr = config_graph(name, tensors)
     times = []

@@ -22,6 +22,14 @@ Three more measure the IR extensions (permute, batched_matmul):
   batched_matmul     relu(batched_matmul(A, B) + bias) - 0.5
                                          A, B ~ U(-1,1)/32 [32,1024,1024],
                                          bias ~ N(0,.01) [1,1,1024]
+
+Two more, not in the default run, measure shapes the others do not reach:
+  attention_scores   batched_matmul(q, k) * 0.125
+                                         q ~ U(-1,1) [16,4096,64], k ~ U(-1,1)
+                                         [16,64,4096] (a short K: the
+                                         persistent product kernel)
+  vocab_softmax      softmax(x, 1)       x ~ N(0,3) [512,262144], 1% set to +20
+                                         (rows beyond the register cache)
 """
 
 from __future__ import annotations
@@ -60,6 +68,14 @@ def config_inputs(name: str, size: dict | None = None) -> list[np.ndarray]:
         return [synth.uniform(b * m * k, 801, -1.0, 1.0) / np.float32(32.0),
                 synth.uniform(b * k * n, 802, -1.0, 1.0) / np.float32(32.0),
                 synth.normal(n, 803, 0.0, 0.01)]
+    if name == "attention_scores":
+        b, m, k, n = s["batch"], s["m"], s["k"], s["n"]
+        return [synth.uniform(b * m * k, 811, -1.0, 1.0), synth.uniform(b * k * n, 812, -1.0, 1.0)]
+    if name == "vocab_softmax":
+        rows, cols = s["rows"], s["cols"]
+        x = synth.normal(rows * cols, 901, 0.0, 3.0)
+        synth.replace(x, 902, 0.01, 20.0)
+        return [x]
     if name == "matmul_epilogue":
         m, k, n = s["m"], s["k"], s["n"]
         return [synth.uniform(m * k, 501, -1.0, 1.0) / np.float32(64.0),
@@ -78,6 +94,8 @@ CONFIG_SIZES = {
     "batched_transpose": {"batch": 64, "rows": 512, "cols": 512},
     "heads_permute": {"batch": 32, "seq": 1024, "heads": 16, "dim": 128},
     "batched_matmul": {"batch": 32, "m": 1024, "k": 1024, "n": 1024},
+    "attention_scores": {"batch": 16, "m": 4096, "k": 64, "n": 4096},
+    "vocab_softmax": {"rows": 512, "cols": 262144},
 }
 
 
@@ -103,6 +121,11 @@ def config_shapes(name: str, size: dict | None = None) -> list[list[int]]:
     if name == "batched_matmul":
         b, m, k, n = s["batch"], s["m"], s["k"], s["n"]
         return [[b, m, k], [b, k, n], [1, 1, n]]
+    if name == "attention_scores":
+        b, m, k, n = s["batch"], s["m"], s["k"], s["n"]
+        return [[b, m, k], [b, k, n]]
+    if name == "vocab_softmax":
+        return [[s["rows"], s["cols"]]]
     raise ValueError(name)
 
 
@@ -144,4 +167,10 @@ def config_graph(name: str, tensors, size: dict | None = None):
         a, b, bias = tensors
         shape = [s["batch"], s["m"], s["n"]]
         return porch.relu(porch.batched_matmul(a, b) + porch.broadcast_to(bias, shape)) - 0.5
+    if name == "attention_scores":
+        q, k = tensors
+        return porch.batched_matmul(q, k) * 0.125
+    if name == "vocab_softmax":
+        (x,) = tensors
+        return porch.softmax(x, 1)
     raise ValueError(name)
