@@ -296,6 +296,23 @@ def test_softmax_of_batched_scores(gpu):
 
 
 @pytest.mark.gpu
+def test_softmax_of_persistent_scores(gpu):
+    # the persistent product writes a temporary that the row program reads
+    rng = np.random.default_rng(14)
+
+    def make(shape):
+        return gpu.tensor(list(shape), ints(shape, rng).reshape(-1))
+
+    expr = attention_scores(make, 12, 1024, 64, 1024)
+    plan = gpu.plan(expr)
+    assert [k["kind"] for k in plan["kernels"]] == ["gemm.mfma", "row"]
+    assert "rr += gridDim.x" in gpu.kernel_source(expr, 0)
+    ref = host.evaluate(expr)
+    out = gpu.materialize(expr).cpu().reshape(expr.shape())
+    np.testing.assert_allclose(out, ref, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("shape_a, shape_b", [([2, 3, 0], [2, 0, 4]), ([0, 3, 5], [0, 5, 4]),
                                               ([2, 0, 5], [2, 5, 4])])
 def test_empty_extents(gpu, shape_a, shape_b):
