@@ -94,6 +94,29 @@ def test_softmax_full_size_ulp_histogram(gpu):
     assert d.max() <= 8
 
 
+@pytest.mark.parametrize("cols", [4096, 262147])
+def test_softmax_special_values_match_oracle(gpu, cols):
+    # rows with -inf entries (exp gives 0), one +inf (max is inf: inf - inf
+    # is NaN), one NaN (the sum is NaN), and plain rows, on a row held in
+    # registers and on one past the register cache (online max and sum)
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal((5, cols)).astype(np.float32)
+    x[0, ::7] = -np.inf
+    x[1, cols // 3] = np.inf
+    x[2, cols // 2] = np.nan
+    x[3, :] = -np.inf
+    x[3, 5] = 0.0
+    t = gpu.tensor([5, cols], x.reshape(-1))
+    expr = gpu.softmax(t, 1)
+    out = gpu.materialize(expr).cpu().reshape(5, cols)
+    ref = host.evaluate(expr)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    finite = ~np.isnan(ref)
+    np.testing.assert_allclose(out[finite], ref[finite], rtol=1e-6, atol=1e-7)
+    assert np.all(np.isnan(out[1])) and np.all(np.isnan(out[2]))
+    assert out[3, 5] == 1.0 and np.count_nonzero(out[3]) == 1
+
+
 # short rows: several rows per wave (lane segments of 1 to 32), row counts
 # that leave the last wave's segments partly empty
 @pytest.mark.parametrize("cols", [1, 2, 3, 5, 8, 31, 32, 33, 64, 100, 128, 200, 255])
