@@ -457,3 +457,25 @@ def test_mfma_gemm_operand_layouts(gpu, layout):
     # against the oracle (sequential fp32 sum): both within the bound, and
     # the epilogue's -0.25 cancels, so the comparison is absolute
     assert (np.abs(out - host.evaluate(expr)) <= 2e-5 * bound + 1e-7).all()
+
+
+def test_mfma_keeps_denormals(gpu):
+    # denormal operands (sums of denormals are exact: they are fixed point)
+    # and denormal products: the MFMA path must not flush them, as an IEEE
+    # fp32 multiply-add (the reference's loop) does not
+    porch = gpu
+    m, k, n = 256, 64, 256
+    rng = np.random.default_rng(21)
+    a = (rng.integers(1, 5, size=(m, k)) * np.float32(1e-40)).astype(np.float32)
+    b = rng.integers(1, 4, size=(k, n)).astype(np.float32)
+    expr = porch.matmul(porch.tensor([m, k], a.reshape(-1)), porch.tensor([k, n], b.reshape(-1)))
+    assert porch.plan(expr)["kernels"][0]["kind"] == "gemm.mfma"
+    out = porch.materialize(expr).cpu().reshape(m, n)
+    assert np.array_equal(out, host.evaluate(expr))
+    a2 = (rng.integers(1, 5, size=(m, k)) * np.float32(1e-20)).astype(np.float32)
+    b2 = (rng.integers(1, 4, size=(k, n)) * np.float32(1e-20)).astype(np.float32)
+    expr2 = porch.matmul(porch.tensor([m, k], a2.reshape(-1)), porch.tensor([k, n], b2.reshape(-1)))
+    out2 = porch.materialize(expr2).cpu().reshape(m, n)
+    ref2 = host.evaluate(expr2)
+    assert np.count_nonzero(out2) == out2.size
+    np.testing.assert_allclose(out2, ref2, rtol=1e-5)
