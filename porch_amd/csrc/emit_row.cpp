@@ -266,9 +266,17 @@ namespace porch::cg {
         // over many chunks issues all its loads at once and spills (softmax
         // [512, 262144], 64 chunks: 68 VGPRs spilled).
         const bool partial_unroll = cached.empty() && hoisted.empty() && chunks > 16;
-        auto chunk_open = [&](std::string& code, const std::string& indent) {
+        // Rows read from memory once per pass walk their chunks in
+        // alternate directions, so each pass starts on the chunks the
+        // previous one read last, which are the likeliest still cached.
+        int memory_passes = 0;
+        auto chunk_open = [&](std::string& code, const std::string& indent, bool row_pass = false) {
+            const bool reverse = row_pass && partial_unroll && memory_passes++ % 2 == 1;
             code += indent + (partial_unroll ? "#pragma unroll 8\n" : "#pragma unroll\n");
-            code += indent + "for (int j = 0; j < " + NC + "; ++j) {\n";
+            if (reverse)
+                code += indent + "for (int j = " + std::to_string(chunks - 1) + "; j >= 0; --j) {\n";
+            else
+                code += indent + "for (int j = 0; j < " + NC + "; ++j) {\n";
             code += indent + "    const " + T + " " + qc + " = (" + T + ")(j * " +
                     std::to_string(lanes) + " + tl) * " + W + ";\n";
             if (ragged && segmented)
@@ -510,7 +518,7 @@ namespace porch::cg {
         auto fold_pass = [&](size_t pass, int root, bool is_max, const std::string& acc) {
             std::string code;
             code += "        float " + acc + " = " + (is_max ? "-PORCH_FLT_MAX" : "0.0f") + ";\n";
-            chunk_open(code, "        ");
+            chunk_open(code, "        ", true);
             std::string body;
             auto em = make_emitter(body, pass);
             const std::vector<std::string> v = em->emit(root);
@@ -552,7 +560,7 @@ namespace porch::cg {
             std::string code;
             code += "        float acc_m = -PORCH_FLT_MAX;\n        float acc_a = -PORCH_FLT_MAX;\n"
                     "        float acc_s = 0.0f;\n";
-            chunk_open(code, "        ");
+            chunk_open(code, "        ", true);
             std::string body;
             auto em = make_emitter(body, pass);
             const std::vector<std::string> v = em->emit(root);
@@ -594,7 +602,7 @@ namespace porch::cg {
         }
         else {
             std::string code;
-            chunk_open(code, "        ");
+            chunk_open(code, "        ", true);
             std::string body;
             auto em = make_emitter(body, out_pass);
             const std::vector<std::string> v = em->emit(r.output);
