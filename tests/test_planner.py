@@ -150,6 +150,9 @@ def test_long_softmax_rows_read_twice():
 
     assert reads(65536) == (1, True, False)
     assert reads(262144) == (2, False, True)
+    # the second read walks the row backwards
+    source = porch.kernel_source(porch.softmax(placeholder([4, 262144]), 1))
+    assert source.count("for (int j = 63; j >= 0; --j)") == 1
     # a plain sum of exp over such rows stays one streaming pass
     source = porch.kernel_source(porch.sum(porch.exp(placeholder([4, 262144])), 1))
     assert source.count("a0 + (") == 1 and "acc_a" not in source
