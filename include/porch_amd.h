@@ -148,7 +148,8 @@ porch_status porch_launch_fused_reduction(
 #define PORCH_OP_EXP 17
 #define PORCH_OP_RECIPROCAL 18
 /* Rank-N axis permutation.  No counterpart in the reference, whose only
- * axis reordering is the rank-2 transpose (src/tensor.cpp:1142-1150); this
+ * axis reordering is the rank-2 transpose (src/tensor.cpp:424-438 for its
+ * shape rule, 562-571 for its index map, 1425-1429 for its builder); this
  * generalises it.  rank/dims hold the permutation: output dimension i is
  * operand dimension dims[i]. */
 #define PORCH_OP_PERMUTE 19

@@ -1,6 +1,7 @@
 // The extern "C" boundary declared in include/porch_amd.h.
 
 #include "porch_amd.h"
+#include "capi_internal.hpp"
 #include "disk_cache.hpp"
 
 #include "internal.hpp"
@@ -12,10 +13,6 @@
 #include <unordered_map>
 #include <stdexcept>
 #include <string>
-
-struct porch_buffer {
-    porch::hip_jit::device_buffer handle;
-};
 
 struct porch_code_object {
     std::shared_ptr<const porch::rt::code_object> object;
@@ -285,39 +282,8 @@ namespace {
             const auto begin = std::chrono::steady_clock::now();
             require(out != nullptr, "output pointer is null");
             *out = nullptr;
-            const std::string key = table_key(graph);
-            table_entry entry;
-            bool hit = false;
-            if (!key.empty()) {
-                std::scoped_lock lock{tables().mutex};
-                auto found = tables().entries.find(key);
-                if (found != tables().entries.end()) {
-                    entry = found->second;
-                    hit = true;
-                }
-            }
-            if (!hit) {
-                ir::graph g = validated(graph);
-                const ir::node& root = g.at(g.root());
-                if (root.is_scalar)
-                    throw std::invalid_argument(
-                        "scalar expression cannot materialize to a tensor");
-                entry.out_shape = root.out;
-                entry.n_inputs = g.n_inputs;
-                if (ir::checked_numel(root.out) > 0) {
-                    bool plan_hit = false;
-                    entry.plan = plan::lookup(ir::compact(g), &plan_hit);
-                    hit = plan_hit;
-                    if (!key.empty()) {
-                        std::scoped_lock lock{tables().mutex};
-                        // Bounded: a caller producing ever new tables (say,
-                        // changing shapes) must not grow this without end.
-                        // Entries are rebuilt cheaply from the plan cache.
-                        if (tables().entries.size() >= 4096) tables().entries.clear();
-                        tables().entries.emplace(key, entry);
-                    }
-                }
-            }
+            const capi::prepared_graph entry = capi::prepare(graph);
+            const bool hit = entry.hit;
             require(n_inputs >= entry.n_inputs, "graph needs more input buffers");
             require(n_inputs == 0 || inputs != nullptr, "inputs are null");
             write_shape(entry.out_shape, out_shape, capacity, out_rank);
@@ -327,13 +293,7 @@ namespace {
                 return;
             }
             try {
-                std::vector<rt::buffer_state*> buffers(static_cast<size_t>(n_inputs));
-                for (int32_t i = 0; i < n_inputs; ++i) {
-                    buffers[static_cast<size_t>(i)] =
-                        inputs[i] == nullptr
-                            ? nullptr
-                            : hip_jit::buffer_access::state(inputs[i]->handle).get();
-                }
+                std::vector<rt::buffer_state*> buffers = capi::input_states(inputs, n_inputs);
                 std::shared_ptr<rt::buffer_state> state = plan::run(
                     *entry.plan, buffers,
                     [](size_t bytes) -> std::shared_ptr<rt::buffer_state> {
@@ -363,6 +323,70 @@ namespace {
         });
     }
 } // namespace
+
+extern "C++" {
+namespace porch::capi {
+
+    porch_status guarded_call(const std::function<void()>& body) {
+        return guarded(body);
+    }
+
+    prepared_graph prepare(const porch_graph* graph) {
+        const std::string key = table_key(graph);
+        prepared_graph entry;
+        if (!key.empty()) {
+            std::scoped_lock lock{tables().mutex};
+            auto found = tables().entries.find(key);
+            if (found != tables().entries.end()) {
+                entry.plan = found->second.plan;
+                entry.out_shape = found->second.out_shape;
+                entry.n_inputs = found->second.n_inputs;
+                entry.hit = true;
+                return entry;
+            }
+        }
+        ir::graph g = validated(graph);
+        const ir::node& root = g.at(g.root());
+        if (root.is_scalar)
+            throw std::invalid_argument("scalar expression cannot materialize to a tensor");
+        table_entry table;
+        table.out_shape = root.out;
+        table.n_inputs = g.n_inputs;
+        if (ir::checked_numel(root.out) > 0) {
+            bool plan_hit = false;
+            table.plan = plan::lookup(ir::compact(g), &plan_hit);
+            entry.hit = plan_hit;
+            if (!key.empty()) {
+                std::scoped_lock lock{tables().mutex};
+                // Bounded: a caller producing ever new tables (say, changing
+                // shapes) must not grow this without end.  Entries are
+                // rebuilt cheaply from the plan cache.
+                if (tables().entries.size() >= 4096) tables().entries.clear();
+                tables().entries.emplace(key, table);
+            }
+        }
+        entry.plan = table.plan;
+        entry.out_shape = table.out_shape;
+        entry.n_inputs = table.n_inputs;
+        return entry;
+    }
+
+    std::vector<rt::buffer_state*> input_states(const porch_buffer* const* inputs, int32_t n_inputs) {
+        std::vector<rt::buffer_state*> buffers(static_cast<size_t>(std::max(n_inputs, 0)));
+        for (int32_t i = 0; i < n_inputs; ++i) {
+            buffers[static_cast<size_t>(i)] =
+                inputs[i] == nullptr ? nullptr : hip_jit::buffer_access::state(inputs[i]->handle).get();
+        }
+        return buffers;
+    }
+
+    void write_result_shape(const std::vector<int64_t>& shape, int64_t* out, int32_t capacity,
+                            int32_t* rank) {
+        write_shape(shape, out, capacity, rank);
+    }
+
+} // namespace porch::capi
+} // extern "C++"
 
 porch_status porch_materialize(const porch_graph* graph, const porch_buffer* const* inputs,
                                int32_t n_inputs, porch_buffer** out, int64_t* out_shape,

@@ -92,6 +92,15 @@ namespace porch::cg {
         // > 1: the axis is split into `parts` chunks (grid y); chunk g's
         // fold goes to out[g * outputs + o] for a second pass to combine.
         int64_t parts = 1;
+        // Max over the whole axis only: the reduction as the reference
+        // states it (`exact_producer` over `exact_shape`, reduced along
+        // `exact_axis`; for a second pass, the first pass's), evaluated in
+        // the reference's order for outputs whose order-free result may
+        // differ from it.  Null for a first pass of a split axis.
+        const kexpr* exact_expr = nullptr;
+        int exact_producer = -1;
+        std::vector<int64_t> exact_shape;
+        size_t exact_axis = 0;
     };
 
     kernel_code emit_column_reduce(const column_reduce_request& request);

@@ -359,6 +359,25 @@ __device__ __forceinline__ float porch_exp_flush(float x) {
 __device__ __forceinline__ float porch_exp_flush_finite(float x) {
     return porch_exp_flush_reduced(__builtin_fmaxf(x, -104.0f));
 }
+// Order-free max for folds and lane reductions (v_maximum3_f32): NaN if
+// either operand is NaN, and -0 < +0, so every grouping gives the same
+// value and a NaN anywhere reaches the result.
+__device__ __forceinline__ float porch_fmax(float a, float b) {
+    return __builtin_elementwise_maximum(a, b);
+}
+// The reference's max step, t = t > v ? t : v (src/tensor.cpp:849-851,
+// 939-958): NaN survives only as the right operand, and a tie between
+// +0 and -0 goes to the right operand.
+__device__ __forceinline__ float porch_refmax(float a, float b) {
+    return a > b ? a : b;
+}
+// Can a max reduction's order-free result differ from the reference's
+// block order?  Only for NaN (which survives there by position) and for a
+// +0 maximum (a -0 in the row may win the tie there).  A -0 maximum means
+// every zero is -0; any other value is unique.
+__device__ __forceinline__ bool porch_max_order_matters(float m) {
+    return m != m || __builtin_bit_cast(unsigned, m) == 0u;
+}
 )";
         }
     } // namespace

@@ -67,6 +67,85 @@ namespace porch::cg {
         }
     } // namespace
 
+    namespace {
+        // Outputs whose order-free max may differ from the reference's
+        // (porch_max_order_matters: a NaN, or a +0 maximum) are recomputed
+        // by the whole workgroup in the reference's block order
+        // (src/tensor.cpp:896-962): thread t folds axis positions t,
+        // t + 256, ... with t = t > v ? t : v from -FLT_MAX, and the 256
+        // partials go through the tree with strides 128, 64, ..., 1 (the
+        // first two within each lane of wave 0, the rest across its lanes).
+        // Every wave ballots the flags from the combined results in LDS, so
+        // the loop over flagged outputs is uniform; the result replaces the
+        // combined value before the store.
+        std::string exact_column_max(const column_reduce_request& r, const std::string& W,
+                                     const std::string& C, const char* T) {
+            const kexpr& k = *r.exact_expr;
+            const size_t rank = r.exact_shape.size();
+            std::vector<int64_t> out_shape;
+            std::vector<size_t> out_dims;
+            for (size_t d = 0; d < rank; ++d) {
+                if (d == r.exact_axis) continue;
+                out_shape.push_back(r.exact_shape[d]);
+                out_dims.push_back(d);
+            }
+            std::vector<std::string> names;
+            for (size_t d = 0; d < rank; ++d) names.push_back("q" + std::to_string(d));
+            const std::string qa = "q" + std::to_string(r.exact_axis);
+            std::string s;
+            s += "        #pragma unroll\n        for (int e = 0; e < " + W + "; ++e) {\n";
+            s += "            const bool xflag = lane < " + C + " && base + lane < " + std::to_string(
+                     ir::numel(out_shape) / std::stoll(W)) + " && porch_max_order_matters(partial[0][lane][e]);\n";
+            s += "            unsigned long long xmask = __ballot(xflag);\n";
+            s += "            while (xmask) {\n";
+            s += "                const int u = __builtin_ctzll(xmask);\n";
+            s += "                xmask &= xmask - 1;\n";
+            s += "                const idx_t xo = (base + u) * " + W + " + e;\n";
+            const std::vector<int64_t> ostr = ir::contiguous_strides(out_shape);
+            for (size_t i = 0; i < out_dims.size(); ++i) {
+                std::string value;
+                if (out_shape[i] == 1) value = "0";
+                else if (i == 0) value = "xo / " + std::to_string(ostr[i]);
+                else if (ostr[i] == 1) value = "xo % " + std::to_string(out_shape[i]);
+                else value = "(xo / " + std::to_string(ostr[i]) + ") % " + std::to_string(out_shape[i]);
+                s += std::string("                const ") + T + " q" + std::to_string(out_dims[i]) + " = " + value + ";\n";
+            }
+            s += "                float xf = -PORCH_FLT_MAX;\n";
+            s += std::string("                for (") + T + " " + qa + " = threadIdx.x; " + qa + " < " +
+                 std::to_string(r.exact_shape[r.exact_axis]) + "; " + qa + " += 256) {\n";
+            std::string body;
+            emitter em(k, body, 1);
+            em.indent = "                    ";
+            em.declare_roots({r.exact_producer});
+            em.load = [&](int id) {
+                const knode& n = k.at(id);
+                return std::vector<std::string>{"a" + std::to_string(n.slot) + "[" + index_text(n.index, names) + "]"};
+            };
+            em.condition = [&](const kcond& c) {
+                return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
+            };
+            em.row_value = [](int) -> std::string {
+                throw std::logic_error("row value in a column reduction");
+            };
+            const std::vector<std::string> v = em.emit(r.exact_producer);
+            em.line("xf = porch_refmax(xf, " + v[0] + ");");
+            s += body + "                }\n";
+            s += "                ex[threadIdx.x] = xf;\n";
+            s += "                __syncthreads();\n";
+            s += "                if (wave == 0) {\n";
+            s += "                    float xh = porch_refmax(porch_refmax(ex[lane], ex[lane + 128]),\n"
+                 "                                            porch_refmax(ex[lane + 64], ex[lane + 192]));\n";
+            for (int m = 32; m >= 1; m /= 2)
+                s += "                    xh = porch_refmax(xh, __shfl_xor(xh, " + std::to_string(m) + ", 64));\n";
+            s += "                    if (lane == 0) partial[0][u][e] = xh;\n";
+            s += "                }\n";
+            s += "                __syncthreads();\n";
+            s += "            }\n";
+            s += "        }\n";
+            return s;
+        }
+    } // namespace
+
     int64_t column_reduce_parts(const column_reduce_request& r, int compute_units) {
         const int64_t extent = r.shape[r.axis];
         const int64_t outputs = ir::numel(r.shape) / std::max<int64_t>(extent, 1);
@@ -123,6 +202,13 @@ namespace porch::cg {
         s += "extern \"C\" __global__ void __launch_bounds__(256) porch_reduce(" +
              kernel_params(r.n_slots) + ") {\n";
         if (strands > 1) s += "    __shared__ float partial[" + S + "][" + C + "][" + W + "];\n";
+        const bool exact = r.is_max && r.exact_expr != nullptr;
+        if (exact) {
+            if (strands < 2) throw std::logic_error("exact column max needs the strand partials in LDS");
+            s += "    __shared__ float ex[257];\n";
+            s += "    const int lane = threadIdx.x & 63;\n";
+            s += "    const int wave = threadIdx.x >> 6;\n";
+        }
         s += "    const int cl = threadIdx.x % " + C + ";\n";
         s += "    const int strand = threadIdx.x / " + C + ";\n";
         // The group loop is uniform across the workgroup (barriers inside);
@@ -191,8 +277,10 @@ namespace porch::cg {
         };
         const std::vector<std::string> v = em.emit(r.producer);
         s += body;
+        // Max folds are order-free (porch_fmax); outputs where the order
+        // can matter are recomputed in the reference's order below.
         auto combine = [&](const std::string& a, const std::string& b) {
-            return r.is_max ? a + " > " + b + " ? " + a + " : " + b : a + " + " + b;
+            return r.is_max ? "porch_fmax(" + a + ", " + b + ")" : a + " + " + b;
         };
         for (int e = 0; e < width; ++e) {
             const std::string a = "acc[" + std::to_string(e) + "]";
@@ -214,6 +302,7 @@ namespace porch::cg {
             s += "            }\n            __syncthreads();\n        }\n";
             result = "partial[0][cl]";
         }
+        if (exact) s += exact_column_max(r, W, C, T);
         s += std::string("        if (") + (strands > 1 ? "strand == 0 && " : "") + "live) {\n";
         if (width == 4)
             s += "            *reinterpret_cast<float4*>(out + " + dst + ") = make_float4(" + result + "[0], " +

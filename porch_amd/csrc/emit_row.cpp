@@ -228,7 +228,6 @@ namespace porch::cg {
 
         std::string& s = kc.source;
         s = kernel_prologue(r.n_slots, T);
-        s += "__device__ __forceinline__ float porch_max(float a, float b) { return a > b ? a : b; }\n";
         s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(kc.block) + ") porch_row(" +
              kernel_params(r.n_slots) + ") {\n";
         s += "    const int lane = threadIdx.x & 63;\n";
@@ -243,6 +242,10 @@ namespace porch::cg {
                  "][" + std::to_string(block_waves) + "];\n";
             s += "    const int tl = threadIdx.x;\n";
             s += "    int it = 0;\n";
+            bool any_max = r.reduce_output && r.output_is_max;
+            for (const row_reduction& red : r.reductions) any_max = any_max || red.is_max;
+            // Virtual-lane partials of a max taken in the reference's order.
+            if (any_max) s += "    __shared__ float ex[257];\n";
         }
         else if (seg == 64) {
             s += "    const int tl = lane;\n";
@@ -401,12 +404,14 @@ namespace porch::cg {
         // Lane reduction, lowest distance first: within a row of 16 lanes
         // by DPP (quad permutations for distances 1 and 2, then the half-row
         // and row mirrors, which pair lanes across groups that already hold
-        // one value each), across rows by ds_bpermute (__shfl_xor).  Every
-        // lane ends with the same value, as a + b == b + a.
+        // one value each), across rows by ds_bpermute (__shfl_xor).  Both
+        // combines are commutative (a + b == b + a; porch_fmax orders -0
+        // below +0 and returns NaN for any NaN), so every lane of a row ends
+        // with the same value, up to the payload of a NaN.
         auto reduce_lanes = [&](const std::string& acc, bool is_max) {
             std::string code;
             auto combine = [&](const std::string& partner) {
-                return is_max ? "porch_max(" + acc + ", " + partner + ")" : acc + " + " + partner;
+                return is_max ? "porch_fmax(" + acc + ", " + partner + ")" : acc + " + " + partner;
             };
             const int span = std::min(lanes, 64);
             const char* dpp[] = {"0xB1", "0x4E", "0x141", "0x140"}; // distances 1, 2, 4, 8
@@ -427,7 +432,7 @@ namespace porch::cg {
                 while (terms.size() > 1) {
                     std::vector<std::string> next;
                     for (size_t t = 0; t + 1 < terms.size(); t += 2)
-                        next.push_back(is_max ? "porch_max(" + terms[t] + ", " + terms[t + 1] + ")"
+                        next.push_back(is_max ? "porch_fmax(" + terms[t] + ", " + terms[t + 1] + ")"
                                               : "(" + terms[t] + " + " + terms[t + 1] + ")");
                     terms = next;
                 }
@@ -503,6 +508,113 @@ namespace porch::cg {
             return em;
         };
 
+        // A max whose order-free result may differ from the reference's
+        // (porch_max_order_matters: a NaN in the row, or a +0 maximum) is
+        // recomputed in the reference's block order (src/tensor.cpp:896-962):
+        // 256 virtual lanes, virtual lane t folding columns t, t + 256, ...
+        // with t = t > v ? t : v from -FLT_MAX, then the tree with strides
+        // 128, 64, ..., 1.  Lane tl of a row's `seg` lanes takes virtual
+        // lanes tl, tl + seg, ...: the tree's strides of seg and more combine
+        // within the lane, the smaller ones across lanes.  A workgroup row
+        // stages its 256 virtual partials in LDS and finishes in wave 0.  The
+        // branch is uniform over the row's lanes, and the result is the
+        // row leader's, so every lane holds the same bits.
+        auto leaf_fold = [&](const std::string& first, int root, const std::string& f,
+                             const std::string& indent, bool guard_live) {
+            std::string code = indent + "float " + f + " = -PORCH_FLT_MAX;\n";
+            if (guard_live) code += indent + "if (live)\n";
+            code += indent + "for (" + T + " " + qc + " = " + first + "; " + qc + " < " + std::to_string(length) +
+                    "; " + qc + " += 256) {\n";
+            std::string body;
+            emitter em(k, body, 1);
+            em.indent = indent + "    ";
+            em.declare_roots(row_roots);
+            em.relaxed = [&](int id) { return relaxed[static_cast<size_t>(id)] != 0; };
+            em.load = [&](int id) {
+                const knode& n = k.at(id);
+                return std::vector<std::string>{"a" + std::to_string(n.slot) + "[" + index_text(n.index, names) + "]"};
+            };
+            em.row_value = [](int row) { return "rv" + std::to_string(row); };
+            em.condition = [&](const kcond& c) {
+                return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
+            };
+            const std::vector<std::string> v = em.emit(root);
+            em.line(f + " = porch_refmax(" + f + ", " + v[0] + ");");
+            code += body + indent + "}\n";
+            return code;
+        };
+        // The reference's tree over virtual lanes lo, lo + step, ... (n of
+        // them, n a power of two) held in `leaf`: strides n/2, ..., 1 in
+        // units of `step`.  Leaves named "" are empty virtual lanes
+        // (-FLT_MAX); a pair of them folds away at generation time.
+        int tree_counter = 0;
+        auto lane_tree = [&](std::vector<std::string> leaf, const std::string& indent, std::string& code) {
+            for (size_t h = leaf.size() / 2; h >= 1; h /= 2) {
+                for (size_t i = 0; i < h; ++i) {
+                    if (leaf[i].empty() && leaf[i + h].empty()) continue;
+                    const std::string a = leaf[i].empty() ? "-PORCH_FLT_MAX" : leaf[i];
+                    const std::string b = leaf[i + h].empty() ? "-PORCH_FLT_MAX" : leaf[i + h];
+                    const std::string t = "xt" + std::to_string(tree_counter++);
+                    code += indent + "const float " + t + " = porch_refmax(" + a + ", " + b + ");\n";
+                    leaf[i] = t;
+                }
+            }
+            return leaf[0].empty() ? std::string("-PORCH_FLT_MAX") : leaf[0];
+        };
+        auto exact_max = [&](int root, const std::string& acc) {
+            // Rows sharing a wave take the path together when any of them
+            // needs it (its cross-lane steps then run with the whole wave
+            // active), and keep the result only where they do.
+            std::string code = segmented
+                ? "        if (__ballot(porch_max_order_matters(" + acc + ")) != 0) {\n"
+                  "            const bool xflag = porch_max_order_matters(" + acc + ");\n"
+                : "        if (porch_max_order_matters(" + acc + ")) {\n";
+            const std::string in = "            ";
+            if (block_mode) {
+                code += in + "if (threadIdx.x < 256) {\n";
+                code += leaf_fold("(" + std::string(T) + ")threadIdx.x", root, "xf", in + "    ", false);
+                code += in + "    ex[threadIdx.x] = xf;\n" + in + "}\n";
+                code += in + "__syncthreads();\n";
+                code += in + "if (wave == 0) {\n";
+                std::vector<std::string> leaf;
+                for (int r = 0; r < 4; ++r) {
+                    leaf.push_back("xl" + std::to_string(r));
+                    code += in + "    const float xl" + std::to_string(r) + " = ex[lane + " + std::to_string(64 * r) + "];\n";
+                }
+                code += in + "    float xh = " + lane_tree(leaf, in + "    ", code) + ";\n";
+                for (int m = 32; m >= 1; m /= 2)
+                    code += in + "    xh = porch_refmax(xh, __shfl_xor(xh, " + std::to_string(m) + ", 64));\n";
+                code += in + "    if (lane == 0) ex[256] = xh;\n" + in + "}\n";
+                code += in + "__syncthreads();\n";
+                code += in + acc + " = ex[256];\n";
+            }
+            else {
+                // Virtual lane tl + seg * r holds columns only while
+                // seg * r < length.
+                const int per_lane = 256 / seg;
+                std::vector<std::string> leaf(static_cast<size_t>(per_lane));
+                for (int r = 0; r < per_lane; ++r) {
+                    if (static_cast<int64_t>(seg) * r >= length) break;
+                    const std::string f = "xf" + std::to_string(r);
+                    code += leaf_fold("tl + " + std::to_string(seg * r), root, f, in, segmented);
+                    leaf[static_cast<size_t>(r)] = f;
+                }
+                code += in + "float xh = " + lane_tree(leaf, in, code) + ";\n";
+                for (int m = seg / 2; m >= 1; m /= 2)
+                    code += in + "xh = porch_refmax(xh, __shfl_xor(xh, " + std::to_string(m) + ", 64));\n";
+                const std::string result = "__shfl(xh, " + (seg == 64 ? std::string("0") : "lane & " + std::to_string(64 - seg)) + ", 64)";
+                if (segmented) {
+                    code += in + "const float xr = " + result + ";\n";
+                    code += in + "if (xflag) " + acc + " = xr;\n";
+                }
+                else {
+                    code += in + acc + " = " + result + ";\n";
+                }
+            }
+            code += "        }\n";
+            return code;
+        };
+
         auto store_caches = [&](emitter& em, size_t pass, int root) {
             for (const int c : cached) {
                 if (first_pass[c] != pass) continue;
@@ -524,12 +636,13 @@ namespace porch::cg {
             const std::vector<std::string> v = em->emit(root);
             store_caches(*em, pass, root);
             for (int e = 0; e < width; ++e) {
-                if (is_max) em->line(acc + " = porch_max(" + acc + ", " + v[e] + ");");
+                if (is_max) em->line(acc + " = porch_fmax(" + acc + ", " + v[e] + ");");
                 else em->line(acc + " += " + v[e] + ";");
             }
             code += body;
             chunk_close(code, "        ");
             code += reduce_lanes(acc, is_max);
+            if (is_max) code += exact_max(root, acc);
             return code;
         };
 
@@ -565,9 +678,9 @@ namespace porch::cg {
             auto em = make_emitter(body, pass);
             const std::vector<std::string> v = em->emit(root);
             std::string cm = v[0];
-            for (int e = 1; e < width; ++e) cm = "porch_max(" + cm + ", " + v[e] + ")";
+            for (int e = 1; e < width; ++e) cm = "porch_fmax(" + cm + ", " + v[e] + ")";
             em->line("const float cm = " + cm + ";");
-            em->line("acc_m = porch_max(acc_m, cm);");
+            em->line("acc_m = porch_fmax(acc_m, cm);");
             em->line("if (cm > acc_a + 64.0f) {");
             em->line("    acc_s = acc_s * porch_exp(acc_a - cm);");
             em->line("    acc_a = cm;");
@@ -576,6 +689,7 @@ namespace porch::cg {
             code += body;
             chunk_close(code, "        ");
             code += reduce_lanes("acc_m", true);
+            code += exact_max(root, "acc_m");
             code += "        acc_s = acc_s * porch_exp(acc_a - acc_m);\n";
             code += reduce_lanes("acc_s", false);
             return code;

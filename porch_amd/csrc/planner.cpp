@@ -405,6 +405,12 @@ namespace porch::plan {
                 const int64_t outputs = ir::numel(n.out);
                 const int64_t parts = cg::column_reduce_parts(r, compute_units);
                 if (parts < 2) {
+                    if (r.is_max) {
+                        r.exact_expr = &k;
+                        r.exact_producer = producer;
+                        r.exact_shape = shape;
+                        r.exact_axis = r.axis;
+                    }
                     add_step(cg::emit_column_reduce(r), dest);
                     return;
                 }
@@ -428,6 +434,12 @@ namespace porch::plan {
                 c.is_max = r.is_max;
                 c.n_slots = n_slots();
                 c.width = width;
+                if (r.is_max) {
+                    c.exact_expr = &k;
+                    c.exact_producer = producer;
+                    c.exact_shape = shape;
+                    c.exact_axis = r.axis;
+                }
                 add_step(cg::emit_column_reduce(c), dest);
             }
 
@@ -585,79 +597,138 @@ namespace porch::plan {
         cache().entries.clear();
     }
 
+    namespace {
+        void check_inputs(const graph_plan& plan, const std::vector<rt::buffer_state*>& inputs) {
+            if (static_cast<int>(inputs.size()) < plan.n_inputs) {
+            throw std::invalid_argument("graph needs more input buffers");
+        }
+            for (int i = 0; i < plan.n_inputs; ++i) {
+                const int64_t need = plan.input_elems[static_cast<size_t>(i)];
+                const rt::buffer_state* in = inputs[static_cast<size_t>(i)];
+                const size_t have = in == nullptr ? 0 : in->bytes;
+                if (need > 0 && have < static_cast<size_t>(need) * sizeof(float)) {
+                    throw std::invalid_argument(
+                        have == 0 ? "GPU kernel input is empty"
+                                  : "input device buffer is too small"
+                    );
+                }
+            }
+        }
+
+        // Loads the plan's modules (once) and orders the inputs' producers
+        // before work on `s`.
+        void prepare_launch(graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
+                            const std::shared_ptr<rt::stream>& s) {
+            {
+                std::scoped_lock lock{plan.load_mutex};
+                if (!plan.loaded) {
+                    for (step& st : plan.steps)
+                        st.kernel = rt::load_kernel(st.object, st.code.name);
+                    plan.loaded = true;
+                }
+            }
+            for (int i = 0; i < plan.n_inputs; ++i) {
+                rt::buffer_state* in = inputs[static_cast<size_t>(i)];
+                if (in != nullptr && in->bytes > 0) in->before_read(s);
+            }
+        }
+
+        // The plan's kernels in order: slot i < n_inputs is input i, the
+        // rest are the temporaries at `temps`, and each step writes `out`
+        // or a temporary.
+        void launch_steps(const graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
+                          void* out, const std::vector<void*>& temps, const rt::stream& s,
+                          hip::event_t start, hip::event_t stop) {
+            std::vector<void*> pointers;
+            std::vector<void*> params;
+            for (size_t index = 0; index < plan.steps.size(); ++index) {
+                const step& st = plan.steps[index];
+                const int slots = st.code.n_slots;
+                pointers.assign(static_cast<size_t>(slots) + 1, nullptr);
+                for (int i = 0; i < slots; ++i) {
+                    if (i < plan.n_inputs) {
+                        rt::buffer_state* in = inputs[static_cast<size_t>(i)];
+                        pointers[i] = in == nullptr ? nullptr : in->ptr;
+                    }
+                    else {
+                        const size_t t = static_cast<size_t>(i - plan.n_inputs);
+                        pointers[i] = t < temps.size() ? temps[t] : nullptr;
+                    }
+                }
+                pointers[slots] = st.dest.what == arg_ref::kind::output
+                                      ? out
+                                      : temps[static_cast<size_t>(st.dest.index)];
+                params.assign(pointers.size(), nullptr);
+                for (size_t i = 0; i < pointers.size(); ++i) params[i] = &pointers[i];
+                rt::launch(st.kernel, st.code.grid_x, st.code.grid_y, st.code.grid_z,
+                           st.code.block, 0, params.data(), s,
+                           index == 0 ? start : nullptr,
+                           index + 1 == plan.steps.size() ? stop : nullptr);
+            }
+        }
+    } // namespace
+
     std::shared_ptr<rt::buffer_state> run(
         graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
         const std::function<std::shared_ptr<rt::buffer_state>(size_t)>& allocate,
         hip::event_t start, hip::event_t stop
     ) {
-        if (static_cast<int>(inputs.size()) < plan.n_inputs) {
-            throw std::invalid_argument("graph needs more input buffers");
-        }
-        for (int i = 0; i < plan.n_inputs; ++i) {
-            const int64_t need = plan.input_elems[static_cast<size_t>(i)];
-            const rt::buffer_state* in = inputs[static_cast<size_t>(i)];
-            const size_t have = in == nullptr ? 0 : in->bytes;
-            if (need > 0 && have < static_cast<size_t>(need) * sizeof(float)) {
-                throw std::invalid_argument(
-                    have == 0 ? "GPU kernel input is empty"
-                              : "input device buffer is too small"
-                );
-            }
-        }
+        check_inputs(plan, inputs);
         const size_t out_bytes =
             static_cast<size_t>(ir::numel(plan.out_shape)) * sizeof(float);
         if (out_bytes == 0) return allocate(0);
 
         std::shared_ptr<rt::stream> s = rt::current_stream();
-        {
-            std::scoped_lock lock{plan.load_mutex};
-            if (!plan.loaded) {
-                for (step& st : plan.steps)
-                    st.kernel = rt::load_kernel(st.object, st.code.name);
-                plan.loaded = true;
-            }
-        }
-        for (int i = 0; i < plan.n_inputs; ++i) {
-            rt::buffer_state* in = inputs[static_cast<size_t>(i)];
-            if (in != nullptr && in->bytes > 0) in->before_read(s);
-        }
+        prepare_launch(plan, inputs, s);
         std::shared_ptr<rt::buffer_state> out = allocate(out_bytes);
         std::vector<std::shared_ptr<rt::buffer_state>> temps;
+        std::vector<void*> temp_ptrs;
         temps.reserve(plan.temp_elems.size());
         for (const int64_t elems : plan.temp_elems) {
             temps.push_back(std::make_shared<rt::buffer_state>(
                 static_cast<size_t>(std::max<int64_t>(elems, 1)) * sizeof(float)
             ));
+            temp_ptrs.push_back(temps.back()->ptr);
         }
-        std::vector<void*> pointers;
-        std::vector<void*> params;
-        for (size_t index = 0; index < plan.steps.size(); ++index) {
-            const step& st = plan.steps[index];
-            const int slots = st.code.n_slots;
-            pointers.assign(static_cast<size_t>(slots) + 1, nullptr);
-            for (int i = 0; i < slots; ++i) {
-                if (i < plan.n_inputs) {
-                    rt::buffer_state* in = inputs[static_cast<size_t>(i)];
-                    pointers[i] = in == nullptr ? nullptr : in->ptr;
-                }
-                else {
-                    const size_t t = static_cast<size_t>(i - plan.n_inputs);
-                    pointers[i] = t < temps.size() ? temps[t]->ptr : nullptr;
-                }
-            }
-            pointers[slots] = st.dest.what == arg_ref::kind::output
-                                  ? out->ptr
-                                  : temps[static_cast<size_t>(st.dest.index)]->ptr;
-            params.assign(pointers.size(), nullptr);
-            for (size_t i = 0; i < pointers.size(); ++i) params[i] = &pointers[i];
-            rt::launch(st.kernel, st.code.grid_x, st.code.grid_y, st.code.grid_z,
-                       st.code.block, 0, params.data(), *s,
-                       index == 0 ? start : nullptr,
-                       index + 1 == plan.steps.size() ? stop : nullptr);
-        }
+        launch_steps(plan, inputs, out->ptr, temp_ptrs, *s, start, stop);
         out->after_write(s);
         // Temporaries are freed stream-ordered after the launches above.
         return out;
+    }
+
+    std::vector<size_t> workspace_layout(const graph_plan& plan, size_t* total) {
+        std::vector<size_t> offsets;
+        size_t at = 0;
+        for (const int64_t elems : plan.temp_elems) {
+            offsets.push_back(at);
+            const size_t bytes = static_cast<size_t>(std::max<int64_t>(elems, 1)) * sizeof(float);
+            at += (bytes + 255) / 256 * 256;
+        }
+        *total = at;
+        return offsets;
+    }
+
+    void run_in_workspace(graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
+                          rt::buffer_state& out, char* workspace, size_t workspace_bytes) {
+        check_inputs(plan, inputs);
+        const size_t out_bytes =
+            static_cast<size_t>(ir::numel(plan.out_shape)) * sizeof(float);
+        if (out_bytes == 0) return;
+        if (out.bytes < out_bytes) throw std::invalid_argument("output device buffer is too small");
+        size_t need = 0;
+        const std::vector<size_t> offsets = workspace_layout(plan, &need);
+        if (need > workspace_bytes)
+            throw std::invalid_argument("the graph's temporaries need " + std::to_string(need) +
+                                        " bytes of device workspace; " + std::to_string(workspace_bytes) +
+                                        " are available");
+        std::vector<void*> temp_ptrs;
+        for (const size_t offset : offsets) temp_ptrs.push_back(workspace + offset);
+        std::shared_ptr<rt::stream> s = rt::current_stream();
+        prepare_launch(plan, inputs, s);
+        // The output may still be read or written by work on other streams.
+        out.before_write(s);
+        launch_steps(plan, inputs, out.ptr, temp_ptrs, *s, nullptr, nullptr);
+        out.after_write(s);
     }
 
 } // namespace porch::plan

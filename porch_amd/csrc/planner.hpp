@@ -82,4 +82,15 @@ namespace porch::plan {
         hip::event_t start = nullptr, hip::event_t stop = nullptr
     );
 
+    // Byte offset of each temporary in one device region (256-byte
+    // aligned, in plan order); *total receives the region's size.
+    std::vector<size_t> workspace_layout(const graph_plan& plan, size_t* total);
+
+    // run() into the existing buffer `out`, with the temporaries at
+    // `workspace` (laid out by workspace_layout; at most `workspace_bytes`):
+    // allocates no device memory.  Throws invalid_argument when `out` or the
+    // workspace is too small.
+    void run_in_workspace(graph_plan& plan, const std::vector<rt::buffer_state*>& inputs,
+                          rt::buffer_state& out, char* workspace, size_t workspace_bytes);
+
 } // namespace porch::plan

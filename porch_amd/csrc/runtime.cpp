@@ -389,7 +389,10 @@ namespace porch::rt {
                         staged_copy(static_cast<char*>(dst) + done, chunks[i]->host, sizes[i]);
                 }
                 done += sizes[i];
-                release_chunk(chunks[i], false);
+                // After a failed wait this piece's DMA, and the later ones',
+                // may still be queued: the chunk stays pending, so it is
+                // reused only once its event reports the DMA done.
+                release_chunk(chunks[i], waited != hip::success);
             }
             hip::check(queued, "hipMemcpyDtoHAsync");
             hip::check(waited, "hipEventSynchronize");
@@ -611,8 +614,9 @@ namespace porch::rt {
             int major = 0;
             int minor = 0;
             if (c.rtc_version != nullptr) (void)c.rtc_version(&major, &minor);
-            return std::string("\0hiprtc ") + std::to_string(major) + "." + std::to_string(minor) +
-                   "\0porch code object 1";
+            using namespace std::string_literals;
+            return "\0hiprtc "s + std::to_string(major) + "." + std::to_string(minor) +
+                   "\0porch code object 1"s;
         }();
         const std::string disk_key = key + compiler_tag;
         {

@@ -36,21 +36,26 @@ def _input_floats(t) -> int:
 def _program(source: str, name: str, sizes: list[int], grid, block: int, only=None) -> str:
     args = ", ".join(f"b{i}" for i in range(len(sizes)))
     subset = ", {" + ", ".join(str(int(x)) for x in only) + "}" if only else ""
-    decls = "".join(f"    float* b{i} = emu::guarded({n}, tail);\n" for i, n in enumerate(sizes))
+    decls = "".join(f"    float* b{i} = emu::guarded({n}, tail);\n"
+                    f"    emu::load(b{i}, {n}, dir, {i});\n" for i, n in enumerate(sizes))
     return (
         '#include "prelude.hpp"\n#include "runner.hpp"\n' + source +
         "\nint main(int argc, char** argv) {\n"
-        "    const bool tail = argc > 1 && argv[1][0] == '1';\n" + decls +
+        "    const bool tail = argc > 1 && argv[1][0] == '1';\n"
+        "    const char* dir = argc > 2 ? argv[2] : nullptr;\n" + decls +
         f"    emu::run({{{grid[0]}, {grid[1]}, {grid[2]}}}, {block}, [&] {{ {name}({args}); }}{subset});\n"
+        f"    emu::save(b{len(sizes) - 1}, {sizes[-1]}, dir);\n"
         '    std::puts("ok");\n    return 0;\n}\n'
     )
 
 
 def run_kernel(source: str, name: str, sizes: list[int], grid, block: int = 256,
-               timeout: float = 120.0, only=None) -> tuple[bool, str]:
+               timeout: float = 120.0, only=None, values=None) -> tuple[bool, str]:
     """Builds and runs one kernel over `grid` (or only the block x indices
     in `only`) with guarded buffers of `sizes` floats (its parameters in
-    order); (stayed in bounds, detail)."""
+    order); (stayed in bounds, detail).  `values`: a directory holding
+    b<i>.bin contents for the buffers; the destination is written to
+    out.bin there."""
     os.makedirs(BUILD, exist_ok=True)
     program = _program(source, name, sizes, grid, block, only)
     key = hashlib.sha1(program.encode()).hexdigest()[:16]
@@ -66,7 +71,8 @@ def run_kernel(source: str, name: str, sizes: list[int], grid, block: int = 256,
         os.replace(exe + ".tmp", exe)
     for placement in ("1", "0"):
         try:
-            ran = subprocess.run([exe, placement], capture_output=True, text=True, timeout=timeout)
+            ran = subprocess.run([exe, placement] + ([values] if values else []),
+                                 capture_output=True, text=True, timeout=timeout)
         except subprocess.TimeoutExpired:
             return False, f"timed out (placement {placement})"
         if ran.returncode != 0 or "ok" not in ran.stdout:
@@ -74,10 +80,16 @@ def run_kernel(source: str, name: str, sizes: list[int], grid, block: int = 256,
     return True, ""
 
 
-def emulate(expr, timeout: float = 120.0, only=None) -> list[dict]:
+# The test of a max reduction's result that sends it down the path in the
+# reference's order (a NaN, or a +0 maximum); force_exact replaces it.
+_ORDER_TEST = "return m != m || __builtin_bit_cast(unsigned, m) == 0u;"
+
+
+def emulate(expr, timeout: float = 120.0, only=None, force_exact: bool = False) -> list[dict]:
     """Per kernel of the plan: {"kind", "ok", "detail"}.  `only`: run just
     these block x indices of each kernel (for persistent grids whose
-    workgroups each walk many tiles)."""
+    workgroups each walk many tiles).  `force_exact`: every max reduction
+    also takes its path in the reference's order, whatever the values."""
     expr = porch.tensor_expr(expr)
     plan = porch.plan(expr)
     _, _, _, inputs, _ = porch.serialize(expr._root)
@@ -88,7 +100,44 @@ def emulate(expr, timeout: float = 120.0, only=None) -> list[dict]:
     for i, k in enumerate(plan["kernels"]):
         slots = input_floats + temps
         dest = out_floats if k["dest"] == "output" else temps[int(k["dest"][4:])]
-        ok, detail = run_kernel(porch.kernel_source(expr, i), k["name"], slots[: k["slots"]] + [dest],
+        source = porch.kernel_source(expr, i)
+        if force_exact:
+            assert _ORDER_TEST in source
+            source = source.replace(_ORDER_TEST, "return true;")
+        ok, detail = run_kernel(source, k["name"], slots[: k["slots"]] + [dest],
                                 k["grid"], k["block"], timeout, only)
         results.append({"kind": k["kind"], "ok": ok, "detail": detail})
     return results
+
+
+def evaluate(expr, inputs: list[np.ndarray], force_exact: bool = False, timeout: float = 120.0) -> np.ndarray:
+    """The graph's result computed by its generated kernels run on the CPU
+    (in plan order, temporaries carried between them), for input values
+    `inputs` (the serialised input order).  Arithmetic follows the host's
+    libm where the kernels call device math, so only exact operations
+    (views, + - * /, max, reductions of integers) compare bit for bit."""
+    import tempfile
+
+    expr = porch.tensor_expr(expr)
+    plan = porch.plan(expr)
+    _, _, _, tensors, _ = porch.serialize(expr._root)
+    input_floats = [max(_input_floats(t), 1) for t in tensors]
+    buffers = [np.ascontiguousarray(np.asarray(v, np.float32).reshape(-1)) for v in inputs]
+    assert [b.size for b in buffers] == input_floats, ([b.size for b in buffers], input_floats)
+    temps = [np.zeros(max(int(n), 1), np.float32) for n in plan["temps"]]
+    out = np.zeros(max(int(np.prod(plan["out_shape"], dtype=np.int64)) if plan["out_shape"] else 1, 1),
+                   np.float32)
+    with tempfile.TemporaryDirectory() as work:
+        for i, k in enumerate(plan["kernels"]):
+            slots = (buffers + temps)[: k["slots"]]
+            dest = out if k["dest"] == "output" else temps[int(k["dest"][4:])]
+            for j, b in enumerate(slots + [dest]):
+                b.tofile(os.path.join(work, f"b{j}.bin"))
+            source = porch.kernel_source(expr, i)
+            if force_exact:
+                source = source.replace(_ORDER_TEST, "return true;")
+            ok, detail = run_kernel(source, k["name"], [b.size for b in slots] + [dest.size],
+                                    k["grid"], k["block"], timeout, values=work)
+            assert ok, detail
+            dest[:] = np.fromfile(os.path.join(work, "out.bin"), np.float32)
+    return out.reshape(plan["out_shape"])

@@ -8,7 +8,7 @@
 // not the point (the oracle checks those); addresses are.
 //
 // Emulated: thread/block indices, __syncthreads (a barrier over the
-// block's threads), wave64 __shfl_xor, DPP row patterns and
+// block's threads), wave64 __shfl_xor, __shfl, __ballot, DPP row patterns and
 // v_mfma_f32_32x32x2f32 (barriers
 // over the wave's 64 threads, operand layouts as on gfx950), raw buffer
 // stores (range-checked against the resource's size), LDS arrays
@@ -48,6 +48,29 @@ namespace emu {
         const float r = wave_a[w][src];
         wave_barrier[w]->arrive_and_wait();
         return r;
+    }
+
+    inline float shfl(float v, int src_lane, int width) {
+        const int w = wave();
+        const int l = lane();
+        wave_a[w][l] = v;
+        wave_barrier[w]->arrive_and_wait();
+        const int src = (src_lane & (width - 1)) | (l & ~(width - 1));
+        const float r = wave_a[w][src];
+        wave_barrier[w]->arrive_and_wait();
+        return r;
+    }
+
+    inline unsigned long long ballot(bool p) {
+        const int w = wave();
+        const int l = lane();
+        wave_a[w][l] = p ? 1.0f : 0.0f;
+        wave_barrier[w]->arrive_and_wait();
+        unsigned long long mask = 0;
+        for (int i = 0; i < 64; ++i)
+            if (wave_a[w][i] != 0.0f) mask |= 1ull << i;
+        wave_barrier[w]->arrive_and_wait();
+        return mask;
     }
 
     // DPP row patterns used by the kernels: quad_perm [1,0,3,2] and
@@ -114,6 +137,8 @@ namespace emu {
 #define __restrict__ __restrict
 #define __syncthreads() emu::syncthreads()
 #define __shfl_xor(v, m, w) emu::shfl_xor((v), (m), (w))
+#define __shfl(v, s, w) emu::shfl((v), (s), (w))
+#define __ballot(p) emu::ballot(p)
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)

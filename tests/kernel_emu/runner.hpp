@@ -10,6 +10,7 @@
 #include <cstdlib>
 #include <functional>
 #include <memory>
+#include <string>
 #include <thread>
 #include <vector>
 
@@ -43,6 +44,24 @@ namespace emu {
         float* f = reinterpret_cast<float*>(start);
         for (size_t i = 0; i < floats; ++i) f[i] = static_cast<float>(static_cast<int>(i % 7) - 3);
         return f;
+    }
+
+    // Values mode: buffer i takes the floats of <dir>/b<i>.bin when that
+    // file exists, and the destination is written to <dir>/out.bin.
+    inline void load(float* b, size_t floats, const char* dir, int i) {
+        if (dir == nullptr) return;
+        const std::string path = std::string(dir) + "/b" + std::to_string(i) + ".bin";
+        FILE* f = std::fopen(path.c_str(), "rb");
+        if (f == nullptr) return;
+        if (std::fread(b, sizeof(float), floats, f) != floats) std::exit(4);
+        std::fclose(f);
+    }
+    inline void save(const float* b, size_t floats, const char* dir) {
+        if (dir == nullptr) return;
+        const std::string path = std::string(dir) + "/out.bin";
+        FILE* f = std::fopen(path.c_str(), "wb");
+        if (f == nullptr || std::fwrite(b, sizeof(float), floats, f) != floats) std::exit(4);
+        std::fclose(f);
     }
 
     // Runs every block of `grid`, or only the x indices in `only` (the

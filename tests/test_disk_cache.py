@@ -87,3 +87,21 @@ def test_cache_off_writes_nothing(cache_dir):
     porch.reset_jit_cache()
     porch.plan(graph(), compile=True)
     assert entries(cache_dir) == []
+
+
+def test_stored_key_names_the_compiler_and_format(cache_dir):
+    """The key stored in an entry ends with the hiprtc version and the
+    entry format, so a different compiler or format never reads it."""
+    import struct
+
+    porch.plan(graph(), compile=True)
+    (name,) = entries(cache_dir)
+    data = open(os.path.join(cache_dir, name), "rb").read()
+    assert data[:8] == b"PORCHCO1"
+    key_size, code_size, _ = struct.unpack("<3Q", data[8:32])
+    key = data[32:32 + key_size]
+    assert len(data) == 32 + key_size + code_size
+    tag = key[key.rindex(b"\0hiprtc "):]
+    assert tag.endswith(b"\0porch code object 1")
+    major, minor = tag[len(b"\0hiprtc "):-len(b"\0porch code object 1")].split(b".")
+    assert int(major) >= 6 and int(minor) >= 0

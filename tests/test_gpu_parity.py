@@ -117,6 +117,32 @@ def test_softmax_special_values_match_oracle(gpu, cols):
     assert out[3, 5] == 1.0 and np.count_nonzero(out[3]) == 1
 
 
+def test_softmax_online_pass_with_moving_anchors(gpu):
+    """Rows past the register cache run max and sum as one pass with a
+    per-lane anchor that moves (rescaling the lane's sum) whenever a value
+    exceeds it by more than 64.  Wide-range rows make the anchors move many
+    times within a lane: a scaled normal, a rising ramp, and a sawtooth whose
+    teeth rise.  Bar: 1e-6 relative or 2 ulp per element (values far below
+    the row max are denormal or zero)."""
+    cols = 262148
+    rng = np.random.default_rng(31)
+    x = np.empty((4, cols), np.float32)
+    x[0] = rng.standard_normal(cols) * 40
+    x[1] = np.linspace(-300.0, 300.0, cols)
+    x[2] = (np.arange(cols) % 4096) * 0.05 + np.arange(cols) * 1e-3
+    x[3] = np.linspace(300.0, -300.0, cols)
+    t = gpu.tensor([4, cols], x.reshape(-1))
+    expr = gpu.softmax(t, 1)
+    plan = gpu.plan(expr)
+    assert [k["kind"] for k in plan["kernels"]] == ["row"] and plan["kernels"][0]["block"] == 1024
+    out = gpu.materialize(expr).cpu().reshape(4, cols)
+    ref = host.evaluate(expr)
+    rel = np.abs(out.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), 1e-38)
+    ok = (rel <= 1e-6) | (ulp_distance(out, ref).reshape(out.shape) <= 2)
+    assert ok.all(), (np.argwhere(~ok)[:5], out[~ok][:5], ref[~ok][:5])
+    assert np.allclose(out.sum(axis=1), 1.0, atol=2e-5)
+
+
 # short rows: several rows per wave (lane segments of 1 to 32), row counts
 # that leave the last wave's segments partly empty
 @pytest.mark.parametrize("cols", [1, 2, 3, 5, 8, 31, 32, 33, 64, 100, 128, 200, 255])
