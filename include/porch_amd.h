@@ -206,6 +206,30 @@ porch_status porch_materialize(const porch_graph* graph,
                                int64_t* out_shape, int32_t capacity,
                                int32_t* out_rank);
 
+/* Size of the device array porch_materialize_noalloc takes temporaries
+ * from: one per GPU, held from the first call there until the process
+ * ends. */
+#define PORCH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* porch_materialize into `out`, an existing buffer of at least the result's
+ * size, allocating no device memory (no hipMalloc, hipFree or their async
+ * forms, in the library or any routine it calls).  The same kernels run;
+ * the graph's temporaries (memoised reductions, split-reduction partials,
+ * materialised product operands) come from the fixed per-GPU array of
+ * PORCH_NOALLOC_SCRATCH_BYTES, and a graph that needs more fails with
+ * PORCH_ERR_INVALID_ARGUMENT.  Every call on a GPU shares that array:
+ * calls that overlap on one GPU (threads with different streams) race;
+ * calls on one stream are ordered.  The first call for a graph's structure
+ * compiles and loads its kernels as porch_materialize does.  Exported by
+ * the companion library libporch_amd_noalloc.so, which holds the array.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid it). */
+porch_status porch_materialize_noalloc(const porch_graph* graph,
+                                       const porch_buffer* const* inputs,
+                                       int32_t n_inputs, porch_buffer* out,
+                                       int64_t* out_shape, int32_t capacity,
+                                       int32_t* out_rank);
+
 /* porch_materialize with HIP events attached to the first and the last
  * kernel launch (hipExtModuleLaunchKernel), so elapsed time between them is
  * the kernels' own execution on the calling thread's stream.  Events come

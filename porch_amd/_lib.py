@@ -149,6 +149,33 @@ _SIGNATURES = {
 }
 
 
+# Exported by the companion library libporch_amd_noalloc.so (loaded on
+# first use: it links libamdhip64, the main library does not).
+NOALLOC_LIBRARY_PATH = os.path.join(_HERE, "libporch_amd_noalloc.so")
+_NOALLOC_SIGNATURES = {
+    "porch_materialize_noalloc": (ctypes.c_int32, [ctypes.POINTER(Graph), ctypes.POINTER(_P),
+                                                   ctypes.c_int32, _P,
+                                                   ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
+                                                   ctypes.POINTER(ctypes.c_int32)]),
+}
+_noalloc_lib = None
+
+
+def noalloc_lib() -> ctypes.CDLL:
+    """libporch_amd_noalloc.so, bound on first use."""
+    global _noalloc_lib
+    if _noalloc_lib is None:
+        if not os.path.exists(NOALLOC_LIBRARY_PATH):
+            raise ImportError(f"{NOALLOC_LIBRARY_PATH} is missing: build it with `make -C porch_amd`")
+        library = ctypes.CDLL(NOALLOC_LIBRARY_PATH)
+        for name, (restype, argtypes) in _NOALLOC_SIGNATURES.items():
+            fn = getattr(library, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _noalloc_lib = library
+    return _noalloc_lib
+
+
 def _load() -> ctypes.CDLL:
     if not os.path.exists(LIBRARY_PATH):
         raise ImportError(

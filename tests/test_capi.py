@@ -26,20 +26,29 @@ def declared_functions():
 
 
 def test_every_declared_symbol_is_exported():
+    """By libporch_amd.so, or (the allocation-free entry point) by its
+    companion libporch_amd_noalloc.so."""
     names = declared_functions()
-    assert len(names) >= 31
+    assert len(names) >= 32
     lib = ctypes.CDLL(_lib.LIBRARY_PATH)
-    missing = [n for n in names if not hasattr(lib, n)]
+    companion = ctypes.CDLL(_lib.NOALLOC_LIBRARY_PATH)
+    missing = [n for n in names if not hasattr(lib, n) and not hasattr(companion, n)]
     assert not missing, missing
+    assert hasattr(companion, "porch_materialize_noalloc") and not hasattr(lib, "porch_materialize_noalloc")
 
 
 def test_every_declared_symbol_has_a_python_binding():
-    assert set(declared_functions()) <= set(_lib._SIGNATURES)
+    assert set(declared_functions()) <= set(_lib._SIGNATURES) | set(_lib._NOALLOC_SIGNATURES)
 
 
 def test_library_links_no_rocm_library():
     out = subprocess.run(["ldd", _lib.LIBRARY_PATH], capture_output=True, text=True).stdout
     assert "amdhip" not in out and "hiprtc" not in out
+
+
+def test_noalloc_companion_links_the_hip_runtime_and_the_library():
+    out = subprocess.run(["ldd", _lib.NOALLOC_LIBRARY_PATH], capture_output=True, text=True).stdout
+    assert "libamdhip64" in out and "libporch_amd.so" in out and "not found" not in out
 
 
 def test_unavailable_when_hip_runtime_is_missing(tmp_path):

@@ -1,0 +1,141 @@
+"""porch_materialize_noalloc (libporch_amd_noalloc.so) against
+porch_materialize, through the C ABI.
+
+The allocation-free entry point runs the same kernels, with the graph's
+temporaries in a fixed per-GPU device array instead of fresh allocations.
+Its results must equal porch_materialize's bit for bit (NaN compared as
+NaN), on two calls in a row for each graph, the second with a smaller
+input: the array keeps the first call's contents, so a temporary read
+before it is written would show.  Graphs with temporaries of every kind:
+split column reductions (partials), memoised reductions, a materialised
+product operand; and one without.  Sizes past the array's limit, and an
+output buffer too small, are rejected before any launch.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import porch_amd as porch
+from porch_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+LIMIT = 64 << 20  # PORCH_NOALLOC_SCRATCH_BYTES
+
+
+def call_noalloc(expr, out_floats=None):
+    """(status, error message, output values, shape written) of
+    porch_materialize_noalloc into a NaN-filled buffer of `out_floats`
+    (default: the result's size)."""
+    nodes, dims, n_dims, inputs, _ = porch.serialize(expr._root)
+    g = porch._graph(nodes, dims, n_dims)
+    handles = (ctypes.c_void_p * max(len(inputs), 1))(
+        *[t._state.realized().buffer.handle for t in inputs])
+    count = int(np.prod(expr.shape()))
+    size = count if out_floats is None else out_floats
+    out = porch._Buffer.upload(np.full(size, np.nan, np.float32))
+    shape = (ctypes.c_int64 * 64)()
+    rank = ctypes.c_int32()
+    status = _lib.noalloc_lib().porch_materialize_noalloc(
+        ctypes.byref(g), handles, len(inputs), out.handle, shape, 64, ctypes.byref(rank))
+    message = porch.lib.porch_last_error().decode()  # before later calls clear it
+    porch.synchronize()
+    return status, message, out.download(size), [shape[i] for i in range(rank.value)]
+
+
+def noalloc(expr):
+    status, message, values, shape = call_noalloc(expr)
+    assert status == _lib.OK, message
+    assert shape == list(expr.shape())
+    return values.reshape(expr.shape())
+
+
+def assert_same(a, b):
+    a = np.asarray(a, np.float32).reshape(-1)
+    b = np.asarray(b, np.float32).reshape(-1)
+    same = (np.isnan(a) & np.isnan(b)) | (a.view(np.uint32) == b.view(np.uint32))
+    assert same.all(), (np.flatnonzero(~same)[:8], a[~same][:8], b[~same][:8])
+
+
+def rand(shape, seed, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal(int(np.prod(shape))) * scale).astype(np.float32)
+
+
+def softmax_first_axis(shape, seed):
+    return porch.softmax(porch.tensor(shape, rand(shape, seed, 3.0)), 0)
+
+
+def split_column_max(shape, seed):
+    return porch.max(porch.tensor(shape, rand(shape, seed)), 0, False)
+
+
+def product_of_expression(m, k, n, seed):
+    a = porch.tensor([m, k], rand([m, k], seed))
+    b = porch.tensor([k, n], rand([k, n], seed + 1))
+    return porch.relu(porch.matmul(porch.relu(a), b) + 1.0)
+
+
+def nested_reduction(shape, seed):
+    x = porch.tensor(shape, rand(shape, seed))
+    return porch.sum(x - porch.broadcast_to(porch.max(x, 0, True), shape), 1, False)
+
+
+def elementwise(n, seed):
+    a = porch.tensor([n], rand([n], seed))
+    return (a + 1.0) * 2.0 - 1.0
+
+
+CASES = {
+    # name: (graph builder, first call's arguments, second call's (smaller)
+    # arguments, kernels of each call)
+    "softmax over the first axis": (softmax_first_axis, ([6000, 200],), ([3000, 100],), (5, 3)),
+    "split column max": (split_column_max, ([262144, 8],), ([131072, 8],), (2, 2)),
+    "product of an expression": (product_of_expression, (512, 256, 384), (200, 96, 136), (2, 2)),
+    "nested reduction": (nested_reduction, ([300, 500],), ([70, 30],), (2, 2)),
+    "no temporaries": (elementwise, (1 << 20,), (1000,), (1, 1)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_matches_materialize_on_two_calls(gpu, name):
+    build, first, second, kernels = CASES[name]
+    for seed, args, count in ((11, first, kernels[0]), (12, second, kernels[1])):
+        expr = build(*args, seed)
+        plan = porch.plan(expr)
+        assert len(plan["kernels"]) == count, plan
+        assert (count > 1) == bool(plan["temps"])
+        expected = porch.materialize(expr).cpu().reshape(expr.shape())
+        assert_same(noalloc(expr), expected)
+        # and again on the same array contents, with the result unchanged
+        assert_same(noalloc(expr), expected)
+
+
+def test_uses_the_fixed_array_for_temporaries(gpu):
+    """Two different graphs in turn on the same array: the second's
+    temporaries overwrite the first's, and both stay exact."""
+    a = split_column_max([262144, 8], 21)
+    b = softmax_first_axis([4000, 64], 22)
+    ra, rb = porch.materialize(a).cpu(), porch.materialize(b).cpu()
+    for _ in range(2):
+        assert_same(noalloc(a), ra)
+        assert_same(noalloc(b), rb)
+
+
+def test_rejects_temporaries_beyond_the_limit(gpu):
+    expr = product_of_expression(4200, 4096, 64, 31)  # relu(a) is a 68.8 MB temporary
+    need = sum(max(t, 1) * 4 for t in porch.plan(expr)["temps"])
+    assert need > LIMIT
+    status, message, values, _ = call_noalloc(expr)
+    assert status == _lib.ERR_INVALID_ARGUMENT
+    assert "PORCH_NOALLOC_SCRATCH_BYTES" in message and str(need) in message, message
+    assert np.isnan(values).all()  # nothing ran
+
+
+def test_rejects_a_short_output_buffer(gpu):
+    expr = elementwise(4096, 41)
+    status, message, values, _ = call_noalloc(expr, out_floats=4095)
+    assert status == _lib.ERR_INVALID_ARGUMENT
+    assert "too small" in message, message
+    assert np.isnan(values).all()
