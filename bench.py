@@ -26,6 +26,7 @@ for a copy kernel of known size; both come from the counter summaries under
 profiles/ (null when a workload has none).
 
     python bench.py [--steps K] [--warmup W] [--configs view_chain,...] [--no-cpu]
+    python bench.py --controls LAUNCHES   (elementwise control kernels, under rocprofv3)
 """
 
 from __future__ import annotations
@@ -170,13 +171,16 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
     porch.synchronize()
     elapsed = time.perf_counter() - t0
 
-    # Timed region B (roofline): the same K steps, each kernel launched with
-    # a HIP event pair attached to its dispatch on porch's stream
+    # Timed region B (roofline): the same steps, each kernel launched with a
+    # HIP event pair attached to its dispatch on porch's stream
     # (hipExtModuleLaunchKernel), so start/stop bracket the kernel itself.
-    starts = [synth.Event() for _ in range(steps)]
-    stops = [synth.Event() for _ in range(steps)]
+    # Short HBM-bound kernels get at least 200 launches, so that a few slow
+    # dispatches do not decide the mean.
+    launches = max(steps, 200) if WORK[name][0] == "hbm" else steps
+    starts = [synth.Event() for _ in range(launches)]
+    stops = [synth.Event() for _ in range(launches)]
     porch.synchronize()
-    for i in range(steps):
+    for i in range(launches):
         step(i, starts[i], stops[i])
     porch.synchronize()
     kernel_ms = [a.elapsed_ms(b) for a, b in zip(starts, stops)]
@@ -208,7 +212,10 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
         "kernel_ms_mean": float(np.mean(kernel_ms)),
         "kernel_ms_median": float(np.median(kernel_ms)),
         "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
-                     "frac": achieved / peak, "traffic": profiled_traffic(name)},
+                     "frac": achieved / peak, "traffic": profiled_traffic(name),
+                     "launch_us": {"mean": float(np.mean(kernel_ms)) * 1e3,
+                                   "median": float(np.median(kernel_ms)) * 1e3,
+                                   "launches": launches, "frac_uses": "mean"}},
         "jit_ms": {"cold": cold_ms, "cold_codegen": cold_split["codegen_ms"],
                    "cold_hiprtc": cold_split["compile_ms"], "cold_module_load": cold_split["module_load_ms"],
                    "disk": disk_ms, "hit": float(np.median(hit_us)) / 1e3},
@@ -315,9 +322,93 @@ def cpu_baseline(name: str, min_seconds: float = 10.0) -> dict:
     bound, work = WORK[name]
     value = work / seconds / (1e9 if bound == "hbm" else 1e12)
     return {"value": value, "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
-            "cores": host.threads(), "kind": "port",
+            "cores": host.threads(), "cpu_model": cpu_model(), "kind": "port",
             "sample": f"host evaluator on {sample}, median of {len(times)} runs over {spent:.1f} s",
             "seconds": seconds}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# Control kernels at the elementwise workload's launch geometry (1024
+# workgroups of 256 lanes, one float4 of each operand per lane), launched
+# through porch's raw launch path (the reference's in0, in1, out, count
+# parameters): an empty kernel, the reads alone, the writes alone, and a
+# copy.  Their rocprofv3 durations set the floor the elementwise kernel is
+# compared with.
+CONTROL_SOURCE = r"""
+typedef float porch_v4f __attribute__((ext_vector_type(4)));
+extern "C" __global__ void __launch_bounds__(256) porch_control_empty(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {}
+extern "C" __global__ void __launch_bounds__(256) porch_control_read(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {
+    const unsigned long long g = blockIdx.x * 256ull + threadIdx.x;
+    if (g >= count) return;
+    const porch_v4f x = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0) + g);
+    const porch_v4f y = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a1) + g);
+    const float s = ((x.x + x.y) + (x.z + x.w)) + ((y.x + y.y) + (y.z + y.w));
+    if (s == 1234.5f) out[g] = s;  // never true for U[-1,1] inputs: keeps the loads, stores nothing
+}
+extern "C" __global__ void __launch_bounds__(256) porch_control_write(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {
+    const unsigned long long g = blockIdx.x * 256ull + threadIdx.x;
+    if (g >= count) return;
+    reinterpret_cast<float4*>(out)[g] = make_float4(1.0f, 2.0f, 3.0f, (float)g);
+}
+extern "C" __global__ void __launch_bounds__(256) porch_control_copy(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {
+    const unsigned long long g = blockIdx.x * 256ull + threadIdx.x;
+    if (g >= count) return;
+    const porch_v4f x = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0) + g);
+    reinterpret_cast<float4*>(out)[g] = make_float4(x.x, x.y, x.z, x.w);
+}
+"""
+
+
+def controls(launches: int) -> int:
+    """Each control kernel, then the elementwise workload's own kernel,
+    `launches` times each over rotated (cache-cold) buffers; timed by the
+    profiler this runs under (rocprofv3 --kernel-trace --stats)."""
+    import porch_amd as porch
+    from porch_amd import _lib
+    from porch_amd.workloads import config_graph, config_inputs, config_shapes
+
+    if not porch.is_available():
+        return 1
+    n = 1 << 20
+    copies = ROTATION["elementwise"]
+    host = config_inputs("elementwise")
+    sets = [[porch.tensor([n], v) for v in host] for _ in range(copies)]
+    outs = [porch.zeros([n]).realize() for _ in range(copies)]
+    code = ctypes.c_void_p()
+    _lib.check(_lib.lib.porch_compile(CONTROL_SOURCE.encode(), None, 0, ctypes.byref(code)))
+    data, size = _lib.lib.porch_code_object_data(code), _lib.lib.porch_code_object_size(code)
+    for kernel in ("porch_control_empty", "porch_control_read", "porch_control_write", "porch_control_copy"):
+        for i in range(launches):
+            a, b = sets[i % copies]
+            ins = (ctypes.c_void_p * 2)(a.device_data().handle, b.device_data().handle)
+            _lib.check(_lib.lib.porch_launch_fused_elementwise(
+                data, size, kernel.encode(), ins, 2, outs[i % copies].device_data().handle, n // 4))
+        porch.synchronize()
+        log(f"controls: {kernel} x {launches}")
+    for i in range(launches):
+        porch.materialize(config_graph("elementwise", sets[i % copies]))
+    porch.synchronize()
+    log(f"controls: elementwise workload x {launches}")
+    _lib.lib.porch_code_object_release(code)
+    return 0
 
 
 def main() -> int:
@@ -329,9 +420,13 @@ def main() -> int:
                                              "batched_transpose,heads_permute,batched_matmul")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--jit-probe", default=None, help=argparse.SUPPRESS)
+    parser.add_argument("--controls", type=int, default=0, metavar="LAUNCHES",
+                        help="launch the elementwise control kernels (for rocprofv3) and exit")
     args = parser.parse_args()
     if args.jit_probe:
         return jit_probe(args.jit_probe)
+    if args.controls:
+        return controls(args.controls)
     if args.gpus != 1:
         print("bench.py measures one GPU: porch's fused-graph path runs every graph on "
               "one device and has no multi-GPU execution; run with --gpus 1.",

@@ -298,9 +298,8 @@ namespace porch::cg {
         // porch_rcp: hardware reciprocal (about 1 ulp) refined by one
         // Newton-Raphson step with fused multiply-adds.  For |d| in
         // [2^-125, 2^125] this equals the IEEE quotient 1.0f / d bit for bit
-        // (verified exhaustively on gfx950 over the binades 2^-125, 2^-60,
-        // 2^-1, 2^0, 2^1, 2^10 and 2^124; the sequence is scale-invariant in
-        // between); NaN propagates.
+        // (verified exhaustively on gfx950 over every float with |d| in
+        // [2^-125, 2^125], both signs); NaN propagates.
         //
         // porch_exp / porch_exp_finite: exp(x) for x <= 88 by Cody-Waite
         // style reduction onto the hardware exp2: k = rint(x log2 e) with

@@ -1,5 +1,8 @@
-"""The persistent code-object cache (no GPU: planning with compile=True runs
-hiprtc, which is all the cache sits in front of)."""
+"""The persistent code-object cache.  On the CPU, planning with compile=True
+runs hiprtc, which is all the cache sits in front of: hits, damaged and
+truncated entries, the key's compiler tag.  On the GPU, fresh child
+processes fill the cache, then run the five benchmark graphs from it alone
+(no hiprtc call) and match the oracle, also after an entry is damaged."""
 
 import os
 import tempfile
@@ -105,3 +108,45 @@ def test_stored_key_names_the_compiler_and_format(cache_dir):
     assert tag.endswith(b"\0porch code object 1")
     major, minor = tag[len(b"\0hiprtc "):-len(b"\0porch code object 1")].split(b".")
     assert int(major) >= 6 and int(minor) >= 0
+
+
+# -- on the GPU: kernels read back from the cache run and give the oracle's results
+
+def _child(directory):
+    """Runs tests/disk_cache_child.py as a fresh process (never an exec of
+    this one) with the cache in `directory`; its JSON report."""
+    import json
+    import subprocess
+    import sys
+
+    env = dict(os.environ, PORCH_CACHE_DIR=str(directory))
+    result = subprocess.run([sys.executable, os.path.join(REPO, "tests", "disk_cache_child.py")],
+                            capture_output=True, text=True, timeout=600, env=env, cwd=REPO)
+    assert result.returncode == 0, result.stderr[-2000:]
+    return json.loads(result.stdout.strip().splitlines()[-1])
+
+
+@pytest.mark.gpu
+def test_kernels_loaded_from_the_cache_match_the_oracle(gpu, tmp_path):
+    directory = tmp_path / "cache"
+    first = _child(directory)
+    assert all(first["matched"].values()), first
+    assert first["compiles"] == first["kernels"] and first["disk_hits"] == 0, first
+    assert len(entries(directory)) == first["kernels"]
+
+    # a fresh process: every kernel from the cache, none compiled
+    second = _child(directory)
+    assert all(second["matched"].values()), second
+    assert second["compiles"] == 0 and second["disk_hits"] == second["kernels"], second
+
+    # a damaged entry is compiled again (and rewritten), the rest still load
+    name = entries(directory)[0]
+    path = os.path.join(directory, name)
+    data = bytearray(open(path, "rb").read())
+    data[len(data) // 2] ^= 0x5A
+    open(path, "wb").write(bytes(data))
+    third = _child(directory)
+    assert all(third["matched"].values()), third
+    assert third["compiles"] == 1 and third["disk_hits"] == third["kernels"] - 1, third
+    fourth = _child(directory)
+    assert fourth["compiles"] == 0 and fourth["disk_hits"] == fourth["kernels"], fourth

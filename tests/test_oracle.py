@@ -103,6 +103,28 @@ def test_softmax_planted_mistake_is_caught():
     assert np.abs(wrong - truth).max() > 1e-3
 
 
+def test_softmax_without_the_max_shift_is_caught():
+    """A softmax built without its max shift, exp(x) / sum(exp(x)), equals
+    softmax mathematically but overflows once a row holds values above 88:
+    the float64 check passes the oracle's softmax and fails the unshifted
+    one on such rows (N(0, 3) scaled by 10, so values reach ~150)."""
+    x = config_inputs("softmax", {"rows": 16, "cols": 64})[0] * np.float32(10.0)
+    t = placeholder([16, 64], x)
+    xm = x.reshape(16, 64)
+    # the shift in binary32, as porch's graph takes it; the rest in float64
+    e = np.exp((xm - xm.max(axis=1, keepdims=True)).astype(np.float64))
+    truth = e / e.sum(axis=1, keepdims=True)
+    assert xm.max() > 88.0
+
+    def passes(out):
+        with np.errstate(invalid="ignore"):
+            return bool(np.all(np.abs(out - truth) <= 1e-6 * truth + 1e-30))
+
+    assert passes(host.evaluate(porch.softmax(t, 1)))
+    unshifted = porch.exp(t) / porch.broadcast_to(porch.sum(porch.exp(t), 1, True), [16, 64])
+    assert not passes(host.evaluate(unshifted))
+
+
 def test_logistic_row_sums_against_float64():
     size = {"rows": 40, "cols": 2048}
     out, (x, w, b) = oracle_of("logistic_rowsum", size)
