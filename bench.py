@@ -80,6 +80,8 @@ DESCRIPTION = {
     "attention_scores": "batched_matmul(q, k) * 0.125, q fp32 [16,4096,64], k fp32 [16,64,4096]",
     "vocab_softmax": "softmax(x, 1), x fp32 [512,262144]",
 }
+# Minimum length of each workload's untimed warm-up (see run_config).
+WARM_SECONDS = 0.25
 # Input copies rotated through so that a step never re-reads cached data.
 ROTATION = {"elementwise": 48, "view_chain": 8, "softmax": 4, "logistic_rowsum": 6,
             "matmul_epilogue": 1, "copy": 2, "batched_transpose": 4, "heads_permute": 2,
@@ -159,9 +161,19 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
         porch.set_disk_cache(None)
         disk_ms = disk_warm_jit_ms(name, cache)
 
-    for i in range(warmup):
-        step(i)
-    porch.synchronize()
+    # Warm-up, untimed: at least `warmup` steps and at least WARM_SECONDS of
+    # back-to-back work, synchronising every 8 steps so the queue stays
+    # short.  An idle MI355X ramps its clocks over the first tens of
+    # milliseconds of load (the 4096^3 matmul runs ~1130 us on the first
+    # launches and settles near 975 us after ~25 of them), so fewer steps
+    # would time the ramp rather than the kernel.
+    warm_start = time.perf_counter()
+    done = 0
+    while done < warmup or time.perf_counter() - warm_start < WARM_SECONDS:
+        for _ in range(8):
+            step(done)
+            done += 1
+        porch.synchronize()
 
     # Timed region A (whole-job value): K steps back to back.
     porch.synchronize()
@@ -176,7 +188,7 @@ def run_config(porch, name: str, steps: int, warmup: int) -> dict:
     # (hipExtModuleLaunchKernel), so start/stop bracket the kernel itself.
     # Short HBM-bound kernels get at least 200 launches, so that a few slow
     # dispatches do not decide the mean.
-    launches = max(steps, 200) if WORK[name][0] == "hbm" else steps
+    launches = max(steps, 200) if WORK[name][0] == "hbm" else max(steps, 20)
     starts = [synth.Event() for _ in range(launches)]
     stops = [synth.Event() for _ in range(launches)]
     porch.synchronize()
@@ -444,9 +456,7 @@ def main() -> int:
     workload_names = [c for c in args.configs.split(",") if c]
     results = {}
     for name in workload_names:
-        # Matmul steps are long; keep its timed region short.
-        steps = args.steps if WORK[name][0] == "hbm" else max(3, args.steps // 40)
-        warmup = args.warmup if WORK[name][0] == "hbm" else max(1, args.warmup // 10)
+        steps, warmup = args.steps, args.warmup
         log(f"{name}: {DESCRIPTION[name]} ({steps} steps)")
         results[name] = run_config(porch, name, steps, warmup)
         r = results[name]

@@ -46,6 +46,20 @@ namespace porch::cg {
         return users > 0;
     }
 
+    int emitter::fusable_product(int id) {
+        if (!relaxed || !relaxed(id)) return -1;
+        const knode& n = k.at(id);
+        for (const int side : {n.a, n.b}) {
+            if (side < 0 || side == (side == n.a ? n.b : n.a)) continue;
+            const knode& m = k.at(side);
+            if (m.op != kop::multiply || !relaxed(side) || find(side) != nullptr) continue;
+            int users = 0;
+            for (const knode& u : k.nodes) users += (u.a == side) + (u.b == side);
+            if (users == 1) return side;
+        }
+        return -1;
+    }
+
     std::string emitter::fresh(const char* prefix) {
         return std::string{prefix} + std::to_string(counter_++);
     }
@@ -99,8 +113,30 @@ namespace porch::cg {
                 for (int e = 0; e < width; ++e) result[e] = text;
                 break;
             }
-            case kop::add: binary("+"); break;
-            case kop::subtract: binary("-"); break;
+            case kop::add:
+            case kop::subtract: {
+                // In a relaxed context a product used only here fuses into
+                // one fma (one rounding instead of two).
+                const int product = fusable_product(id);
+                if (product < 0) {
+                    binary(n.op == kop::add ? "+" : "-");
+                    break;
+                }
+                const knode& m = k.at(product);
+                const std::vector<std::string> x = emit(m.a);
+                const std::vector<std::string> y = emit(m.b);
+                const std::vector<std::string> c = emit(product == n.a ? n.b : n.a);
+                // a*b + c, c + a*b, a*b - c = fma(a, b, -c), c - a*b = fma(-a, b, c)
+                const bool negate_c = n.op == kop::subtract && product == n.a;
+                const bool negate_p = n.op == kop::subtract && product == n.b;
+                for (int e = 0; e < width; ++e) {
+                    const std::string name = fresh("v");
+                    line("const float " + name + " = __builtin_fmaf(" + (negate_p ? "-" : "") + x[e] + ", " + y[e] +
+                         ", " + (negate_c ? "-" : "") + c[e] + ");");
+                    result[e] = name;
+                }
+                break;
+            }
             case kop::multiply: binary("*"); break;
             case kop::divide: binary("/"); break;
             case kop::maximum:

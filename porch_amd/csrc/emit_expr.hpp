@@ -72,6 +72,11 @@ namespace porch::cg {
         // use instruction sequences a few ulp from correctly rounded.
         std::function<bool(int id)> relaxed;
 
+        // The multiply operand of add/subtract `id` that may fuse into it as
+        // an fma: both relaxed, the product used nowhere else and not yet
+        // emitted; -1 if none.
+        int fusable_product(int id);
+
       private:
         std::vector<std::map<int, std::vector<std::string>>> frames_;
         std::vector<vrange> ranges_;

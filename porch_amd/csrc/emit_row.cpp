@@ -633,11 +633,35 @@ namespace porch::cg {
             chunk_open(code, "        ", true);
             std::string body;
             auto em = make_emitter(body, pass);
-            const std::vector<std::string> v = em->emit(root);
-            store_caches(*em, pass, root);
-            for (int e = 0; e < width; ++e) {
-                if (is_max) em->line(acc + " = porch_fmax(" + acc + ", " + v[e] + ");");
-                else em->line(acc + " += " + v[e] + ";");
+            // A relaxed sum of reciprocals 1/d with d proven in [2^-31, 2^31]
+            // (the logistic's 1 + exp(-v) lies in [1, 2]): four terms as
+            // ((d0 + d1) d2 d3 + (d2 + d3) d0 d1) / (d0 d1 d2 d3), one
+            // reciprocal instead of four; every product stays normal and
+            // finite, and each group is within a few ulp of the four terms.
+            const knode& rn = k.at(root);
+            const bool paired = !is_max && width == 4 && relaxed[static_cast<size_t>(root)] &&
+                                rn.op == kop::reciprocal &&
+                                std::find(cached.begin(), cached.end(), root) == cached.end() &&
+                                em->range_of(rn.a).within(0x1p-31F, 0x1p31F);
+            if (paired) {
+                const std::vector<std::string> d = em->emit(rn.a);
+                store_caches(*em, pass, root);
+                const std::string p0 = em->fresh("xp"), p1 = em->fresh("xp");
+                const std::string s0 = em->fresh("xs"), s1 = em->fresh("xs");
+                em->line("const float " + p0 + " = " + d[0] + " * " + d[1] + ";");
+                em->line("const float " + p1 + " = " + d[2] + " * " + d[3] + ";");
+                em->line("const float " + s0 + " = " + d[0] + " + " + d[1] + ";");
+                em->line("const float " + s1 + " = " + d[2] + " + " + d[3] + ";");
+                em->line(acc + " = __builtin_fmaf(__builtin_fmaf(" + s0 + ", " + p1 + ", " + s1 + " * " + p0 +
+                         "), __builtin_amdgcn_rcpf(" + p0 + " * " + p1 + "), " + acc + ");");
+            }
+            else {
+                const std::vector<std::string> v = em->emit(root);
+                store_caches(*em, pass, root);
+                for (int e = 0; e < width; ++e) {
+                    if (is_max) em->line(acc + " = porch_fmax(" + acc + ", " + v[e] + ");");
+                    else em->line(acc + " += " + v[e] + ";");
+                }
             }
             code += body;
             chunk_close(code, "        ");

@@ -117,6 +117,33 @@ def test_relaxed_forms_only_inside_a_final_sum(make, relaxed):
         assert (form in b) == relaxed, form
 
 
+def test_products_fuse_into_fma_only_inside_a_final_sum():
+    x = placeholder([64, 2048])
+    w = porch.broadcast_to(placeholder([1, 2048]), [64, 2048])
+    b = porch.broadcast_to(placeholder([1, 2048]), [64, 2048])
+    affine = x * w + b
+    assert "__builtin_fmaf(" in body(porch.sum(porch.logistic(porch.relu(affine)), 1))
+    assert "__builtin_fmaf(" in body(porch.sum(b - x * w, 1))
+    # stored, or selected by a max: each product rounds on its own
+    assert "__builtin_fmaf(" not in body(affine)
+    assert "__builtin_fmaf(" not in body(porch.max(affine, 1))
+    # a product used twice is computed once, not fused into either use
+    assert "__builtin_fmaf(" not in body(porch.sum((x * w + b) * (x * w), 1))
+
+
+def test_reciprocals_share_one_rcp_only_when_their_operands_are_bounded():
+    x = placeholder([64, 2048])
+    # the logistic's 1 + exp(-relu(x)) lies in [1, 2]: four terms, one rcp
+    paired = body(porch.sum(porch.logistic(porch.relu(x)), 1))
+    assert paired.count("__builtin_amdgcn_rcpf(") == 1 and "__builtin_amdgcn_rcpf(xp" in paired
+    # 1/x for an unbounded x: one reciprocal per term
+    assert "__builtin_amdgcn_rcpf(xp" not in body(porch.sum(porch.reciprocal(x), 1))
+    # exp(-x) is unbounded above without the relu
+    assert "__builtin_amdgcn_rcpf(xp" not in body(porch.sum(porch.logistic(x), 1))
+    # not a final sum
+    assert "rcpf(xp" not in body(porch.logistic(porch.relu(x)))
+
+
 def test_negation_folds_into_exp_only_for_positive_zero():
     x = placeholder([256])
     assert "expf(-" in body(porch.exp(0.0 - x))
