@@ -143,11 +143,35 @@ namespace porch::cg {
             case kop::minimum: {
                 const std::vector<std::string> a = emit(n.a);
                 const std::vector<std::string> b = emit(n.b);
-                const char* cmp = n.op == kop::maximum ? " > " : " < ";
+                const bool is_max = n.op == kop::maximum;
+                // Against a constant right operand c, v_max_f32(a, c) (and
+                // v_min_f32) give the ternary's bits for every a: a NaN a
+                // yields c in both, v_max_f32 orders -0 below +0 and
+                // v_min_f32 +0 above -0 (measured on gfx950), so they agree
+                // unless c is the zero the ternary would pass over: +0 for a
+                // max, -0 for a min.  relu(v) = maximum(v, 0.0f) is one
+                // instruction instead of a compare and a select.
+                const knode& c = k.at(n.b);
+                const bool constant = c.op == kop::constant && !std::isnan(c.value);
+                // The other zero: the compiler itself turns a ternary against
+                // a constant into v_min_f32 / v_max_f32 (measured: x < 0.0f ?
+                // x : 0.0f became v_min_f32, giving -0 for x = -0 where the
+                // ternary gives +0; an added 0.0f was folded away too), so
+                // these two fix the zero's sign on the bits
+                // (porch_min_pos0 / porch_max_neg0).
+                const bool other_zero = constant && c.value == 0.0F && std::signbit(c.value) == is_max;
+                const bool hardware = constant && !other_zero;
+                const char* cmp = is_max ? " > " : " < ";
                 for (int e = 0; e < width; ++e) {
                     const std::string name = fresh("v");
-                    line("const float " + name + " = (" + a[e] + cmp + b[e] +
-                         ") ? " + a[e] + " : " + b[e] + ";");
+                    if (hardware)
+                        line("const float " + name + " = " + (is_max ? "__builtin_fmaxf(" : "__builtin_fminf(") + a[e] +
+                             ", " + b[e] + ");");
+                    else if (other_zero)
+                        line("const float " + name + " = " + (is_max ? "porch_max_neg0(" : "porch_min_pos0(") + a[e] +
+                             ");");
+                    else
+                        line("const float " + name + " = (" + a[e] + cmp + b[e] + ") ? " + a[e] + " : " + b[e] + ";");
                     result[e] = name;
                 }
                 break;
@@ -393,6 +417,17 @@ __device__ __forceinline__ float porch_exp_flush(float x) {
 }
 __device__ __forceinline__ float porch_exp_flush_finite(float x) {
     return porch_exp_flush_reduced(__builtin_fmaxf(x, -104.0f));
+}
+// The reference's ternaries against the zero they pass over, x < +0 ? x : +0
+// and x > -0 ? x : -0 (v_min_f32 gives -0 for (-0, +0), v_max_f32 +0 for
+// (+0, -0); the sign is set on the bits, which the compiler keeps).
+__device__ __forceinline__ float porch_min_pos0(float x) {
+    const int i = __builtin_bit_cast(int, __builtin_fminf(x, 0.0f));
+    return __builtin_bit_cast(float, i == (int)0x80000000 ? 0 : i);
+}
+__device__ __forceinline__ float porch_max_neg0(float x) {
+    const int i = __builtin_bit_cast(int, __builtin_fmaxf(x, -0.0f));
+    return __builtin_bit_cast(float, i == 0 ? (int)0x80000000 : i);
 }
 // Order-free max for folds and lane reductions (v_maximum3_f32): NaN if
 // either operand is NaN, and -0 < +0, so every grouping gives the same

@@ -144,6 +144,18 @@ def test_reciprocals_share_one_rcp_only_when_their_operands_are_bounded():
     assert "rcpf(xp" not in body(porch.logistic(porch.relu(x)))
 
 
+@pytest.mark.parametrize("op, constant, hardware", [
+    ("maximum", 0.0, True), ("maximum", -0.0, False), ("maximum", 1.5, True), ("maximum", -2.0, True),
+    ("minimum", -0.0, True), ("minimum", 0.0, False), ("minimum", 1.5, True), ("minimum", -2.0, True),
+])
+def test_max_and_min_against_a_constant_use_one_instruction(op, constant, hardware):
+    x = placeholder([1024])
+    fn = "__builtin_fmaxf(" if op == "maximum" else "__builtin_fminf("
+    assert (fn in body(getattr(porch, op)(x, constant))) == hardware
+    # a constant on the left keeps the ternary: a NaN x must pass through
+    assert fn not in body(getattr(porch, op)(constant, x))
+
+
 def test_negation_folds_into_exp_only_for_positive_zero():
     x = placeholder([256])
     assert "expf(-" in body(porch.exp(0.0 - x))
@@ -266,3 +278,22 @@ def test_fast_exp_propagates_nan(gpu):
     out = gpu.materialize(expr).cpu()
     assert np.isnan(out[0]) and out[1] == 1.0 and out[3] == 0.0
     assert ulp_distance(out[1:], host.evaluate(expr)[1:]).max() <= 2
+
+
+@pytest.mark.gpu
+def test_max_and_min_against_constants_match_the_ternaries(gpu):
+    """maximum(x, c) and minimum(x, c) as v_max_f32 / v_min_f32 give the
+    reference's ternary bits (src/tensor.cpp:677-682) on signed zeros, NaN
+    of either sign, infinities and denormals, for every constant form; the
+    forms the emitter keeps as ternaries are checked alongside."""
+    nan = np.float32(np.nan)
+    specials = np.array([-0.0, 0.0, nan, -nan, np.inf, -np.inf, 1e-45, -1e-45, 1.0, -1.0, 1.5, -2.0, 3.0],
+                        dtype=np.float32)
+    x = np.concatenate([specials, np.random.default_rng(4).standard_normal(4096).astype(np.float32)])
+    t = gpu.tensor([x.size], x)
+    for c in (0.0, -0.0, 1.5, -2.0, 1e-45):
+        for op in (gpu.maximum, gpu.minimum):
+            expr = op(t, c)
+            out = gpu.materialize(expr).cpu()
+            ref = host.evaluate(expr)
+            assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (op.__name__, c)
