@@ -362,8 +362,38 @@ namespace porch::plan {
                 r.n_slots = n_slots();
                 r.width = width;
                 r.compute_units = compute_units;
+                const int64_t parts = cg::row_split_parts(r);
+                if (parts > 0) {
+                    // Rows split over workgroups exchange partials through a
+                    // temporary that must read zero when the kernel starts.
+                    const int t = static_cast<int>(plan.temp_elems.size());
+                    plan.temp_elems.push_back(cg::row_split_temp_floats(r));
+                    emit_zero_fill(t);
+                    r.split_slot = g.n_inputs + t;
+                    r.split_parts = parts;
+                    r.n_slots = n_slots();
+                    add_step(cg::emit_row_split(r), dest);
+                    return true;
+                }
                 add_step(cg::emit_row(r), dest);
                 return true;
+            }
+
+            // Zeros into temporary `t` with a fill kernel (not a memset, so
+            // that a captured graph replays it like any other step).
+            void emit_zero_fill(int t) {
+                cg::kexpr k;
+                cg::knode c;
+                c.op = cg::kop::constant;
+                c.value = 0.0F;
+                cg::pointwise_request r;
+                r.expr = &k;
+                r.root = k.add(c);
+                r.shape = {plan.temp_elems[static_cast<size_t>(t)]};
+                r.n_slots = n_slots();
+                r.width = width;
+                r.compute_units = compute_units;
+                add_step(cg::emit_pointwise(r), {arg_ref::kind::temp, t});
             }
 
             // ---------------------------------------------------------

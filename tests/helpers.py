@@ -112,3 +112,59 @@ def check_kat(case, values: np.ndarray) -> None:
 
 
 from porch_amd.workloads import CONFIG_SIZES, config_graph, config_inputs, config_shapes  # noqa: E402,F401
+
+
+def _ulps(a, b):
+    ai = np.asarray(a, np.float32).reshape(-1).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).reshape(-1).view(np.int32).astype(np.int64)
+    ai = np.where(ai < 0, -(ai & 0x7FFFFFFF), ai)
+    bi = np.where(bi < 0, -(bi & 0x7FFFFFFF), bi)
+    return np.abs(ai - bi).reshape(np.shape(a))
+
+
+def assert_softmax_close(out, t, values, rel=1e-6):
+    """Softmax over the last axis of 2-D tensor `t` holding `values`, `out`
+    computed by the kernels, against two references:
+
+    1. the softmax of the same float32 differences x - max(x) with exp, sum
+       and division in float64 (rows of finite values): within `rel`, or
+       2 ulp where the result is far below the row max (tiny or denormal);
+    2. the oracle: NaN exactly where it has NaN, elsewhere within `rel`
+       plus the oracle's own row-sum drift.  The oracle sums in the
+       reference's order, 256 float32 chains of L/256 terms each, so on long
+       rows its sum drifts from the exact one (about 1.1e-6 relative at
+       L = 262144, one part in 10^8 at L = 4096); a result summed more
+       exactly differs from it by that much before any error of its own.
+       The drift is measured per row: the oracle's sum of exp(x - max)
+       against the float64 sum of the same terms."""
+    from oracle import host
+
+    shape = list(out.shape)
+    rows, cols = shape
+    ref = np.asarray(host.evaluate(porch.softmax(t, 1)), np.float32).reshape(shape)
+    out = np.asarray(out, np.float32).reshape(shape)
+    values = np.asarray(values, np.float32).reshape(shape)
+    m = porch.broadcast_to(porch.max(t, 1, True), shape)
+    oracle_sums = np.asarray(host.evaluate(porch.sum(porch.exp(t - m), 1)), np.float64).reshape(rows)
+
+    finite_rows = np.isfinite(values).all(axis=1)
+    with np.errstate(all="ignore"):
+        d = (values - values.max(axis=1, keepdims=True)).astype(np.float32).astype(np.float64)
+        e = np.exp(d)
+        s = e.sum(axis=1, keepdims=True)
+        truth = e / s
+        drift = np.where(finite_rows, np.abs(oracle_sums / s[:, 0] - 1.0), 0.0)
+
+    def rel_err(a, b):
+        return np.abs(a.astype(np.float64) - b) / np.maximum(np.abs(b.astype(np.float64)), 1e-300)
+
+    tr = truth[finite_rows]
+    o = out[finite_rows]
+    ok = (rel_err(o, tr) <= rel) | (_ulps(o, tr.astype(np.float32)) <= 2)
+    assert ok.all(), ("vs float64", np.argwhere(~ok)[:5], o[~ok][:5], tr[~ok][:5])
+
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    finite = ~np.isnan(ref)
+    bar = np.broadcast_to((rel + drift)[:, None], shape)
+    ok = (rel_err(out[finite], ref[finite]) <= bar[finite]) | (_ulps(out[finite], ref[finite]) <= 2)
+    assert ok.all(), ("vs oracle", float(drift.max()), rel_err(out[finite], ref[finite]).max())

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import hashlib
 import os
+import re
 import subprocess
 
 import numpy as np
@@ -85,6 +86,17 @@ def run_kernel(source: str, name: str, sizes: list[int], grid, block: int = 256,
 _ORDER_TEST = "return m != m || __builtin_bit_cast(unsigned, m) == 0u;"
 
 
+# Blocks run one after another here, so a wait on a later block's partial
+# never ends: two polls (the second after a wave-wide step, so that a
+# block's own partial, stored by another of its threads, is visible), then
+# the waiting block's own fallback.
+_SPIN = re.compile(r"#define porch_spin_limit \d+")
+
+
+def _emulated(source: str) -> str:
+    return _SPIN.sub("#define porch_spin_limit 2", source)
+
+
 def emulate(expr, timeout: float = 120.0, only=None, force_exact: bool = False) -> list[dict]:
     """Per kernel of the plan: {"kind", "ok", "detail"}.  `only`: run just
     these block x indices of each kernel (for persistent grids whose
@@ -100,7 +112,7 @@ def emulate(expr, timeout: float = 120.0, only=None, force_exact: bool = False) 
     for i, k in enumerate(plan["kernels"]):
         slots = input_floats + temps
         dest = out_floats if k["dest"] == "output" else temps[int(k["dest"][4:])]
-        source = porch.kernel_source(expr, i)
+        source = _emulated(porch.kernel_source(expr, i))
         if force_exact:
             assert _ORDER_TEST in source
             source = source.replace(_ORDER_TEST, "return true;")
@@ -133,7 +145,7 @@ def evaluate(expr, inputs: list[np.ndarray], force_exact: bool = False, timeout:
             dest = out if k["dest"] == "output" else temps[int(k["dest"][4:])]
             for j, b in enumerate(slots + [dest]):
                 b.tofile(os.path.join(work, f"b{j}.bin"))
-            source = porch.kernel_source(expr, i)
+            source = _emulated(porch.kernel_source(expr, i))
             if force_exact:
                 source = source.replace(_ORDER_TEST, "return true;")
             ok, detail = run_kernel(source, k["name"], [b.size for b in slots] + [dest.size],

@@ -13,7 +13,10 @@
 // over the wave's 64 threads, operand layouts as on gfx950), raw buffer
 // stores (range-checked against the resource's size), LDS arrays
 // (function-local statics, shared by the block's threads; blocks run one
-// after another).  The rest of the device builtins map to host math.
+// after another), relaxed 64-bit atomic loads and stores (host atomics; a
+// block that waits on another block's store sees it only if that block ran
+// earlier, so the emulation caps such waits: emulate.py).  The rest of the
+// device builtins map to host math.
 #pragma once
 
 #include <barrier>
@@ -142,6 +145,10 @@ namespace emu {
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
+#define __builtin_amdgcn_s_sleep(n) ((void)0)
+#define __HIP_MEMORY_SCOPE_AGENT 0
+#define __hip_atomic_load(p, order, scope) __atomic_load_n((p), (order))
+#define __hip_atomic_store(p, v, order, scope) __atomic_store_n((p), (v), (order))
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu::mfma_32x32x2((a), (b), (c))
 #define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu::update_dpp((src), (ctrl))
 #define __builtin_amdgcn_make_buffer_rsrc(p, stride, num, flags) \

@@ -297,3 +297,72 @@ def test_max_and_min_against_constants_match_the_ternaries(gpu):
             out = gpu.materialize(expr).cpu()
             ref = host.evaluate(expr)
             assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (op.__name__, c)
+
+
+# porch_div (the split softmax's output division): RN(q + (a - b q) r) with
+# r = porch_rcp(b) and q = RN(a r) against the GPU's IEEE division a / b,
+# for every significand of a (one binade: the rounding depends on the
+# significands, the exponents only shift it while the quotient stays
+# normal) against 256 divisors, at three exponent pairs spanning the range
+# the kernel uses it in (a in [e^-60, 1], b in [1, 2^31]).
+_DIV_KERNEL = r"""
+extern "C" __global__ void divcheck(const float* b, const float* abits, float* out, unsigned long long count) {
+    const unsigned long long t = blockIdx.x * 256ull + threadIdx.x;
+    if (t >= count) return;
+    const float d = b[t / 4096];
+    const float r = porch_rcp(d);
+    const unsigned first = (unsigned)(t % 4096) * 2048u;
+    const unsigned base = __float_as_uint(abits[0]);
+    float bad = 0.0f;
+    for (unsigned i = 0; i < 2048u; ++i) {
+        const float a = __uint_as_float(base | (first + i));
+        const float q = a / d;
+        const float m = porch_div(a, r, d);
+        bad += __float_as_uint(q) != __float_as_uint(m) ? 1.0f : 0.0f;
+    }
+    out[t] = bad;
+}
+"""
+
+
+def _split_softmax_helpers():
+    source = porch.kernel_source(porch.softmax(placeholder([4, 262144]), 1), 1)
+    found = [re.search(r"__device__ __forceinline__ float %s\(.*?\n}\n" % name, source, re.S)
+             for name in ("porch_rcp", "porch_div")]
+    assert all(found)
+    return "".join(m.group(0) for m in found)
+
+
+def test_split_softmax_uses_the_checked_division():
+    helpers = _split_softmax_helpers()
+    assert "__builtin_amdgcn_rcpf(d)" in helpers
+    assert "__builtin_fmaf(__builtin_fmaf(-b, q, a), r, q)" in helpers
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("a_exp, b_exp", [(0, 0), (-60, 30), (-1, 20)])
+def test_reciprocal_division_is_ieee(gpu, a_exp, b_exp):
+    import ctypes
+
+    from porch_amd import _lib
+
+    rng = np.random.default_rng((a_exp + 100) * 100 + b_exp)
+    significands = [0, 1, (1 << 23) - 1, 1 << 22, 1 << 21, 3 << 21, 0x3504F3, (1 << 22) - 1, (1 << 22) + 1]
+    significands += [int(v) for v in rng.integers(0, 1 << 23, size=256 - len(significands))]
+    b = (np.array(significands, np.uint32) | np.uint32((127 + b_exp) << 23)).view(np.float32)
+    abits = np.array([(127 + a_exp) << 23], np.uint32).view(np.float32)
+    code = ctypes.c_void_p()
+    _lib.check(_lib.lib.porch_compile((_split_softmax_helpers() + _DIV_KERNEL).encode(), None, 0, ctypes.byref(code)))
+    try:
+        size = _lib.lib.porch_code_object_size(code)
+        data = _lib.lib.porch_code_object_data(code)
+        bb = gpu._Buffer.upload(b)
+        ab = gpu._Buffer.upload(abits)
+        count = b.size * 4096
+        out = gpu._Buffer.upload(np.zeros(count, np.float32))
+        ins = (ctypes.c_void_p * 2)(bb.handle, ab.handle)
+        _lib.check(_lib.lib.porch_launch_fused_elementwise(data, size, b"divcheck", ins, 2, out.handle, count))
+        bad = out.download(count)
+    finally:
+        _lib.lib.porch_code_object_release(code)
+    assert bad.sum() == 0, (bad.sum(), b[np.flatnonzero(bad.reshape(b.size, 4096).sum(axis=1))[:4]])

@@ -28,7 +28,7 @@ import pytest
 
 import porch_amd as porch
 from oracle import host
-from tests.helpers import placeholder
+from tests.helpers import assert_softmax_close, placeholder
 from tests.kernel_emu import emulate as emu
 
 FLT_MAX = np.float32(3.4028234663852886e38)
@@ -256,14 +256,12 @@ def test_column_max_matches_the_oracle_on_gpu(gpu, shape, axis, keepdim):
 @pytest.mark.parametrize("shape", [[40, 64], [20, 1000], [20, 4096], [2, 262148]])
 def test_softmax_of_special_rows_matches_the_oracle_on_gpu(gpu, shape):
     """Softmax over the same rows: NaN exactly where the oracle has NaN,
-    elsewhere within 1e-6 relative."""
+    elsewhere within 1e-6 relative (beyond the oracle's own row-sum drift:
+    assert_softmax_close)."""
     x = special_rows(*shape, seed=shape[1] + 3)
-    expr = gpu.softmax(gpu.tensor(shape, x), 1)
-    out = gpu.materialize(expr).cpu().reshape(shape)
-    ref = host.evaluate(expr)
-    assert np.array_equal(np.isnan(out), np.isnan(ref))
-    finite = ~np.isnan(ref)
-    assert np.all(np.abs(out[finite] - ref[finite]) <= 1e-6 * np.abs(ref[finite]))
+    t = gpu.tensor(shape, x)
+    out = gpu.materialize(gpu.softmax(t, 1)).cpu().reshape(shape)
+    assert_softmax_close(out, t, x)
 
 
 @pytest.mark.gpu

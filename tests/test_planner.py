@@ -143,15 +143,17 @@ def test_scalars_are_emitted_exactly():
 
 def test_long_softmax_rows_read_twice():
     # rows within the register cache: one read of x; beyond it, max and sum
-    # share one pass, so two reads (not three), with ordinary loads
-    def reads(cols):
-        source = porch.kernel_source(porch.softmax(placeholder([4, cols]), 1))
+    # share one pass, so two reads (not three), with ordinary loads (a
+    # softmax over a product of two leaves: not the split form)
+    def reads(expr):
+        source = porch.kernel_source(expr)
         return source.count("a0 + ("), "__builtin_nontemporal_load" in source, "acc_a" in source
 
-    assert reads(65536) == (1, True, False)
-    assert reads(262144) == (2, False, True)
+    assert reads(porch.softmax(placeholder([4, 65536]), 1)) == (1, True, False)
+    assert reads(porch.softmax(placeholder([4, 262144]) * placeholder([4, 262144]), 1)) == (2, False, True)
     # the second read walks the row backwards
-    source = porch.kernel_source(porch.softmax(placeholder([4, 262144]), 1))
+    x, y = placeholder([4, 262144]), placeholder([4, 262144])
+    source = porch.kernel_source(porch.softmax(x * y, 1))
     assert source.count("for (int j = 63; j >= 0; --j)") == 1
     # a plain sum of exp over such rows stays one streaming pass
     source = porch.kernel_source(porch.sum(porch.exp(placeholder([4, 262144])), 1))

@@ -1,0 +1,241 @@
+"""Softmax rows split over workgroups (kernel kind row.split).
+
+Rows longer than one workgroup's register cache, in a softmax-shaped row
+program over one leaf, are split into parts of 16384 values, one part per
+workgroup held in registers; the parts of a row exchange (max, sum of
+exp(f - max)) words through a zeroed temporary, combine them as M = max m_p,
+S = sum s_p exp(m_p - M), and write their outputs from registers, so the row
+is read from memory once.  A part whose partners do not publish within a
+bounded wait computes the row's max and sum itself from memory.
+
+CPU: the planner's choice and the temporary, bounds and values of the
+kernels run on the CPU (blocks run one after another there, so a row's last
+part takes the exchange path and the others their own fallback), and a
+planted mistake in each path.  GPU: parity with the oracle at the workload's
+size and at ragged sizes and row counts, and the fallback alone, forced from
+the host with a spin limit of zero.  Bar (assert_softmax_close): 1e-6
+relative per element against the float64 softmax of the same float32
+differences, and against the oracle 1e-6 plus the oracle's own measured
+row-sum drift; NaN exactly where the oracle has NaN (the row max is the
+reference's, exactly).  On the CPU, where exp is the host's, 1e-6 against
+the oracle alone.
+"""
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+import porch_amd as porch
+from oracle import host
+from porch_amd import _lib
+from tests.helpers import CONFIG_SIZES, assert_softmax_close, config_inputs, placeholder
+from tests.kernel_emu import emulate as emu
+from tests.test_max_order import special_rows
+
+needs_clang = pytest.mark.skipif(not emu.available(), reason="host clang++ from ROCm is required")
+
+
+def _kinds(expr):
+    return [k["kind"] for k in porch.plan(expr)["kernels"]]
+
+
+def _close(out, ref, rel=1e-6):
+    out = np.asarray(out, np.float32).reshape(ref.shape)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    finite = ~np.isnan(ref)
+    err = np.abs(out[finite].astype(np.float64) - ref[finite]) / np.maximum(np.abs(ref[finite].astype(np.float64)), 1e-30)
+    assert err.size == 0 or err.max() <= rel, err.max()
+
+
+@pytest.mark.parametrize("cols, parts", [(65540, 5), (131072, 8), (200004, 13), (262144, 16), (262148, 17)])
+def test_planner_splits_long_softmax_rows(cols, parts):
+    expr = porch.softmax(placeholder([7, cols]), 1)
+    plan = porch.plan(expr)
+    assert _kinds(expr) == ["pointwise.flat", "row.split"]
+    # the temporary: one 64-bit word per row and part, zeroed by the first step
+    assert plan["temps"] == [7 * parts * 2]
+    assert plan["kernels"][0]["dest"] == "temp0" and plan["kernels"][1]["dest"] == "output"
+    # at most two workgroups per compute unit, in whole row groups per XCD
+    grid = plan["kernels"][1]["grid"][0]
+    assert grid <= 512 and grid % (8 * parts) == 0
+    source = porch.kernel_source(expr, 1)
+    assert "__launch_bounds__(256, 2)" in source
+    assert "__HIP_MEMORY_SCOPE_AGENT" in source and "__ATOMIC_RELAXED" in source
+    assert re.search(r"#define porch_spin_limit \d+", source)
+
+
+@pytest.mark.parametrize("build", [
+    lambda: porch.softmax(placeholder([4, 65536]), 1),       # fits the register cache
+    lambda: porch.softmax(placeholder([4, 262147]), 1),      # odd length: no 128-bit loads
+    lambda: porch.softmax(placeholder([4, 262144]) * placeholder([4, 262144]), 1),  # two leaves
+    lambda: porch.sum(porch.exp(placeholder([4, 262144])), 1),  # no elementwise output
+    lambda: porch.exp(placeholder([4, 262144]) - porch.broadcast_to(
+        porch.max(placeholder([4, 262144]), 1, True), [4, 262144])),  # one reduction
+])
+def test_other_row_programs_are_not_split(build):
+    assert "row.split" not in _kinds(build())
+
+
+@needs_clang
+@pytest.mark.parametrize("shape", [[3, 65540], [2, 262148]])
+def test_emulated_split_rows_match_the_oracle(shape):
+    rng = np.random.default_rng(shape[1])
+    x = (rng.standard_normal(shape) * 3).astype(np.float32)
+    x[0, 7] = 25.0  # one part's max far above the others'
+    expr = porch.softmax(placeholder(shape, x), 1)
+    assert all(r["ok"] for r in emu.emulate(expr))
+    ref = host.evaluate(expr)
+    _close(emu.evaluate(expr, [x]), ref)
+
+
+@needs_clang
+def test_emulated_special_rows_take_the_reference_max():
+    shape = [10, 65540]
+    x = special_rows(*shape, seed=5)
+    expr = porch.softmax(placeholder(shape, x), 1)
+    ref = host.evaluate(expr)
+    _close(emu.evaluate(expr, [x]), ref)
+    # every max also recomputed in the reference's order
+    _close(emu.evaluate(expr, [x], force_exact=True), ref)
+
+
+def _evaluate_planted(expr, x, old, new):
+    """emu.evaluate with `old` replaced by `new` in the split kernel."""
+    original = porch.kernel_source
+
+    def planted(e, index=0):
+        source = original(e, index)
+        if "row.split" in porch.plan(e)["kernels"][index]["kind"]:
+            assert old in source
+            source = source.replace(old, new)
+        return source
+
+    porch.kernel_source = planted
+    try:
+        return emu.evaluate(expr, [x])
+    finally:
+        porch.kernel_source = original
+
+
+@needs_clang
+@pytest.mark.parametrize("old, new, path", [
+    # the exchange: partial sums taken without rescaling to the row max
+    ("xps * porch_exp(xpm - rv0)", "xps", "exchange"),
+    # the fallback: lane sums not rescaled to the row max
+    ("acc_s = acc_s * porch_exp(acc_a - acc_m);", "", "fallback"),
+])
+def test_emulation_catches_a_planted_mistake_in_each_path(old, new, path):
+    shape = [2, 65540]
+    x = (np.random.default_rng(3).standard_normal(shape) * 3).astype(np.float32)
+    x[:, 70000 % shape[1]] = 30.0
+    x[:, 5] = 20.0
+    expr = porch.softmax(placeholder(shape, x), 1)
+    ref = host.evaluate(expr)
+    got = _evaluate_planted(expr, x, old, new).reshape(shape)
+    err = np.abs(got.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), 1e-30)
+    assert err.max() > 1e-3, path
+
+
+def test_softmax_bar_accepts_the_oracle_and_rejects_a_scaled_result():
+    # the check used on the GPU below, on the CPU: the oracle's own result
+    # passes; a result off by 3e-6 (or with one value off) does not
+    shape = [4, 65540]
+    x = (np.random.default_rng(8).standard_normal(shape) * 3).astype(np.float32)
+    t = placeholder(shape, x)
+    ref = np.asarray(host.evaluate(porch.softmax(t, 1)), np.float32).reshape(shape)
+    assert_softmax_close(ref, t, x)
+    with pytest.raises(AssertionError):
+        assert_softmax_close((ref * np.float32(1 + 3e-6)).astype(np.float32), t, x)
+    bad = ref.copy()
+    bad[2, 100] = np.nextafter(np.nextafter(np.nextafter(bad[2, 100], 1), 1), 1) * np.float32(1 + 2e-6)
+    with pytest.raises(AssertionError):
+        assert_softmax_close(bad, t, x)
+
+
+# -- GPU -----------------------------------------------------------------------
+
+
+@pytest.mark.gpu
+def test_vocab_softmax_full_size(gpu):
+    size = CONFIG_SIZES["vocab_softmax"]
+    (x,) = config_inputs("vocab_softmax")
+    shape = [size["rows"], size["cols"]]
+    t = gpu.tensor(shape, x)
+    expr = gpu.softmax(t, 1)
+    assert _kinds(expr) == ["pointwise.flat", "row.split"]
+    out = gpu.materialize(expr).cpu().reshape(shape)
+    assert_softmax_close(out, t, x)
+    assert np.allclose(out.sum(axis=1), 1.0, atol=2e-5)
+    # a second run on the same inputs: the temporary is zeroed again (bits
+    # may differ only where a part took its own fallback)
+    again = gpu.materialize(expr).cpu().reshape(shape)
+    assert np.allclose(again, out, rtol=1e-6, atol=0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows, cols", [
+    (1, 65540),      # one row, five parts, the last ragged
+    (1000, 65540),   # many rounds
+    (33, 131072),    # one round, partly filled
+    (70, 262144),    # three rounds: the odd round ends the loop
+    (97, 262144),    # four rounds, the last partly filled
+    (40, 200004),
+])
+def test_split_rows_match_the_oracle(gpu, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    x[rng.random((rows, cols)) < 0.01] = 20.0
+    t = gpu.tensor([rows, cols], x)
+    expr = gpu.softmax(t, 1)
+    assert _kinds(expr) == ["pointwise.flat", "row.split"]
+    out = gpu.materialize(expr).cpu().reshape(rows, cols)
+    assert_softmax_close(out, t, x)
+
+
+@pytest.mark.gpu
+def test_special_rows_split_on_gpu(gpu):
+    shape = [30, 131076]
+    x = special_rows(*shape, seed=17)
+    t = gpu.tensor(shape, x)
+    expr = gpu.softmax(t, 1)
+    assert _kinds(expr) == ["pointwise.flat", "row.split"]
+    out = gpu.materialize(expr).cpu().reshape(shape)
+    assert_softmax_close(out, t, x)
+
+
+@pytest.mark.gpu
+def test_fallback_alone_matches_the_oracle(gpu):
+    """Every part computes its row's max and sum itself: the kernel built
+    with a spin limit of zero never reads a partner's word, as when the
+    partners are not resident."""
+    rows, cols = 45, 65540
+    x = special_rows(rows, cols, seed=23)
+    x[10:20] = np.random.default_rng(2).standard_normal((10, cols)).astype(np.float32) * 40
+    t = gpu.tensor([rows, cols], x)
+    expr = gpu.softmax(t, 1)
+    plan = gpu.plan(expr)
+    kernel = plan["kernels"][1]
+    source = gpu.kernel_source(expr, 1)
+    forced = re.sub(r"#define porch_spin_limit \d+", "#define porch_spin_limit 0", source)
+    assert forced != source
+    code = ctypes.c_void_p()
+    _lib.check(_lib.lib.porch_compile(forced.encode(), None, 0, ctypes.byref(code)))
+    try:
+        size = _lib.lib.porch_code_object_size(code)
+        data = _lib.lib.porch_code_object_data(code)
+        # inputs as the planner lays them out: x, then the exchange words
+        # (never read here, but still written)
+        xs = gpu._Buffer.upload(x.reshape(-1))
+        words = gpu._Buffer.upload(np.zeros(plan["temps"][0], np.float32))
+        out = gpu._Buffer.upload(np.zeros(rows * cols, np.float32))
+        ins = (ctypes.c_void_p * 2)(xs.handle, words.handle)
+        # one 256-lane workgroup per "output": the kernel's own grid
+        assert kernel["block"] == 256
+        _lib.check(_lib.lib.porch_launch_fused_reduction(data, size, b"porch_row", ins, 2, out.handle,
+                                                         kernel["grid"][0]))
+        got = out.download(rows * cols).reshape(rows, cols)
+    finally:
+        _lib.lib.porch_code_object_release(code)
+    assert_softmax_close(got, t, x)
