@@ -29,6 +29,12 @@
 // The max stays the reference's: where the order-free maximum may differ
 // from the reference's block order (NaN, or a +0 maximum), it is recomputed
 // in that order from memory, as in emit_row.
+//
+// Measured on [512, 262144] (MI355X): the kernel takes the time of a plain
+// non-temporal copy of the same 512 MiB each way (about 190 us), and neither
+// the exchange (no waits at all), the arithmetic (no exp or division), a
+// third register set in flight, four workgroups per compute unit, nor other
+// chunk orders change that.
 
 #include "codegen.hpp"
 #include "emit_expr.hpp"
@@ -44,6 +50,10 @@ namespace porch::cg {
 
         constexpr int64_t part_values = 16384; // 256 lanes x 64 values
         constexpr int chunks_per_part = 16;     // float4 per lane per part
+        constexpr int groups_per_cu = 2;        // workgroups resident per compute unit
+        // Parts a workgroup holds in registers at once: one being written
+        // out, one published, and (with three) one still loading.
+        constexpr int register_sets = 2;
         // Polls of a row's partials before a workgroup computes the row
         // itself (each poll is a memory round trip plus a short sleep).
         constexpr int spin_limit = 16384;
@@ -91,7 +101,7 @@ namespace porch::cg {
             for (size_t dd = 0; dd + 1 < rank; ++dd)
                 if (leaf.index.w[dd] % 4 != 0) return sh;
             const int64_t parts = (length + part_values - 1) / part_values;
-            const int64_t resident = 2 * static_cast<int64_t>(std::max(r.compute_units, 8));
+            const int64_t resident = groups_per_cu * static_cast<int64_t>(std::max(r.compute_units, 8));
             const int64_t groups = resident / (8 * parts);
             if (groups < 1) return sh;
             int64_t rows = 1;
@@ -268,10 +278,13 @@ namespace porch::cg {
         // The row's max and sum from memory over the whole row (a
         // workgroup whose partners did not arrive): one pass, each lane
         // keeping the exact running max and a sum against an anchor moved
-        // (with the sum rescaled) only by more than 64, as in emit_row.
+        // (with the sum rescaled) only by more than 64, as in emit_row.  A
+        // lane adds L / 256 terms one after another, so it sums in double.
+        // LDS slots of its own (after the register sets').
+        const int fallback_slot = 3 * register_sets;
         auto whole_row = [&](const std::string& in) {
             std::string c;
-            c += in + "float acc_m = -PORCH_FLT_MAX;\n" + in + "float acc_a = -PORCH_FLT_MAX;\n" + in + "float acc_s = 0.0f;\n";
+            c += in + "float acc_m = -PORCH_FLT_MAX;\n" + in + "float acc_a = -PORCH_FLT_MAX;\n" + in + "double acc_s = 0.0;\n";
             c += in + "#pragma unroll 4\n";
             c += in + "for (" + std::string(T) + " xj = 0; xj < " + std::to_string((length + 1023) / 1024) + "; ++xj) {\n";
             c += in + "    const " + T + " " + qc + " = xj * 1024 + tl * 4;\n";
@@ -286,13 +299,14 @@ namespace porch::cg {
             c += in + "        const float cm = porch_fmax(porch_fmax(" + v[0] + ", " + v[1] + "), porch_fmax(" + v[2] + ", " +
                  v[3] + "));\n";
             c += in + "        acc_m = porch_fmax(acc_m, cm);\n";
-            c += in + "        if (cm > acc_a + 64.0f) {\n" + in + "            acc_s = acc_s * porch_exp(acc_a - cm);\n" + in +
-                 "            acc_a = cm;\n" + in + "        }\n";
-            for (int e = 0; e < 4; ++e) c += in + "        acc_s += porch_exp(" + v[e] + " - acc_a);\n";
+            c += in + "        if (cm > acc_a + 64.0f) {\n" + in +
+                 "            acc_s = acc_s * (double)porch_exp(acc_a - cm);\n" + in + "            acc_a = cm;\n" + in +
+                 "        }\n";
+            for (int e = 0; e < 4; ++e) c += in + "        acc_s += (double)porch_exp(" + v[e] + " - acc_a);\n";
             c += in + "    }\n" + in + "}\n";
-            c += block_reduce("acc_m", true, 0, in);
-            c += in + "acc_s = acc_s * porch_exp(acc_a - acc_m);\n";
-            c += block_reduce("acc_s", false, 1, in);
+            c += block_reduce("acc_m", true, fallback_slot, in);
+            c += in + "float acc_l = (float)(acc_s * (double)porch_exp(acc_a - acc_m));\n";
+            c += block_reduce("acc_l", false, fallback_slot + 1, in);
             return c;
         };
         // The reference's block order for a max whose order-free value may
@@ -344,7 +358,7 @@ namespace porch::cg {
             c += i2 + "if (xstat[" + S + "][2] != 0.0f) {\n";
             c += whole_row(i2 + "    ");
             c += exact_max("acc_m", i2 + "    ");
-            c += i2 + "    rv0 = acc_m;\n" + i2 + "    rv1 = acc_s;\n";
+            c += i2 + "    rv0 = acc_m;\n" + i2 + "    rv1 = acc_l;\n";
             c += i2 + "}\n" + i2 + "else {\n";
             c += exact_max("rv0", i2 + "    ");
             c += i2 + "    if (wave == 0) {\n";
@@ -354,9 +368,10 @@ namespace porch::cg {
             c += i2 + "    __syncthreads();\n";
             c += i2 + "    rv1 = xstat[" + S + "][1];\n";
             c += i2 + "}\n";
+            // written once and not read again here: past the caches
             auto store = [&](const std::vector<std::string>& v) {
-                return i2 + "        *reinterpret_cast<float4*>(out + row * " + L + " + " + qc + ") = make_float4(" +
-                       v[0] + ", " + v[1] + ", " + v[2] + ", " + v[3] + ");\n";
+                return i2 + "        __builtin_nontemporal_store((porch_v4f){" + v[0] + ", " + v[1] + ", " + v[2] + ", " +
+                       v[3] + "}, reinterpret_cast<porch_v4f*>(out + row * " + L + " + " + qc + "));\n";
             };
             std::string general;
             {
@@ -416,26 +431,47 @@ namespace porch::cg {
                  "    return __builtin_fmaf(__builtin_fmaf(-b, q, a), r, q);\n}\n";
         }
         s += "#define porch_spin_limit " + std::to_string(spin_limit) + "\n";
-        s += "extern \"C\" __global__ void __launch_bounds__(256, 2) porch_row(" + params + ") {\n";
+        s += "extern \"C\" __global__ void __launch_bounds__(256, " + std::to_string(groups_per_cu) + ") porch_row(" + params +
+             ") {\n";
         s += "    const int tl = threadIdx.x;\n    const int lane = tl & 63;\n    const int wave = tl >> 6;\n";
-        s += "    __shared__ float xred[6][4];\n    __shared__ float xstat[2][3];\n    __shared__ float ex[257];\n";
+        s += "    __shared__ float xred[" + std::to_string(3 * register_sets + 2) + "][4];\n";
+        s += "    __shared__ float xstat[" + std::to_string(register_sets) + "][3];\n    __shared__ float ex[257];\n";
         s += "    const int xcd = (int)(blockIdx.x % 8);\n    const int xslot = (int)(blockIdx.x / 8);\n";
         s += "    const int group = xslot / " + P + ";\n    const int part = xslot % " + P + ";\n";
         s += "    unsigned long long* __restrict__ xw = reinterpret_cast<unsigned long long*>(a" +
              std::to_string(r.split_slot) + ");\n";
-        s += "    float xa[" + std::to_string(chunks_per_part) + "][4];\n    float xb[" + std::to_string(chunks_per_part) +
-             "][4];\n";
+        // Register set i holds items i, i + n, i + 2n, ... (n sets).  Step
+        // for item t: load item t + n - 1 (into the set item t - 1 left),
+        // publish item t + 1, write item t out.  A part thus waits for its
+        // partners' words of item t a whole step after publishing its own,
+        // and with three sets its loads stay in flight across a step.
+        const int n_sets = register_sets;
+        std::vector<std::string> X;
+        for (int i = 0; i < n_sets; ++i) {
+            X.push_back("x" + std::string(1, static_cast<char>('a' + i)));
+            s += "    float " + X.back() + "[" + std::to_string(chunks_per_part) + "][4];\n";
+            if (sh.fast_output) s += "    float xn" + X.back() + " = 0.0f;\n";
+        }
         s += "    float xpm = 0.0f;\n    float xps = 0.0f;\n";
-        if (sh.fast_output) s += "    float xnxa = 0.0f;\n    float xnxb = 0.0f;\n";
         const std::string R = std::to_string(sh.rounds);
-        s += load_item("xa", "0") + publish("xa", "0", 0);
-        s += "    for (int k = 0; k < " + R + "; k += 2) {\n";
-        s += "    if (k + 1 < " + R + ") {\n" + load_item("xb", "k + 1") + publish("xb", "k + 1", 3) + "    }\n";
-        s += finish("xa", "k", 0);
-        s += "    if (k + 1 < " + R + ") {\n";
-        s += "    if (k + 2 < " + R + ") {\n" + load_item("xa", "k + 2") + publish("xa", "k + 2", 0) + "    }\n";
-        s += finish("xb", "k + 1", 1);
-        s += "    }\n    }\n}\n";
+        auto guarded = [&](const std::string& cond, const std::string& code) {
+            return "    if (" + cond + ") {\n" + code + "    }\n";
+        };
+        for (int i = 0; i + 1 < n_sets; ++i)
+            s += guarded(std::to_string(i) + " < " + R, load_item(X[i], std::to_string(i)));
+        s += publish(X[0], "0", 0);
+        s += "    for (int k = 0; k < " + R + "; k += " + std::to_string(n_sets) + ") {\n";
+        for (int t = 0; t < n_sets; ++t) {
+            const auto item = [&](int d) { return "k + " + std::to_string(t + d); };
+            std::string step;
+            const int load_set = (t + n_sets - 1) % n_sets;
+            const int pub_set = (t + 1) % n_sets;
+            step += guarded(item(n_sets - 1) + " < " + R, load_item(X[load_set], item(n_sets - 1)));
+            step += guarded(item(1) + " < " + R, publish(X[pub_set], item(1), 3 * pub_set));
+            step += finish(X[t], item(0), t);
+            s += t == 0 ? step : guarded(item(0) + " < " + R, step);
+        }
+        s += "    }\n}\n";
         return kc;
     }
 

@@ -87,14 +87,13 @@ _ORDER_TEST = "return m != m || __builtin_bit_cast(unsigned, m) == 0u;"
 
 
 # Blocks run one after another here, so a wait on a later block's partial
-# never ends: two polls (the second after a wave-wide step, so that a
-# block's own partial, stored by another of its threads, is visible), then
-# the waiting block's own fallback.
+# never ends: a few hundred polls (each yielding, time for the other waves
+# of the block to publish theirs), then the waiting wave's own fallback.
 _SPIN = re.compile(r"#define porch_spin_limit \d+")
 
 
 def _emulated(source: str) -> str:
-    return _SPIN.sub("#define porch_spin_limit 2", source)
+    return _SPIN.sub("#define porch_spin_limit 200", source)
 
 
 def emulate(expr, timeout: float = 120.0, only=None, force_exact: bool = False) -> list[dict]:
