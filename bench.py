@@ -26,7 +26,8 @@ for a copy kernel of known size; both come from the counter summaries under
 profiles/ (null when a workload has none).
 
     python bench.py [--steps K] [--warmup W] [--configs view_chain,...] [--no-cpu]
-    python bench.py --controls LAUNCHES   (elementwise control kernels, under rocprofv3)
+    python bench.py --controls LAUNCHES   (control kernels beside the elementwise and
+                                          vocabulary-softmax workloads, under rocprofv3)
 """
 
 from __future__ import annotations
@@ -386,13 +387,27 @@ extern "C" __global__ void __launch_bounds__(256) porch_control_copy(
     const porch_v4f x = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0) + g);
     reinterpret_cast<float4*>(out)[g] = make_float4(x.x, x.y, x.z, x.w);
 }
+// A plain copy at a large size: `count` lanes, each copying four float4 of
+// a0 to out, strided by the lane count (non-temporal loads and stores).
+extern "C" __global__ void __launch_bounds__(256) porch_control_stream(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {
+    const unsigned long long g = blockIdx.x * 256ull + threadIdx.x;
+    if (g >= count) return;
+    const porch_v4f* x = reinterpret_cast<const porch_v4f*>(a0);
+    porch_v4f* y = reinterpret_cast<porch_v4f*>(out);
+    for (int r = 0; r < 4; ++r)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(x + g + r * count), y + g + r * count);
+}
 """
 
 
 def controls(launches: int) -> int:
     """Each control kernel, then the elementwise workload's own kernel,
-    `launches` times each over rotated (cache-cold) buffers; timed by the
-    profiler this runs under (rocprofv3 --kernel-trace --stats)."""
+    `launches` times each over rotated (cache-cold) buffers; then a plain
+    copy of the vocabulary softmax's bytes and that workload itself,
+    `launches` times each; timed by the profiler this runs under
+    (rocprofv3 --kernel-trace --stats)."""
     import porch_amd as porch
     from porch_amd import _lib
     from porch_amd.workloads import config_graph, config_inputs, config_shapes
@@ -419,6 +434,25 @@ def controls(launches: int) -> int:
         porch.materialize(config_graph("elementwise", sets[i % copies]))
     porch.synchronize()
     log(f"controls: elementwise workload x {launches}")
+    del sets, outs
+
+    # The vocabulary softmax beside a plain copy of the same bytes (512 MiB
+    # each way: twice the Infinity Cache, so no launch finds its data there).
+    shape = config_shapes("vocab_softmax")[0]
+    total = shape[0] * shape[1]
+    (values,) = config_inputs("vocab_softmax")
+    x = porch.tensor(shape, values)
+    y = porch.zeros([total]).realize()
+    ins = (ctypes.c_void_p * 2)(x.device_data().handle, x.device_data().handle)
+    for _ in range(launches):
+        _lib.check(_lib.lib.porch_launch_fused_elementwise(
+            data, size, b"porch_control_stream", ins, 2, y.device_data().handle, total // 16))
+    porch.synchronize()
+    log(f"controls: porch_control_stream x {launches}")
+    for _ in range(launches):
+        porch.materialize(config_graph("vocab_softmax", [x]))
+    porch.synchronize()
+    log(f"controls: vocab_softmax workload x {launches}")
     _lib.lib.porch_code_object_release(code)
     return 0
 
