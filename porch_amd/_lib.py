@@ -11,7 +11,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIBRARY_PATH = os.path.join(_HERE, "libporch_amd.so")
+# PORCH_AMD_LIBRARY names another build of the same library (the
+# sanitizer builds of porch_amd/Makefile) to load in its place.
+LIBRARY_PATH = os.environ.get("PORCH_AMD_LIBRARY") or os.path.join(_HERE, "libporch_amd.so")
 
 OK = 0
 ERR_INVALID_ARGUMENT = 1
