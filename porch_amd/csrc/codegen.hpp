@@ -16,9 +16,9 @@
 //                    read once into registers, each row reduction is a
 //                    register fold plus a wave butterfly, and the outputs (or
 //                    the row's reduction) are written in the same pass;
-//   row.split        softmax-shaped rows too long for one workgroup's
-//                    registers: each row split over workgroups that exchange
-//                    partial (max, sum) words, so the row is read once;
+//   row.split        softmax-shaped rows of more than 32768 values: each row
+//                    split over workgroups that exchange partial (max, sum)
+//                    words, so the row is read once;
 //   reduce.column    one lane per output, sequential fold over a non-last
 //                    axis with lanes along the contiguous output dimension;
 //   gemm             LDS-tiled v_mfma_f32_32x32x2f32 with the elementwise
@@ -88,10 +88,10 @@ namespace porch::cg {
     };
 
     kernel_code emit_row(const row_request& request);
-    // How many workgroups each row is split over (0: not split): rows too
-    // long for one workgroup's registers, in a softmax-shaped program
-    // (a max, then a sum of exp(f - that max), then an elementwise output)
-    // over a single leaf, so that each row is read from memory once.
+    // How many workgroups each row is split over (0: not split): rows of
+    // more than 32768 values in a softmax-shaped program (a max, then a
+    // sum of exp(f - that max), then an elementwise output) over a single
+    // leaf, so that each row is read from memory once.
     int64_t row_split_parts(const row_request& request);
     // Floats of the exchange temporary a split row program needs.
     int64_t row_split_temp_floats(const row_request& request);

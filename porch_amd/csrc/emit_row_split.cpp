@@ -1,8 +1,9 @@
-// Softmax-shaped row programs over rows too long for one workgroup's
-// registers, read from memory once.  The row program row_request describes
-// (a max of f, a sum of exp(f - that max), an elementwise output) runs with
-// each row split into parts of 16384 values, one part per 256-lane
-// workgroup held in registers (64 values per lane).  Each part publishes its
+// Softmax-shaped row programs over long rows (more than 32768 values), read
+// from memory once.  The row program row_request describes (a max of f, a
+// sum of exp(f - that max), an elementwise output) runs with each row split
+// into parts of at most 16384 values (as even as whole chunks of 1024
+// allow), one part per 256-lane workgroup held in registers (up to 64
+// values per lane).  Each part publishes its
 // partial (max m, sum of exp(f - m)) as one 64-bit word; the parts of a row
 // then combine the row's partials the same way, M = max of the m, S = sum
 // of s exp(m - M) in part order, and write their outputs from registers.
@@ -48,8 +49,9 @@
 namespace porch::cg {
     namespace {
 
-        constexpr int64_t part_values = 16384; // 256 lanes x 64 values
-        constexpr int chunks_per_part = 16;     // float4 per lane per part
+        // At most 16 chunks of 1024 values per part (64 values per lane);
+        // a row's parts are as even as whole chunks allow.
+        constexpr int64_t max_chunks = 16;
         constexpr int groups_per_cu = 2;        // workgroups resident per compute unit
         // Parts a workgroup holds in registers at once: one being written
         // out, one published, and (with three) one still loading.
@@ -60,6 +62,7 @@ namespace porch::cg {
 
         struct split_shape {
             int64_t parts = 0;
+            int64_t chunks = 0; // chunks of 1024 values (4 per lane) per part
             int64_t groups = 0; // row groups per XCD per round
             int64_t grid = 0;
             int64_t rounds = 0;
@@ -78,7 +81,11 @@ namespace porch::cg {
             const size_t rank = r.shape.size();
             const size_t col = rank - 1;
             const int64_t length = r.shape[col];
-            if (length <= 65536 || length % 4 != 0) return sh;
+            // Rows of up to 32768 values are at least as fast in one
+            // workgroup (emit_row); beyond, the split form is faster
+            // (softmax over 1 GiB of rows of 32772 / 40964 / 49156 / 65536
+            // values: 225 / 226 / 231 / 215 -> 206 / 211 / 222 / 194 us).
+            if (length <= 32768 || length % 4 != 0) return sh;
             // the online pair: sum of exp(f - rv0) with f the max's producer
             const knode& g = k.at(r.reductions[1].producer);
             if (g.op != kop::exp) return sh;
@@ -100,13 +107,15 @@ namespace porch::cg {
             if (!leaf.index.is_affine || leaf.index.w[col] != 1 || leaf.index.c0 % 4 != 0) return sh;
             for (size_t dd = 0; dd + 1 < rank; ++dd)
                 if (leaf.index.w[dd] % 4 != 0) return sh;
-            const int64_t parts = (length + part_values - 1) / part_values;
+            const int64_t parts = (length + max_chunks * 1024 - 1) / (max_chunks * 1024);
+            const int64_t chunks = (length + parts * 1024 - 1) / (parts * 1024);
             const int64_t resident = groups_per_cu * static_cast<int64_t>(std::max(r.compute_units, 8));
             const int64_t groups = resident / (8 * parts);
             if (groups < 1) return sh;
             int64_t rows = 1;
             for (size_t dd = 0; dd + 1 < rank; ++dd) rows *= r.shape[dd];
             sh.parts = parts;
+            sh.chunks = chunks;
             sh.groups = groups;
             sh.grid = 8 * parts * groups;
             sh.rounds = (rows + 8 * groups - 1) / (8 * groups);
@@ -185,8 +194,8 @@ namespace porch::cg {
         };
         auto chunk_loop = [&](const std::string& indent, const std::string& body) {
             std::string c = indent + "#pragma unroll\n";
-            c += indent + "for (int j = 0; j < " + std::to_string(chunks_per_part) + "; ++j) {\n";
-            c += indent + "    const " + T + " " + qc + " = (" + T + ")part * " + std::to_string(part_values) +
+            c += indent + "for (int j = 0; j < " + std::to_string(sh.chunks) + "; ++j) {\n";
+            c += indent + "    const " + T + " " + qc + " = (" + T + ")part * " + std::to_string(sh.chunks * 1024) +
                  " + j * 1024 + tl * 4;\n";
             c += indent + "    if (" + qc + " < " + L + ") {\n" + body + indent + "    }\n";
             c += indent + "}\n";
@@ -449,7 +458,7 @@ namespace porch::cg {
         std::vector<std::string> X;
         for (int i = 0; i < n_sets; ++i) {
             X.push_back("x" + std::string(1, static_cast<char>('a' + i)));
-            s += "    float " + X.back() + "[" + std::to_string(chunks_per_part) + "][4];\n";
+            s += "    float " + X.back() + "[" + std::to_string(sh.chunks) + "][4];\n";
             if (sh.fast_output) s += "    float xn" + X.back() + " = 0.0f;\n";
         }
         s += "    float xpm = 0.0f;\n    float xps = 0.0f;\n";

@@ -1,8 +1,8 @@
 """Softmax rows split over workgroups (kernel kind row.split).
 
-Rows longer than one workgroup's register cache, in a softmax-shaped row
-program over one leaf, are split into parts of 16384 values, one part per
-workgroup held in registers; the parts of a row exchange (max, sum of
+Rows of more than 32768 values, in a softmax-shaped row program over one
+leaf, are split into parts of at most 16384 values (as even as whole chunks
+of 1024 allow), one part per workgroup held in registers; the parts of a row exchange (max, sum of
 exp(f - max)) words through a zeroed temporary, combine them as M = max m_p,
 S = sum s_p exp(m_p - M), and write their outputs from registers, so the row
 is read from memory once.  A part whose partners do not publish within a
@@ -40,7 +40,8 @@ def _kinds(expr):
     return [k["kind"] for k in porch.plan(expr)["kernels"]]
 
 
-@pytest.mark.parametrize("cols, parts", [(65540, 5), (131072, 8), (200004, 13), (262144, 16), (262148, 17)])
+@pytest.mark.parametrize("cols, parts", [(32772, 3), (40964, 3), (65536, 4), (65540, 5), (131072, 8), (200004, 13),
+                                         (262144, 16), (262148, 17)])
 def test_planner_splits_long_softmax_rows(cols, parts):
     expr = porch.softmax(placeholder([7, cols]), 1)
     plan = porch.plan(expr)
@@ -58,7 +59,7 @@ def test_planner_splits_long_softmax_rows(cols, parts):
 
 
 @pytest.mark.parametrize("build", [
-    lambda: porch.softmax(placeholder([4, 65536]), 1),       # fits the register cache
+    lambda: porch.softmax(placeholder([4, 32768]), 1),       # as fast in one workgroup
     lambda: porch.softmax(placeholder([4, 262147]), 1),      # odd length: no 128-bit loads
     lambda: porch.softmax(placeholder([4, 262144]) * placeholder([4, 262144]), 1),  # two leaves
     lambda: porch.sum(porch.exp(placeholder([4, 262144])), 1),  # no elementwise output
@@ -70,7 +71,7 @@ def test_other_row_programs_are_not_split(build):
 
 
 @needs_clang
-@pytest.mark.parametrize("shape", [[3, 65540], [2, 262148]])
+@pytest.mark.parametrize("shape", [[3, 65540], [2, 262148], [2, 40964]])
 def test_emulated_split_rows_match_the_oracle(shape):
     rng = np.random.default_rng(shape[1])
     x = (rng.standard_normal(shape) * 3).astype(np.float32)
