@@ -231,3 +231,35 @@ def test_fallback_alone_matches_the_oracle(gpu):
     finally:
         _lib.lib.porch_code_object_release(code)
     assert_softmax_close(got, t, x)
+
+
+@pytest.mark.gpu
+def test_two_split_softmaxes_on_two_streams_at_once(gpu):
+    """Two threads (each with its own stream) materialise split softmaxes
+    at the same time.  Their workgroups then share the GPU, so a row's
+    parts may not all be resident together; a part that waits too long
+    computes its row alone.  Both results must still match the oracle."""
+    import threading
+
+    shape = [256, 131072]
+    inputs = [(np.random.default_rng(50 + i).standard_normal(shape) * 3).astype(np.float32) for i in range(2)]
+    tensors = [gpu.tensor(shape, x) for x in inputs]
+    results = [None, None]
+    errors = []
+
+    def run(i):
+        try:
+            outs = [gpu.materialize(gpu.softmax(tensors[i], 1)) for _ in range(4)]
+            results[i] = [o.cpu().reshape(shape) for o in outs]
+        except Exception as e:  # reported below, on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        for out in results[i]:
+            assert_softmax_close(out, tensors[i], inputs[i])

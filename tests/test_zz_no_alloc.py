@@ -8,7 +8,8 @@ NaN), on two calls in a row for each graph, the second with a smaller
 input: the array keeps the first call's contents, so a temporary read
 before it is written would show.  Graphs with temporaries of every kind:
 split column reductions (partials), memoised reductions, a materialised
-product operand; and one without.  Sizes past the array's limit, and an
+product operand, split softmax rows (exchange words that a fill kernel
+must zero before each launch); and one without.  Sizes past the array's limit, and an
 output buffer too small, are rejected before any launch.
 """
 
@@ -67,6 +68,11 @@ def softmax_first_axis(shape, seed):
     return porch.softmax(porch.tensor(shape, rand(shape, seed, 3.0)), 0)
 
 
+def split_softmax_rows(shape, seed):
+    # rows split over workgroups: a zeroed exchange temporary, then the rows
+    return porch.softmax(porch.tensor(shape, rand(shape, seed, 3.0)), 1)
+
+
 def split_column_max(shape, seed):
     return porch.max(porch.tensor(shape, rand(shape, seed)), 0, False)
 
@@ -92,6 +98,7 @@ CASES = {
     # arguments, kernels of each call)
     "softmax over the first axis": (softmax_first_axis, ([6000, 200],), ([3000, 100],), (5, 3)),
     "split column max": (split_column_max, ([262144, 8],), ([131072, 8],), (2, 2)),
+    "split softmax rows": (split_softmax_rows, ([40, 131072],), ([9, 65540],), (2, 2)),
     "product of an expression": (product_of_expression, (512, 256, 384), (200, 96, 136), (2, 2)),
     "nested reduction": (nested_reduction, ([300, 500],), ([70, 30],), (2, 2)),
     "no temporaries": (elementwise, (1 << 20,), (1000,), (1, 1)),
