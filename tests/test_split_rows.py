@@ -93,6 +93,38 @@ def test_emulated_special_rows_take_the_reference_max():
     assert_softmax_close(emu.evaluate(expr, [x], force_exact=True).reshape(shape), t, x)
 
 
+# Other programs of the split form: f an expression of the leaf, the leaf a
+# view (a column offset that keeps 128-bit alignment), more than one row
+# dimension.  (`storage`: the leaf's values; `build`: the graph over it.)
+FORMS = {
+    "scaled": ([3, 65540], lambda t: porch.softmax(t * 0.5 + 1.0, 1), lambda x: x * np.float32(0.5) + np.float32(1.0)),
+    "view": ([3, 65544], lambda t: porch.softmax(t[porch.slice(0, 3), porch.slice(4, 65544)], 1), lambda x: x[:, 4:]),
+    "rank3": ([2, 3, 40964], lambda t: porch.softmax(t, 2), lambda x: x.reshape(6, 40964)),
+}
+
+
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_other_forms_are_split(form):
+    shape, build, _ = FORMS[form]
+    assert _kinds(build(placeholder(shape))) == ["pointwise.flat", "row.split"]
+    # a column offset that breaks 128-bit alignment is not split
+    if form == "view":
+        t = placeholder(shape)
+        assert "row.split" not in _kinds(porch.softmax(t[porch.slice(0, 3), porch.slice(1, 65541)], 1))
+
+
+@needs_clang
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_emulated_other_forms_match_the_oracle(form):
+    shape, build, _ = FORMS[form]
+    x = (np.random.default_rng(9).standard_normal(shape) * 3).astype(np.float32)
+    expr = build(placeholder(shape, x))
+    got = emu.evaluate(expr, [x])
+    ref = host.evaluate(expr)
+    rel = np.abs(got.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), 1e-30)
+    assert rel.max() <= 2e-6, rel.max()
+
+
 def _evaluate_planted(expr, x, old, new):
     """emu.evaluate with `old` replaced by `new` in the split kernel."""
     original = porch.kernel_source
@@ -263,3 +295,23 @@ def test_two_split_softmaxes_on_two_streams_at_once(gpu):
     for i in range(2):
         for out in results[i]:
             assert_softmax_close(out, tensors[i], inputs[i])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_other_forms_on_gpu(gpu, form):
+    shape, build, rows_of = FORMS[form]
+    x = (np.random.default_rng(19).standard_normal(shape) * 3).astype(np.float32)
+    t = gpu.tensor(shape, x)
+    expr = build(t)
+    assert _kinds(expr) == ["pointwise.flat", "row.split"]
+    out = gpu.materialize(expr).cpu()
+    ref = host.evaluate(expr)
+    # the oracle's softmax of the same rows: 1e-6 beyond its own row-sum
+    # drift, and the float64 softmax of the same differences (the rows as
+    # the leaf's values arrive at the row program)
+    rows = np.ascontiguousarray(rows_of(x))
+    flat = rows.reshape(-1, rows.shape[-1])
+    t2 = placeholder(list(flat.shape), flat)
+    assert_softmax_close(out.reshape(flat.shape), t2, flat)
+    assert np.allclose(out.reshape(-1), ref.reshape(-1), rtol=3e-6, atol=0)
