@@ -3,11 +3,11 @@
 // sum of exp(f - that max), an elementwise output) runs with each row split
 // into parts of at most 16384 values (as even as whole chunks of 1024
 // allow), one part per 256-lane workgroup held in registers (up to 64
-// values per lane).  Each part publishes its
-// partial (max m, sum of exp(f - m)) as one 64-bit word; the parts of a row
-// then combine the row's partials the same way, M = max of the m, S = sum
-// of s exp(m - M) in part order, and write their outputs from registers.
-// The whole-workgroup form (emit_row) reads such rows twice.
+// values per lane).  Each part publishes its partial (max m, sum s of
+// exp(f - m)) as one 64-bit word; every part of a row then combines the
+// row's words, M = max of the m and S = sum of s exp(m - M), and writes its
+// outputs from registers.  The one-workgroup form (emit_row) reads rows
+// past its register cache twice.
 //
 // Exchange: the partials go to a temporary zeroed before the launch (a
 // published word is never zero: its sum is at least 1, or NaN, or its max
@@ -52,7 +52,9 @@ namespace porch::cg {
         // At most 16 chunks of 1024 values per part (64 values per lane);
         // a row's parts are as even as whole chunks allow.
         constexpr int64_t max_chunks = 16;
-        constexpr int groups_per_cu = 2;        // workgroups resident per compute unit
+        // Workgroups resident per compute unit (the register budget allows
+        // two at 225 VGPRs).
+        constexpr int groups_per_cu = 2;
         // Parts a workgroup holds in registers at once: one being written
         // out, one published, and (with three) one still loading.
         constexpr int register_sets = 2;
