@@ -16,6 +16,8 @@
 //                    read once into registers, each row reduction is a
 //                    register fold plus a wave butterfly, and the outputs (or
 //                    the row's reduction) are written in the same pass;
+//   row.partial,     a single fold over few long rows: partials of pieces of
+//   row.combine      each row in one kernel, combined per row in a second;
 //   row.split        softmax-shaped rows of more than 32768 values: each row
 //                    split over workgroups that exchange partial (max, sum)
 //                    words, so the row is read once;
@@ -98,6 +100,14 @@ namespace porch::cg {
     // The split form (emit_row_split.cpp); `request.split_slot` and
     // `split_parts` set, the temporary zeroed before the launch.
     kernel_code emit_row_split(const row_request& request);
+    // A single fold per row over few, long rows (emit_row_partial.cpp): the
+    // number of pieces each row is split into (0: not split), then the two
+    // kernels: partials of every (row, piece) into a [rows, parts]
+    // temporary (the kernel's `out`), and their combination per row from
+    // slot `partial_slot`.
+    int64_t row_partial_parts(const row_request& request);
+    kernel_code emit_row_partial(const row_request& request);
+    kernel_code emit_row_combine(const row_request& request, int partial_slot);
 
     struct column_reduce_request {
         const kexpr* expr = nullptr;

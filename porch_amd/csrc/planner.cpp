@@ -362,6 +362,20 @@ namespace porch::plan {
                 r.n_slots = n_slots();
                 r.width = width;
                 r.compute_units = compute_units;
+                const int64_t pieces = cg::row_partial_parts(r);
+                if (pieces > 1) {
+                    // Few long rows folded into one value each: partials of
+                    // the rows' pieces into a temporary, then per row.
+                    int64_t rows = 1;
+                    for (size_t d = 0; d + 1 < row_shape.size(); ++d) rows *= row_shape[d];
+                    const int t = static_cast<int>(plan.temp_elems.size());
+                    plan.temp_elems.push_back(rows * pieces);
+                    add_step(cg::emit_row_partial(r), {arg_ref::kind::temp, t});
+                    cg::row_request c = r;
+                    c.n_slots = n_slots();
+                    add_step(cg::emit_row_combine(c, g.n_inputs + t), dest);
+                    return true;
+                }
                 const int64_t parts = cg::row_split_parts(r);
                 if (parts > 0) {
                     // Rows split over workgroups exchange partials through a
