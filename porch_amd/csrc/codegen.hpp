@@ -24,7 +24,9 @@
 //   reduce.column    one lane per output, sequential fold over a non-last
 //                    axis with lanes along the contiguous output dimension;
 //   gemm             LDS-tiled v_mfma_f32_32x32x2f32 with the elementwise
-//                    epilogue applied to the accumulators before the store.
+//                    epilogue applied to the accumulators before the store;
+//   gemm.rows,       products with a few rows (or columns), streaming the
+//   gemm.cols        long operand once.
 
 #include "lower.hpp"
 
@@ -159,5 +161,17 @@ namespace porch::cg {
     };
 
     kernel_code emit_gemm(const gemm_request& request);
+
+    // Products with one short side (emit_gemm_skinny.cpp).  A few rows
+    // (m <= 32, n >= 256): `gemm_few_rows_partials` floats of partial
+    // products (0: one K chunk, the first kernel writes the result), then
+    // their sum per output with the epilogue, reading slot `partial_slot`.
+    bool gemm_few_rows(const gemm_request& request);
+    int64_t gemm_few_rows_partials(const gemm_request& request);
+    kernel_code emit_gemm_few_rows(const gemm_request& request);
+    kernel_code emit_gemm_few_rows_combine(const gemm_request& request, int partial_slot);
+    // A few columns (n <= 4, m >= 64): one wave per output row.
+    bool gemm_few_cols(const gemm_request& request);
+    kernel_code emit_gemm_few_cols(const gemm_request& request);
 
 } // namespace porch::cg

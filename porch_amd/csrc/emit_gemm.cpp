@@ -7,40 +7,35 @@
 // the same kernels over (batch entry, tile) pairs, each entry's operands
 // offset by their batch strides.
 
-#include "codegen.hpp"
-#include "emit_expr.hpp"
+#include "emit_gemm.hpp"
 
 #include <algorithm>
 #include <stdexcept>
 
 namespace porch::cg {
+
+    std::string operand_index(const gemm_operand& op, const std::string& row, const std::string& col,
+                              const std::string& batch) {
+        std::string s = std::to_string(op.offset);
+        if (!batch.empty() && op.stride_batch != 0)
+            s += " + (idx_t)(" + batch + ") * " + std::to_string(op.stride_batch);
+        s += " + (idx_t)(" + row + ") * " + std::to_string(op.stride_row);
+        s += " + (idx_t)(" + col + ") * " + std::to_string(op.stride_col);
+        return s;
+    }
+
+    void epilogue_emitter(emitter& em, const gemm_request& r, const std::vector<std::string>& names,
+                          const std::string& acc) {
+        const kexpr& k = *r.expr;
+        em.load = [&k, &names](int id) {
+            const knode& n = k.at(id);
+            return std::vector<std::string>{"a" + std::to_string(n.slot) + "[" + index_text(n.index, names) + "]"};
+        };
+        em.condition = [&names](const kcond& c) { return index_text(c.lhs, names) + " < " + std::to_string(c.bound); };
+        em.row_value = [acc](int) { return acc; };
+    }
+
     namespace {
-
-        std::string operand_index(const gemm_operand& op, const std::string& row,
-                                  const std::string& col, const std::string& batch = "") {
-            std::string s = std::to_string(op.offset);
-            if (!batch.empty() && op.stride_batch != 0)
-                s += " + (idx_t)(" + batch + ") * " + std::to_string(op.stride_batch);
-            s += " + (idx_t)(" + row + ") * " + std::to_string(op.stride_row);
-            s += " + (idx_t)(" + col + ") * " + std::to_string(op.stride_col);
-            return s;
-        }
-
-        void epilogue_emitter(emitter& em, const gemm_request& r,
-                              const std::vector<std::string>& names,
-                              const std::string& acc) {
-            const kexpr& k = *r.expr;
-            em.load = [&k, &names](int id) {
-                const knode& n = k.at(id);
-                return std::vector<std::string>{
-                    "a" + std::to_string(n.slot) + "[" + index_text(n.index, names) + "]"
-                };
-            };
-            em.condition = [&names](const kcond& c) {
-                return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
-            };
-            em.row_value = [acc](int) { return acc; };
-        }
 
         kernel_code emit_gemm_scalar(const gemm_request& r) {
             kernel_code kc;

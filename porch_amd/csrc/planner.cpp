@@ -251,6 +251,26 @@ namespace porch::plan {
                 r.n_slots = n_slots();
                 r.width = width;
                 r.compute_units = compute_units;
+                if (cg::gemm_few_rows(r)) {
+                    // A few rows: chunks of K in parallel, their partial
+                    // products summed by a second kernel (none with one chunk).
+                    const int64_t partials = cg::gemm_few_rows_partials(r);
+                    if (partials == 0) {
+                        add_step(cg::emit_gemm_few_rows(r), dest);
+                        return true;
+                    }
+                    const int t = static_cast<int>(plan.temp_elems.size());
+                    plan.temp_elems.push_back(partials);
+                    add_step(cg::emit_gemm_few_rows(r), {arg_ref::kind::temp, t});
+                    cg::gemm_request c = r;
+                    c.n_slots = n_slots();
+                    add_step(cg::emit_gemm_few_rows_combine(c, g.n_inputs + t), dest);
+                    return true;
+                }
+                if (cg::gemm_few_cols(r)) {
+                    add_step(cg::emit_gemm_few_cols(r), dest);
+                    return true;
+                }
                 add_step(cg::emit_gemm(r), dest);
                 return true;
             }

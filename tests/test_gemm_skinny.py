@@ -1,0 +1,125 @@
+"""Matmuls with one short side (kernel kinds gemm.rows, gemm.rows_combine,
+gemm.cols): a few rows (a vector times a matrix, a small batch of rows) or a
+few columns (a matrix times a vector).
+
+Bars: bit for bit on integer data (every partial sum exact, whatever the
+order); on real data within the accumulation bound (K - 1) u sum |a b| per
+output of a float64 product (u = 2^-24), any summation order meeting it;
+the epilogue on top as in the matmul tests.  CPU: the planner's choice and
+the kernels run on the CPU (bounds, and values on integer data).  GPU: the
+same shapes and layouts against the oracle and float64.
+"""
+
+import numpy as np
+import pytest
+
+import porch_amd as porch
+from oracle import host
+from tests.helpers import placeholder
+from tests.kernel_emu import emulate as emu
+
+needs_clang = pytest.mark.skipif(not emu.available(), reason="host clang++ from ROCm is required")
+
+
+def _kinds(expr):
+    return [k["kind"] for k in porch.plan(expr)["kernels"]]
+
+
+def _ints(shape, seed):
+    return np.random.default_rng(seed).integers(-3, 4, size=shape).astype(np.float32)
+
+
+def _reals(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+# name: (operand shapes (storage), graph over the two tensors, the product
+# of two arrays as the graph takes it, the epilogue on that product,
+# expected kernels)
+CASES = {
+    "vector times matrix": (
+        ([1, 4096], [4096, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.rows", "gemm.rows_combine"]),
+    "eight rows, relu epilogue": (
+        ([8, 2048], [2048, 1024]), lambda a, b: porch.relu(porch.matmul(a, b) - 1.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p - 1.0, 0.0), ["gemm.rows", "gemm.rows_combine"]),
+    "rows, ragged columns": (
+        ([3, 777], [777, 1003]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.rows", "gemm.rows_combine"]),
+    "rows, transposed B": (
+        ([2, 1024], [3000, 1024]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+        lambda p: p, ["gemm.rows", "gemm.rows_combine"]),
+    "rows, batched": (
+        ([4, 3, 512], [4, 512, 1024]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.rows", "gemm.rows_combine"]),
+    "rows, one chunk": (
+        ([2, 64], [64, 4096]), lambda a, b: porch.matmul(a, b) * 0.5, lambda a, b: a @ b, lambda p: p * 0.5,
+        ["gemm.rows"]),
+    "matrix times vector": (
+        ([4096, 4096], [4096, 1]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.cols"]),
+    "three columns, odd K, bias": (
+        ([5000, 701], [701, 3]), lambda a, b: porch.matmul(a, b) + 2.0, lambda a, b: a @ b, lambda p: p + 2.0,
+        ["gemm.cols"]),
+    "columns, transposed A": (
+        ([1024, 2000], [1024, 2]), lambda a, b: porch.matmul(porch.transpose(a), b), lambda a, b: a.T @ b,
+        lambda p: p, ["gemm.cols"]),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_short_sided_products_take_the_skinny_kernels(name):
+    shapes, build, _, _, kinds = CASES[name]
+    expr = build(*[placeholder(s) for s in shapes])
+    assert _kinds(expr) == kinds
+    porch.plan(expr, compile=True)
+
+
+def test_wide_products_keep_mfma():
+    assert _kinds(porch.matmul(placeholder([64, 1024]), placeholder([1024, 1024]))) == ["gemm.mfma"]
+    assert _kinds(porch.matmul(placeholder([8, 64]), placeholder([64, 64]))) == ["gemm.scalar"]
+
+
+@needs_clang
+@pytest.mark.parametrize("name", ["rows, ragged columns", "rows, transposed B", "rows, batched",
+                                  "rows, one chunk", "three columns, odd K, bias", "columns, transposed A"])
+def test_emulated_integer_products_are_exact(name):
+    shapes, build, prod, epi, _ = CASES[name]
+    xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
+    expr = build(*[placeholder(s, x) for s, x in zip(shapes, xs)])
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=600))
+    got = emu.evaluate(expr, xs, timeout=600)
+    want = epi(prod(*[x.astype(np.float64) for x in xs])).astype(np.float32)
+    assert np.array_equal(got.reshape(want.shape), want)
+
+
+# -- GPU -----------------------------------------------------------------------
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_integer_products_bit_exact(gpu, name):
+    shapes, build, _, _, kinds = CASES[name]
+    xs = [_ints(s, i + 7) for i, s in enumerate(shapes)]
+    expr = build(*[gpu.tensor(s, x) for s, x in zip(shapes, xs)])
+    assert _kinds(expr) == kinds
+    out = gpu.materialize(expr).cpu().reshape(expr.shape())
+    ref = host.evaluate(expr)
+    assert np.array_equal(out, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_real_products_within_the_accumulation_bound(gpu, name):
+    shapes, build, prod, epi, _ = CASES[name]
+    xs = [_reals(s, i + 11) for i, s in enumerate(shapes)]
+    expr = build(*[gpu.tensor(s, x) for s, x in zip(shapes, xs)])
+    out = gpu.materialize(expr).cpu().reshape(expr.shape()).astype(np.float64)
+    x64 = [x.astype(np.float64) for x in xs]
+    product = prod(*x64)
+    k = x64[0].shape[-1] if "transposed A" not in name else x64[0].shape[0]
+    bound = (k - 1) * 2.0 ** -24 * prod(*[np.abs(x) for x in x64])
+    want = epi(product)
+    # the product within its bound, then one rounding of the epilogue
+    assert np.all(np.abs(out - want) <= bound + 2.0 ** -24 * np.abs(want) + 1e-37), \
+        np.max(np.abs(out - want) - bound)
