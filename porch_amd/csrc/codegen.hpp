@@ -26,7 +26,9 @@
 //   gemm             LDS-tiled v_mfma_f32_32x32x2f32 with the elementwise
 //                    epilogue applied to the accumulators before the store;
 //   gemm.rows,       products with a few rows (or columns), streaming the
-//   gemm.cols        long operand once.
+//   gemm.cols        long operand once;
+//   gemm.combine     the sum of K-chunk partial products (gemm.rows, or the
+//                    MFMA kernel split over K), with the epilogue.
 
 #include "lower.hpp"
 
@@ -158,18 +160,28 @@ namespace porch::cg {
         int n_slots = 0;
         index_width width;
         int compute_units = 256;
+        // > 1: the MFMA kernel computes K in this many chunks, each
+        // workgroup one chunk of one tile, writing partial products to its
+        // `out` as [chunks, batch, m, n] for emit_gemm_combine.
+        int64_t k_chunks = 1;
     };
 
     kernel_code emit_gemm(const gemm_request& request);
+    // How many chunks of K the MFMA kernel should split a product into (1:
+    // none): when its tiles cannot fill the machine and K is long.
+    int64_t gemm_k_chunks(const gemm_request& request);
+    // Sums `chunks` partial products [chunks, batch, m, n] from slot
+    // `partial_slot` per output and applies the epilogue.
+    kernel_code emit_gemm_combine(const gemm_request& request, int64_t chunks, int partial_slot);
 
     // Products with one short side (emit_gemm_skinny.cpp).  A few rows
     // (m <= 32, n >= 256): `gemm_few_rows_partials` floats of partial
-    // products (0: one K chunk, the first kernel writes the result), then
-    // their sum per output with the epilogue, reading slot `partial_slot`.
+    // products over `gemm_few_rows_chunks` chunks of K (0 partials: one
+    // chunk, the first kernel writes the result), then emit_gemm_combine.
     bool gemm_few_rows(const gemm_request& request);
     int64_t gemm_few_rows_partials(const gemm_request& request);
+    int64_t gemm_few_rows_chunks(const gemm_request& request);
     kernel_code emit_gemm_few_rows(const gemm_request& request);
-    kernel_code emit_gemm_few_rows_combine(const gemm_request& request, int partial_slot);
     // A few columns (n <= 4, m >= 64): one wave per output row.
     bool gemm_few_cols(const gemm_request& request);
     kernel_code emit_gemm_few_cols(const gemm_request& request);

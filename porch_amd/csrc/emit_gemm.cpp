@@ -27,11 +27,12 @@ namespace porch::cg {
     void epilogue_emitter(emitter& em, const gemm_request& r, const std::vector<std::string>& names,
                           const std::string& acc) {
         const kexpr& k = *r.expr;
-        em.load = [&k, &names](int id) {
+        // the names by value: callers may pass a temporary
+        em.load = [&k, names](int id) {
             const knode& n = k.at(id);
             return std::vector<std::string>{"a" + std::to_string(n.slot) + "[" + index_text(n.index, names) + "]"};
         };
-        em.condition = [&names](const kcond& c) { return index_text(c.lhs, names) + " < " + std::to_string(c.bound); };
+        em.condition = [names](const kcond& c) { return index_text(c.lhs, names) + " < " + std::to_string(c.bound); };
         em.row_value = [acc](int) { return acc; };
     }
 
@@ -256,8 +257,15 @@ namespace porch::cg {
             // compute unit.
             const int64_t resident = static_cast<int64_t>(std::max(r.compute_units, 1)) * 2;
             const int64_t out_elems = r.batch * r.m * r.n;
-            const bool persistent = interleaves(BM) && ((r.m + BM - 1) / BM) * tiles_n * r.batch > resident &&
-                                    steps <= 4 && out_elems < (int64_t{1} << 29);
+            const bool persistent = r.k_chunks == 1 && interleaves(BM) &&
+                                    ((r.m + BM - 1) / BM) * tiles_n * r.batch > resident && steps <= 4 &&
+                                    out_elems < (int64_t{1} << 29);
+            // Split over K (k_chunks > 1): workgroup w computes chunk
+            // w % k_chunks of tile w / k_chunks, steps_c K-steps from kbase,
+            // and stores its accumulators unchanged as partial products.
+            const int64_t kc_n = r.k_chunks;
+            if (kc_n > 1 && steps % kc_n != 0) throw std::logic_error("emit_gemm: K chunks must divide the K-steps");
+            const int64_t steps_c = steps / kc_n;
             // Otherwise 256-row tiles (each wave 128 x 64: 4 x 2 MFMA blocks)
             // halve the LDS reads per MFMA and the B re-reads; used while
             // they still give every compute unit a tile (measured 2.7%
@@ -268,7 +276,7 @@ namespace porch::cg {
             const int ib = bm / 64; // 32-row MFMA blocks per wave
             const int64_t tiles_m = (r.m + bm - 1) / bm;
             const int64_t tiles = tiles_m * tiles_n;
-            const int64_t total = tiles * r.batch; // workgroups: (batch entry, tile) pairs
+            const int64_t total = tiles * r.batch; // (batch entry, tile) pairs
             const std::string IB = std::to_string(ib);
             const std::string HALF = std::to_string(bm / 2);
             const int vmem = bm / 64 + BN / 64;
@@ -280,7 +288,7 @@ namespace porch::cg {
             kc.name = "porch_gemm";
             kc.n_slots = r.n_slots;
             kc.block = 256;
-            kc.grid_x = static_cast<unsigned>(persistent ? resident : total);
+            kc.grid_x = static_cast<unsigned>(persistent ? resident : total * kc_n);
             const char* T = r.width.type();
             std::string& s = kc.source;
             s = kernel_prologue(r.n_slots, T);
@@ -332,7 +340,14 @@ namespace porch::cg {
                 d += ind + "const float* __restrict__ B" + sx + " = " + base(r.b) + ";\n";
                 return d;
             };
-            if (!persistent) s += decode("blockIdx.x", "", "    ");
+            if (!persistent && kc_n == 1) s += decode("blockIdx.x", "", "    ");
+            if (kc_n > 1) {
+                s += "    const idx_t ks = (idx_t)blockIdx.x % " + std::to_string(kc_n) + ";\n";
+                s += "    const idx_t kbase = ks * " + std::to_string(steps_c * BK) + ";\n";
+                s += "    const idx_t wt = (idx_t)blockIdx.x / " + std::to_string(kc_n) + ";\n";
+                s += decode("wt", "", "    ");
+            }
+            const std::string kb = kc_n > 1 ? "kbase + " : "";
             // Even step counts of a persistent kernel load two K-slices
             // ahead, through two register sets: a slice's LDS store then
             // waits only for loads issued a step earlier, behind the output
@@ -365,7 +380,8 @@ namespace porch::cg {
             // prologue: the first K-slice of the (first) tile
             s += "    {\n";
             if (persistent) s += decode("blockIdx.x", "", "        ");
-            s += "        const idx_t k0 = 0;\n        const int nb = 0;\n";
+            s += "        const idx_t k0 = " + (kc_n > 1 ? std::string("kbase") : std::string("0")) +
+                 ";\n        const int nb = 0;\n";
             if (ahead2) {
                 s += in_set(load_a + load_b + store_a + store_b, 0);
                 // and its second, held in registers
@@ -432,6 +448,9 @@ namespace porch::cg {
                          "), orsrc, off, 0, 0);\n";
                     e += "    }\n";
                 }
+                else if (kc_n > 1) {
+                    e += "            out[ks * " + std::to_string(out_elems) + " + " + at + "] = acc_v;\n        }\n    }\n";
+                }
                 else {
                     e += "            out[" + at + "] = " + v + ";\n        }\n    }\n";
                 }
@@ -478,13 +497,13 @@ namespace porch::cg {
                 head += "        const int cb = t & 1;\n";
                 head += "        const int nb = cb ^ 1;\n";
                 if (interleave) {
-                    head += "        const idx_t k0 = (idx_t)(t + 1 < " + std::to_string(steps) + " ? t + 1 : t) * " +
-                            std::to_string(BK) + ";\n";
+                    head += "        const idx_t k0 = " + kb + "(idx_t)(t + 1 < " + std::to_string(steps_c) +
+                            " ? t + 1 : t) * " + std::to_string(BK) + ";\n";
                     head += "        {\n" + load_a + load_b + "        }\n";
                 }
                 else {
-                    head += "        const idx_t k0 = (idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
-                    head += "        const bool more = t + 1 < " + std::to_string(steps) + ";\n";
+                    head += "        const idx_t k0 = " + kb + "(idx_t)(t + 1) * " + std::to_string(BK) + ";\n";
+                    head += "        const bool more = t + 1 < " + std::to_string(steps_c) + ";\n";
                     head += "        if (more) {\n" + load_a + load_b + "        }\n";
                 }
             }
@@ -598,7 +617,7 @@ namespace porch::cg {
                 s += epilogue("accP", "m0p", "n0p", "qbp", 0, 2 * ib, true);
             }
             else {
-                s += "    for (int t = 0; t < " + std::to_string(steps) + "; ++t) {\n" + head + step + "    }\n";
+                s += "    for (int t = 0; t < " + std::to_string(steps_c) + "; ++t) {\n" + head + step + "    }\n";
                 s += epilogue("acc", "m0", "n0", "qb", 0, 2 * ib, false);
             }
             s += "}\n";
@@ -607,12 +626,39 @@ namespace porch::cg {
 
     } // namespace
 
-    kernel_code emit_gemm(const gemm_request& r) {
+    namespace {
         // Small products keep the reference's sequential K loop (their
-        // launch is latency-bound anyway); large ones use MFMA.
-        if (r.batch * r.m * r.n * r.k < (int64_t{1} << 18) || r.m < 32 || r.n < 32)
-            return emit_gemm_scalar(r);
-        return emit_gemm_mfma(r);
+        // launch is latency-bound anyway); large ones use MFMA, whatever
+        // their shape: a tile that covers only a few rows or columns still
+        // beats one thread per output running down a long K (the products
+        // with one short side that a skinny kernel serves better do not
+        // get here).
+        bool uses_mfma(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
+    } // namespace
+
+    kernel_code emit_gemm(const gemm_request& r) {
+        return uses_mfma(r) ? emit_gemm_mfma(r) : emit_gemm_scalar(r);
+    }
+
+    int64_t gemm_k_chunks(const gemm_request& r) {
+        if (!uses_mfma(r)) return 1;
+        // 128 x 128 tiles (the tile size of a product too small for 256-row
+        // tiles); split K when they leave over half the compute units idle
+        // and K is long (1024 or more: a shorter loop finishes within the
+        // time of the extra combine launch), into the fewest chunks
+        // (dividing the K-steps, each at least 8 of them) that give two
+        // workgroups per compute unit.
+        const int64_t cus = std::max(r.compute_units, 8);
+        const int64_t tiles = ((r.m + BM - 1) / BM) * ((r.n + BN - 1) / BN) * r.batch;
+        const int64_t steps = (r.k + BK - 1) / BK;
+        if (2 * tiles >= cus || steps < 64) return 1;
+        int64_t best = 1;
+        for (int64_t d = 2; d * 8 <= steps; ++d) {
+            if (steps % d != 0) continue;
+            best = d;
+            if (tiles * d >= 2 * cus) break;
+        }
+        return best;
     }
 
 } // namespace porch::cg

@@ -8,8 +8,8 @@
 //                 of B and a chunk of K, each lane holding m x 4
 //                 accumulators for its four columns, A's values read as
 //                 wave-uniform scalars; the chunks' partial products go to a
-//                 temporary [chunks, batch, m, n] that gemm.rows_combine
-//                 sums per output, applying the epilogue.  With one chunk
+//                 temporary [chunks, batch, m, n] that gemm.combine sums
+//                 per output, applying the epilogue.  With one chunk
 //                 the first kernel applies the epilogue itself.
 //   gemm.cols     few columns (n <= 4, m >= 64): one wave per output row,
 //                 lanes along K reading A with 128-bit loads, n
@@ -26,7 +26,10 @@
 namespace porch::cg {
     namespace {
 
-        constexpr int64_t max_rows = 32;
+        // Up to 16 rows: from 24 on, the MFMA kernel split over K is faster
+        // (measured at K, N in {1024, 4096}: 43-44 against 47-57 us at 24
+        // and 32 rows of 4096 x 4096, 17-20 against 28-40 us at 1024).
+        constexpr int64_t max_rows = 16;
         constexpr int64_t max_cols = 4;
         constexpr int64_t block_cols = 256; // columns per wave in gemm.rows
 
@@ -53,10 +56,11 @@ namespace porch::cg {
             if (r.m > max_rows || r.n < block_cols || !big_enough(r)) return sh;
             sh.blocks = (r.n + block_cols - 1) / block_cols;
             // About eight waves per compute unit in all, and a chunk long
-            // enough that the partials (m x 256 floats per wave) stay small
-            // beside the B rows it reads (chunk x 256 floats).
+            // enough that the partials (m x 256 floats per wave) stay below
+            // the B rows it reads (chunk x 256 floats).  (A chunk of at
+            // least 8 m rows, fewer waves, was 16-30% slower at 16 rows.)
             const int64_t target = std::max<int64_t>(1, 8 * std::max(r.compute_units, 8) / (r.batch * sh.blocks));
-            int64_t chunk = std::max<int64_t>(std::max<int64_t>(64, 8 * r.m), (r.k + target - 1) / target);
+            int64_t chunk = std::max<int64_t>(std::max<int64_t>(64, 2 * r.m), (r.k + target - 1) / target);
             chunk = std::min(chunk, r.k);
             sh.chunks = (r.k + chunk - 1) / chunk;
             sh.chunk = chunk;
@@ -162,15 +166,16 @@ namespace porch::cg {
         return kc;
     }
 
-    kernel_code emit_gemm_few_rows_combine(const gemm_request& r, int partial_slot) {
-        const rows_shape sh = rows_plan(r);
-        if (sh.chunks < 2) throw std::logic_error("emit_gemm_few_rows_combine: one chunk");
+    int64_t gemm_few_rows_chunks(const gemm_request& r) { return rows_plan(r).chunks; }
+
+    kernel_code emit_gemm_combine(const gemm_request& r, int64_t chunks, int partial_slot) {
+        if (chunks < 2) throw std::logic_error("emit_gemm_combine: one chunk");
         const char* T = r.width.type();
         const int64_t outputs = r.batch * r.m * r.n;
         const std::string O = std::to_string(outputs);
 
         kernel_code kc;
-        kc.kind = "gemm.rows_combine";
+        kc.kind = "gemm.combine";
         kc.name = "porch_gemm";
         kc.n_slots = r.n_slots;
         kc.block = 256;
@@ -184,7 +189,7 @@ namespace porch::cg {
         s += "    const float* __restrict__ xp = a" + std::to_string(partial_slot) + " + o;\n";
         s += "    float acc = 0.0f;\n";
         s += "    #pragma unroll 8\n";
-        s += "    for (int c = 0; c < " + std::to_string(sh.chunks) + "; ++c) acc += xp[(idx_t)c * " + O + "];\n";
+        s += "    for (int c = 0; c < " + std::to_string(chunks) + "; ++c) acc += xp[(idx_t)c * " + O + "];\n";
         if (r.batched) s += "    const idx_t qb = o / " + std::to_string(r.m * r.n) + ";\n";
         s += "    const idx_t q0 = (o / " + std::to_string(r.n) + ") % " + std::to_string(r.m) + ";\n";
         s += "    const idx_t q1 = o % " + std::to_string(r.n) + ";\n";

@@ -264,11 +264,23 @@ namespace porch::plan {
                     add_step(cg::emit_gemm_few_rows(r), {arg_ref::kind::temp, t});
                     cg::gemm_request c = r;
                     c.n_slots = n_slots();
-                    add_step(cg::emit_gemm_few_rows_combine(c, g.n_inputs + t), dest);
+                    add_step(cg::emit_gemm_combine(c, cg::gemm_few_rows_chunks(r), g.n_inputs + t), dest);
                     return true;
                 }
                 if (cg::gemm_few_cols(r)) {
                     add_step(cg::emit_gemm_few_cols(r), dest);
+                    return true;
+                }
+                r.k_chunks = cg::gemm_k_chunks(r);
+                if (r.k_chunks > 1) {
+                    // Too few tiles for the machine: chunks of K in
+                    // parallel, their partial products summed after.
+                    const int t = static_cast<int>(plan.temp_elems.size());
+                    plan.temp_elems.push_back(r.k_chunks * r.batch * r.m * r.n);
+                    add_step(cg::emit_gemm(r), {arg_ref::kind::temp, t});
+                    cg::gemm_request c = r;
+                    c.n_slots = n_slots();
+                    add_step(cg::emit_gemm_combine(c, r.k_chunks, g.n_inputs + t), dest);
                     return true;
                 }
                 add_step(cg::emit_gemm(r), dest);

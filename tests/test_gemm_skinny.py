@@ -1,6 +1,7 @@
-"""Matmuls with one short side (kernel kinds gemm.rows, gemm.rows_combine,
+"""Matmuls with one short side (kernel kinds gemm.rows, gemm.combine,
 gemm.cols): a few rows (a vector times a matrix, a small batch of rows) or a
-few columns (a matrix times a vector).
+few columns (a matrix times a vector); and matmuls whose tiles leave most of
+the machine idle over a long K (gemm.mfma split over K, then gemm.combine).
 
 Bars: bit for bit on integer data (every partial sum exact, whatever the
 order); on real data within the accumulation bound (K - 1) u sum |a b| per
@@ -39,19 +40,19 @@ def _reals(shape, seed):
 CASES = {
     "vector times matrix": (
         ([1, 4096], [4096, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
-        ["gemm.rows", "gemm.rows_combine"]),
+        ["gemm.rows", "gemm.combine"]),
     "eight rows, relu epilogue": (
         ([8, 2048], [2048, 1024]), lambda a, b: porch.relu(porch.matmul(a, b) - 1.0), lambda a, b: a @ b,
-        lambda p: np.maximum(p - 1.0, 0.0), ["gemm.rows", "gemm.rows_combine"]),
+        lambda p: np.maximum(p - 1.0, 0.0), ["gemm.rows", "gemm.combine"]),
     "rows, ragged columns": (
         ([3, 777], [777, 1003]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
-        ["gemm.rows", "gemm.rows_combine"]),
+        ["gemm.rows", "gemm.combine"]),
     "rows, transposed B": (
         ([2, 1024], [3000, 1024]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
-        lambda p: p, ["gemm.rows", "gemm.rows_combine"]),
+        lambda p: p, ["gemm.rows", "gemm.combine"]),
     "rows, batched": (
         ([4, 3, 512], [4, 512, 1024]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
-        ["gemm.rows", "gemm.rows_combine"]),
+        ["gemm.rows", "gemm.combine"]),
     "rows, one chunk": (
         ([2, 64], [64, 4096]), lambda a, b: porch.matmul(a, b) * 0.5, lambda a, b: a @ b, lambda p: p * 0.5,
         ["gemm.rows"]),
@@ -64,6 +65,27 @@ CASES = {
     "columns, transposed A": (
         ([1024, 2000], [1024, 2]), lambda a, b: porch.matmul(porch.transpose(a), b), lambda a, b: a.T @ b,
         lambda p: p, ["gemm.cols"]),
+    "split K": (
+        ([64, 4096], [4096, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.mfma", "gemm.combine"]),
+    "split K, ragged K, relu epilogue": (
+        ([40, 1030], [1030, 200]), lambda a, b: porch.relu(porch.matmul(a, b) + 1.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p + 1.0, 0.0), ["gemm.mfma", "gemm.combine"]),
+    "split K, transposed A": (
+        ([2048, 96], [2048, 160]), lambda a, b: porch.matmul(porch.transpose(a), b), lambda a, b: a.T @ b,
+        lambda p: p, ["gemm.mfma", "gemm.combine"]),
+    "split K, five rows": (
+        ([5, 1030], [1030, 200]), lambda a, b: porch.matmul(a, b) * 2.0, lambda a, b: a @ b, lambda p: p * 2.0,
+        ["gemm.mfma", "gemm.combine"]),
+    "split K, eight columns": (
+        ([600, 1024], [1024, 8]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.mfma", "gemm.combine"]),
+    "vector times a narrow matrix": (
+        ([1, 4096], [4096, 100]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.mfma", "gemm.combine"]),
+    "split K, batched": (
+        ([2, 100, 1024], [2, 1024, 300]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b,
+        lambda p: p, ["gemm.mfma", "gemm.combine"]),
 }
 
 
@@ -76,13 +98,63 @@ def test_short_sided_products_take_the_skinny_kernels(name):
 
 
 def test_wide_products_keep_mfma():
-    assert _kinds(porch.matmul(placeholder([64, 1024]), placeholder([1024, 1024]))) == ["gemm.mfma"]
+    assert _kinds(porch.matmul(placeholder([64, 512]), placeholder([512, 1024]))) == ["gemm.mfma"]  # short K
+    assert _kinds(porch.matmul(placeholder([1024, 4096]), placeholder([4096, 2048]))) == ["gemm.mfma"]  # many tiles
     assert _kinds(porch.matmul(placeholder([8, 64]), placeholder([64, 64]))) == ["gemm.scalar"]
+
+
+@pytest.mark.parametrize("shape, chunks", [
+    ((64, 4096, 4096), 16),  # 32 tiles: 16 chunks of 256 give 512 workgroups
+    ((40, 1030, 200), 5),    # 65 K-steps, 2 tiles: the largest divisor with 8 steps a chunk
+    ((512, 1024, 512), 8),   # 16 tiles: 64 K-steps in 8 chunks
+])
+def test_split_k_chunks(shape, chunks):
+    m, k, n = shape
+    plan = porch.plan(porch.matmul(placeholder([m, k]), placeholder([k, n])))
+    assert [x["kind"] for x in plan["kernels"]] == ["gemm.mfma", "gemm.combine"]
+    tiles = -(-m // 128) * -(-n // 128)
+    assert plan["kernels"][0]["grid"][0] == tiles * chunks
+    assert plan["temps"] == [chunks * m * n]
+
+
+# Epilogues that read another input (a bias row): the kernel that applies
+# the epilogue (the combine where there is one) loads it at the output's
+# coordinates.
+BIAS_SHAPES = {
+    (8, 2048, 1024): ["gemm.rows", "gemm.combine"],
+    (40, 1030, 200): ["gemm.mfma", "gemm.combine"],
+    (3000, 300, 2): ["gemm.cols"],
+}
+
+
+def _bias_graph(a, b, bias, m, n):
+    return porch.relu(porch.matmul(a, b) + porch.broadcast_to(bias, [m, n]))
+
+
+@pytest.mark.parametrize("shape", sorted(BIAS_SHAPES))
+def test_epilogues_reading_an_input(shape):
+    m, k, n = shape
+    expr = _bias_graph(placeholder([m, k]), placeholder([k, n]), placeholder([1, n]), m, n)
+    assert _kinds(expr) == BIAS_SHAPES[shape]
+    porch.plan(expr, compile=True)
+
+
+@needs_clang
+def test_emulated_split_k_with_a_bias_is_exact():
+    m, k, n = 40, 1030, 200
+    xs = [_ints([m, k], 1), _ints([k, n], 2), _ints([1, n], 3)]
+    expr = _bias_graph(*[placeholder(x.shape, x) for x in xs], m, n)
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=600))
+    got = emu.evaluate(expr, xs, timeout=600)
+    want = np.maximum(xs[0].astype(np.float64) @ xs[1] + xs[2], 0.0).astype(np.float32)
+    assert np.array_equal(got.reshape(want.shape), want)
 
 
 @needs_clang
 @pytest.mark.parametrize("name", ["rows, ragged columns", "rows, transposed B", "rows, batched",
-                                  "rows, one chunk", "three columns, odd K, bias", "columns, transposed A"])
+                                  "rows, one chunk", "three columns, odd K, bias", "columns, transposed A",
+                                  "split K, ragged K, relu epilogue", "split K, transposed A",
+                                  "split K, five rows", "split K, eight columns"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
     xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
@@ -123,3 +195,14 @@ def test_real_products_within_the_accumulation_bound(gpu, name):
     # the product within its bound, then one rounding of the epilogue
     assert np.all(np.abs(out - want) <= bound + 2.0 ** -24 * np.abs(want) + 1e-37), \
         np.max(np.abs(out - want) - bound)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", sorted(BIAS_SHAPES))
+def test_epilogue_reading_an_input_bit_exact(gpu, shape):
+    m, k, n = shape
+    xs = [_ints([m, k], 21), _ints([k, n], 22), _ints([1, n], 23)]
+    expr = _bias_graph(*[gpu.tensor(list(x.shape), x) for x in xs], m, n)
+    assert _kinds(expr) == BIAS_SHAPES[shape]
+    out = gpu.materialize(expr).cpu().reshape(m, n)
+    assert np.array_equal(out, host.evaluate(expr).reshape(m, n))

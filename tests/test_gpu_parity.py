@@ -434,7 +434,8 @@ def test_mfma_gemm_edges_and_tails(gpu, m, k, n):
     a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, size=(k, n)).astype(np.float32)
     expr = porch.matmul(porch.tensor([m, k], a), porch.tensor([k, n], b))
-    assert porch.plan(expr)["kernels"][-1]["kind"] == "gemm.mfma"
+    # (1024 x 4096 x 96: eight tiles, split over K, then a combine)
+    assert "gemm.mfma" in [x["kind"] for x in porch.plan(expr)["kernels"]]
     out = porch.materialize(expr).cpu().reshape(m, n)
     ref = a.astype(np.float64) @ b.astype(np.float64)
     assert (np.abs(out - ref) <= 1e-5 * gemm_bound(a.astype(np.float64), b.astype(np.float64)) + 1e-30).all()
