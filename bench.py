@@ -387,6 +387,24 @@ extern "C" __global__ void __launch_bounds__(256) porch_control_copy(
     const porch_v4f x = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a0) + g);
     reinterpret_cast<float4*>(out)[g] = make_float4(x.x, x.y, x.z, x.w);
 }
+// The view chain's bytes in coalesced order: `count` lanes, each reading 32
+// float4 of a0 (8 rounds of 4, strided by the lane count: all of x
+// [4096,4096] at count = 131072) and writing two floats of each (out
+// [4096,2048]), with the workload's + 1.
+extern "C" __global__ void __launch_bounds__(256) porch_control_half(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {
+    typedef float porch_v2f __attribute__((ext_vector_type(2)));
+    const unsigned long long g = blockIdx.x * 256ull + threadIdx.x;
+    if (g >= count) return;
+    const porch_v4f* x = reinterpret_cast<const porch_v4f*>(a0);
+    porch_v2f* y = reinterpret_cast<porch_v2f*>(out);
+    for (int round = 0; round < 8; ++round) {
+        porch_v4f v[4];
+        for (int r = 0; r < 4; ++r) v[r] = __builtin_nontemporal_load(x + g + (round * 4 + r) * count);
+        for (int r = 0; r < 4; ++r) y[g + (round * 4 + r) * count] = (porch_v2f){v[r].y + 1.0f, v[r].w + 1.0f};
+    }
+}
 // A plain copy at a large size: `count` lanes, each copying four float4 of
 // a0 to out, strided by the lane count (non-temporal loads and stores).
 extern "C" __global__ void __launch_bounds__(256) porch_control_stream(
@@ -404,8 +422,9 @@ extern "C" __global__ void __launch_bounds__(256) porch_control_stream(
 
 def controls(launches: int) -> int:
     """Each control kernel, then the elementwise workload's own kernel,
-    `launches` times each over rotated (cache-cold) buffers; then a plain
-    copy of the vocabulary softmax's bytes and that workload itself,
+    `launches` times each over rotated (cache-cold) buffers; then the view
+    chain's bytes moved in coalesced order and that workload itself; then
+    a plain copy of the vocabulary softmax's bytes and that workload,
     `launches` times each; timed by the profiler this runs under
     (rocprofv3 --kernel-trace --stats)."""
     import porch_amd as porch
@@ -435,6 +454,27 @@ def controls(launches: int) -> int:
     porch.synchronize()
     log(f"controls: elementwise workload x {launches}")
     del sets, outs
+
+    # The view chain beside a coalesced kernel that moves the same bytes
+    # (all of x read, half as many written), both over rotated buffers.
+    vc_shape = config_shapes("view_chain")[0]
+    (vc_values,) = config_inputs("view_chain")
+    copies = ROTATION["view_chain"]
+    xs = [porch.tensor(vc_shape, vc_values) for _ in range(copies)]
+    halves = [porch.zeros([vc_shape[0] * vc_shape[1] // 2]).realize() for _ in range(copies)]
+    lanes = vc_shape[0] * vc_shape[1] // 128  # 32 float4 per lane
+    for i in range(launches):
+        h = xs[i % copies].device_data().handle
+        ins = (ctypes.c_void_p * 2)(h, h)
+        _lib.check(_lib.lib.porch_launch_fused_elementwise(
+            data, size, b"porch_control_half", ins, 2, halves[i % copies].device_data().handle, lanes))
+    porch.synchronize()
+    log(f"controls: porch_control_half x {launches}")
+    for i in range(launches):
+        porch.materialize(config_graph("view_chain", [xs[i % copies]]))
+    porch.synchronize()
+    log(f"controls: view_chain workload x {launches}")
+    del xs, halves
 
     # The vocabulary softmax beside a plain copy of the same bytes (512 MiB
     # each way: twice the Infinity Cache, so no launch finds its data there).
