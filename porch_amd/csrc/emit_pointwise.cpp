@@ -254,7 +254,8 @@ namespace porch::cg {
         // tiled: LDS transpose for leaves strided along the output's
         // contiguous dimension
         // ---------------------------------------------------------------
-        constexpr int tile = 64;
+        // Tiles are 64 (q) x 64 or 128 (p) outputs; see emit_tiled.
+        constexpr int tile_q = 64;
 
         struct tiling {
             int p = -1;                 // coordinate the staged leaves run along
@@ -473,8 +474,7 @@ namespace porch::cg {
             const size_t p = static_cast<size_t>(t.p);
             const int64_t extent_p = r.shape[p];
             const int64_t extent_q = r.shape[q];
-            const int64_t ntq = (extent_q + tile - 1) / tile;
-            const int64_t ntp = (extent_p + tile - 1) / tile;
+            const size_t n_stage = t.staged.size();
             std::vector<int64_t> other_shape;
             std::vector<size_t> other_dims;
             for (size_t d = 0; d < rank; ++d) {
@@ -483,7 +483,6 @@ namespace porch::cg {
                 other_dims.push_back(d);
             }
             const int64_t others = ir::numel(other_shape);
-            const size_t n_stage = t.staged.size();
             const std::vector<char> in_stage = staged_mask(k, t);
             std::vector<int> tiled_roots(t.staged.begin(), t.staged.end());
             tiled_roots.push_back(r.root);
@@ -510,6 +509,23 @@ namespace porch::cg {
                     break;
                 }
             }
+            // 128 outputs along p where phase 1 reads one unit-stride leaf
+            // (128-bit loads) into one stage: it then reads 512 B of each
+            // source row per tile instead of 256 B, and the stage (33 KB)
+            // still leaves room for four workgroups per compute unit.
+            // Measured (trace means): x^T over [4096, 4096] 27.0 -> 23.2 us,
+            // x^T + y 40.4 -> 36.8, x^T * y + z 54.7 -> 51.9.  Not with two
+            // transposed leaves (x^T + y^T: 38.4 -> 41.5) nor stride-2 reads,
+            // which already cover 512 B (the view chain: 18.0 -> 22.4).
+            int phase1_leaves = 0;
+            for (size_t id = 0; id < k.nodes.size(); ++id) {
+                const knode& n = k.at(static_cast<int>(id));
+                if (in_stage[id] && n.op == kop::load && (!n.index.is_affine || n.index.w[p] != 0)) ++phase1_leaves;
+            }
+            const int64_t tile_p = (n_stage == 1 && V == 4 && phase1_leaves == 1 && extent_p >= 128) ? 128 : 64;
+            const int64_t ntq = (extent_q + tile_q - 1) / tile_q;
+            const int64_t ntp = (extent_p + tile_p - 1) / tile_p;
+
             // Phase 2 width: outputs per lane along q (128-bit stores).
             int64_t W = (extent_q % 4 == 0) ? 4 : 1;
             {
@@ -566,14 +582,13 @@ namespace porch::cg {
             const std::vector<std::string> names = coordinate_names(rank);
             const std::string qs = "q" + std::to_string(q);
             const std::string ps = "q" + std::to_string(p);
-            const std::string TILE = std::to_string(tile);
 
             std::string& s = kc.source;
             s = kernel_prologue(r.n_slots, T);
             s += "extern \"C\" __global__ void __launch_bounds__(256) porch_tiled(" +
                  kernel_params(r.n_slots) + ") {\n";
-            s += "    __shared__ float stage[" + std::to_string(n_stage) + "][" + TILE + "][" +
-                 std::to_string(tile + 1) + "];\n";
+            s += "    __shared__ float stage[" + std::to_string(n_stage) + "][" + std::to_string(tile_p) + "][" +
+                 std::to_string(tile_q + 1) + "];\n";
             // Consecutive workgroups walk along p: neighbouring tiles read
             // neighbouring segments of the same source rows.
             if (persistent)
@@ -598,8 +613,8 @@ namespace porch::cg {
                 }
                 if (other_dims.empty()) s += "    (void)rest;\n";
             }
-            s += "    const idx_t pbase = tp * " + TILE + ";\n";
-            s += "    const idx_t qbase = tq * " + TILE + ";\n";
+            s += "    const idx_t pbase = tp * " + std::to_string(tile_p) + ";\n";
+            s += "    const idx_t qbase = tq * " + std::to_string(tile_q) + ";\n";
             s += "    const int tid = threadIdx.x;\n";
 
             // Per-tile decision of the hoisted selects: 1 = first branch on
@@ -614,14 +629,14 @@ namespace porch::cg {
                     std::string a, b;
                     if (d == p) {
                         a = "pbase";
-                        b = "(pbase + " + std::to_string(tile - 1) + " < " + std::to_string(extent_p) +
-                            " ? pbase + " + std::to_string(tile - 1) + " : (idx_t)" +
+                        b = "(pbase + " + std::to_string(tile_p - 1) + " < " + std::to_string(extent_p) +
+                            " ? pbase + " + std::to_string(tile_p - 1) + " : (idx_t)" +
                             std::to_string(extent_p - 1) + ")";
                     }
                     else if (d == q) {
                         a = "qbase";
-                        b = "(qbase + " + std::to_string(tile - 1) + " < " + std::to_string(extent_q) +
-                            " ? qbase + " + std::to_string(tile - 1) + " : (idx_t)" +
+                        b = "(qbase + " + std::to_string(tile_q - 1) + " < " + std::to_string(extent_q) +
+                            " ? qbase + " + std::to_string(tile_q - 1) + " : (idx_t)" +
                             std::to_string(extent_q - 1) + ")";
                     }
                     else {
@@ -641,13 +656,23 @@ namespace porch::cg {
             auto cond_fn = [&](const kcond& c) {
                 return index_text(c.lhs, names) + " < " + std::to_string(c.bound);
             };
-            const bool full_p = extent_p % tile == 0;
-            const bool full_q = extent_q % tile == 0;
+            const bool full_p = extent_p % tile_p == 0;
+            const bool full_q = extent_q % tile_q == 0;
 
+            // Phase 2 layout: lanes along q, W outputs per lane.
+            const int64_t lanes_q = tile_q / W;
+            const int64_t rows2 = block_threads / lanes_q;
+            const int64_t passes2 = tile_p / rows2;
+            auto phase2_coords = [&](const std::string& ind) {
+                return ind + "const int ql = (tid % " + std::to_string(lanes_q) + ") * " + std::to_string(W) + ";\n" +
+                       ind + "const int pl = tid / " + std::to_string(lanes_q) + " + it * " + std::to_string(rows2) +
+                       ";\n" + ind + "const idx_t " + ps + " = pbase + pl;\n" + ind + "const idx_t " + qs +
+                       " = qbase + ql;\n";
+            };
             // ---- phase 1: lanes along p, V elements per lane ----
-            const int64_t lanes_p = tile / V;
+            const int64_t lanes_p = tile_p / V;
             const int64_t rows1 = block_threads / lanes_p;
-            const int64_t passes1 = tile / rows1;
+            const int64_t passes1 = tile_q / rows1;
             auto phase1_body = [&](const std::vector<int>& modes) {
                 std::string code;
                 code += "        #pragma unroll\n";
@@ -760,16 +785,9 @@ namespace porch::cg {
             s += "    __syncthreads();\n";
 
             // ---- phase 2: lanes along q, W outputs per lane ----
-            const int64_t lanes_q = tile / W;
-            const int64_t rows2 = block_threads / lanes_q;
-            const int64_t passes2 = tile / rows2;
             s += "    #pragma unroll\n";
             s += "    for (int it = 0; it < " + std::to_string(passes2) + "; ++it) {\n";
-            s += "        const int ql = (tid % " + std::to_string(lanes_q) + ") * " + std::to_string(W) + ";\n";
-            s += "        const int pl = tid / " + std::to_string(lanes_q) + " + it * " +
-                 std::to_string(rows2) + ";\n";
-            s += "        const idx_t " + ps + " = pbase + pl;\n";
-            s += "        const idx_t " + qs + " = qbase + ql;\n";
+            s += phase2_coords("        ");
             std::string guard;
             if (!full_p) guard += ps + " < " + std::to_string(extent_p);
             if (!full_q) guard += std::string(guard.empty() ? "" : " && ") + qs + " < " +

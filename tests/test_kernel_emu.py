@@ -83,7 +83,7 @@ def test_benchmark_graphs(name, size):
 
 
 def test_tiled_and_permute_cases():
-    exprs = [build_case(name, placeholder) for name in sorted(TILED_CASES) if name != "transpose_3000x2100"]
+    exprs = [build_case(name, placeholder) for name in sorted(TILED_CASES) if name != "transpose_3000x4100"]
     exprs += [fn(placeholder) for fn, _ in PERMUTE_CASES.values()]
     with ThreadPoolExecutor(6) as pool:
         for results in pool.map(emu.emulate, exprs):

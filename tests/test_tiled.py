@@ -90,8 +90,8 @@ CASES = {
     "interleave_130x66": (interleaved_concat, (130, 66), None, 1, False),
     "transpose_200x136": (transpose_plus, (200, 136), "float4", 0, True),
     "transpose_70x33": (transpose_plus, (70, 33), None, 0, False),
-    # 33 x 47 = 1551 tiles, ragged on both axes: persistent workgroups
-    "transpose_3000x2100": (transpose_plus, (3000, 2100), "float4", 0, True),
+    # 33 x 47 = 1551 tiles of 128 x 64, ragged on both axes: persistent workgroups
+    "transpose_3000x4100": (transpose_plus, (3000, 4100), "float4", 0, True),
     "offset_201x140": (offset_transpose, (201, 140), "float2", 0, True),
     "odd_stride_96x300": (odd_stride_transpose, (96, 300), None, 0, True),
     "batched_3x72x132": (batched_transpose, (3, 72, 132), "float4", 0, True),
@@ -130,13 +130,13 @@ def test_tiled_variant_choice(name):
 
 
 def test_many_tiles_use_persistent_workgroups():
-    many = porch.plan(build_case("transpose_3000x2100", placeholder), compile=True)["kernels"][0]
+    many = porch.plan(build_case("transpose_3000x4100", placeholder), compile=True)["kernels"][0]
     few = porch.plan(build_case("transpose_200x136", placeholder), compile=True)["kernels"][0]
     # at most four workgroups per compute unit walk the 1551 tiles
     assert many["grid"][0] == 4 * 256
     assert "for (idx_t tile_id = blockIdx.x; tile_id < 1551;" in porch.kernel_source(
-        build_case("transpose_3000x2100", placeholder), 0)
-    assert few["grid"][0] == 4 * 3
+        build_case("transpose_3000x4100", placeholder), 0)
+    assert few["grid"][0] == 2 * 4  # 136 x 200 outputs: 2 x 4 tiles of 128 x 64
 
 
 @pytest.mark.gpu
