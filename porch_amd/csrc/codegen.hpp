@@ -124,6 +124,9 @@ namespace porch::cg {
         // > 1: the axis is split into `parts` chunks (grid y); chunk g's
         // fold goes to out[g * outputs + o] for a second pass to combine.
         int64_t parts = 1;
+        // Output groups per workgroup at most (a power of two up to 64);
+        // the rest of its 256 lanes are strands along the axis.
+        int max_cols = 64;
         // Max over the whole axis only: the reduction as the reference
         // states it (`exact_producer` over `exact_shape`, reduced along
         // `exact_axis`; for a second pass, the first pass's), evaluated in

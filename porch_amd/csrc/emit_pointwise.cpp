@@ -90,6 +90,8 @@ namespace porch::cg {
         // ---------------------------------------------------------------
         enum class flat_mode { none, row_vector, contiguous };
 
+        bool uniform_over(const kcond& c, size_t d, int64_t v);
+
         flat_mode choose_flat(const pointwise_request& r) {
             const size_t rank = r.shape.size();
             const int64_t inner = r.shape[rank - 1];
@@ -112,8 +114,11 @@ namespace porch::cg {
                 }
                 if (n.op == kop::select) {
                     contiguous_everywhere = false;
-                    if (!n.cond.lhs.is_affine || n.cond.lhs.w[rank - 1] != 0)
-                        uniform_selects = false;
+                    // the same branch for each group of 4 along the row (a
+                    // concat along the last axis at a multiple of 4): the
+                    // condition is evaluated once, at the group's first
+                    // element
+                    if (!uniform_over(n.cond, rank - 1, 4)) uniform_selects = false;
                 }
             }
             if (!all_affine) return flat_mode::none;

@@ -60,9 +60,9 @@ namespace porch::cg {
         // two up to 64, fewer when there are fewer groups) times
         // 256 / cols strands, each strand folding every strands-th row of
         // the axis.
-        int layout_cols(int64_t groups) {
+        int layout_cols(int64_t groups, int max_cols = 64) {
             int cols = 1;
-            while (cols < 64 && cols < groups) cols *= 2;
+            while (cols < max_cols && cols < groups) cols *= 2;
             return cols;
         }
     } // namespace
@@ -177,7 +177,7 @@ namespace porch::cg {
         const size_t inner = inner_dim(r);
         const int width = lanes_width(r);
         const int64_t groups = outputs / width;
-        const int cols = layout_cols(groups);
+        const int cols = layout_cols(groups, std::clamp(r.max_cols, 1, 64));
         const int strands = 256 / cols;
         kernel_code kc;
         kc.kind = "reduce.column";

@@ -510,6 +510,12 @@ namespace porch::plan {
                 c.is_max = r.is_max;
                 c.n_slots = n_slots();
                 c.width = width;
+                // Enough strands that each folds at most 4 partials: the
+                // pass is a few dependent loads long instead of parts /
+                // strands (a single workgroup over [1024, 256] partials
+                // took 23.5 us).
+                c.max_cols = 64;
+                while (c.max_cols > 1 && (256 / c.max_cols) * 4 < parts) c.max_cols /= 2;
                 if (r.is_max) {
                     c.exact_expr = &k;
                     c.exact_producer = producer;

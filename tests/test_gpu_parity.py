@@ -66,6 +66,25 @@ def test_view_chain_bit_exact(gpu, n):
     assert np.array_equal(out[: n // 2], xm[0::2, 1::2].T + np.float32(1.0))
 
 
+@pytest.mark.parametrize("shapes", [([4096, 4096], [4096, 4096]), ([8, 300, 64], [8, 300, 36]),
+                                    ([37, 6], [37, 10])])
+def test_concat_along_the_last_axis_bit_exact(gpu, shapes):
+    """The flat kernel with one branch per group of 4 (splits at multiples
+    of 4), and the per-element kernel where a group would straddle it."""
+    porch = gpu
+    rng = np.random.default_rng(sum(shapes[1]))
+    xa = rng.standard_normal(int(np.prod(shapes[0]))).astype(np.float32)
+    xb = rng.standard_normal(int(np.prod(shapes[1]))).astype(np.float32)
+    axis = len(shapes[0]) - 1
+    expr = porch.concat(porch.tensor(shapes[0], xa), porch.tensor(shapes[1], xb), axis) - 0.5
+    kind = "pointwise.flat" if shapes[0][-1] % 4 == 0 else "pointwise.scalar"
+    assert [k["kind"] for k in porch.plan(expr)["kernels"]] == [kind]
+    out = porch.materialize(expr).cpu().reshape(-1)
+    assert_bits_equal(out, host.evaluate(expr).reshape(-1))
+    want = np.concatenate([xa.reshape(shapes[0]), xb.reshape(shapes[1])], axis) - np.float32(0.5)
+    assert np.array_equal(out, want.reshape(-1))
+
+
 # -- config 3: softmax, 1e-6 relative ----------------------------------------
 
 @pytest.mark.parametrize("size", [{"rows": 3, "cols": 7}, {"rows": 17, "cols": 256},

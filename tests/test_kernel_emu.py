@@ -82,6 +82,24 @@ def test_benchmark_graphs(name, size):
     in_bounds(config_graph(name, tensors, size))
 
 
+@pytest.mark.parametrize("widths", [(64, 128), (8, 12), (4, 4)])
+def test_concat_along_the_last_axis_values(widths):
+    # the flat kernel with one branch per group of 4: every access in
+    # bounds and the values the oracle gives, on rows whose split falls at
+    # a multiple of 4
+    from oracle import host
+    a, b = widths
+    rng = np.random.default_rng(a * 100 + b)
+    xa = rng.standard_normal(37 * a).astype(np.float32)
+    xb = rng.standard_normal(37 * b).astype(np.float32)
+    expr = porch.concat(placeholder([37, a], xa), placeholder([37, b], xb), 1) * 2.0
+    assert [k["kind"] for k in porch.plan(expr)["kernels"]] == ["pointwise.flat"]
+    in_bounds(expr)
+    got = emu.evaluate(expr, [xa, xb])
+    want = host.evaluate(expr)
+    assert np.array_equal(got.reshape(-1).view(np.uint32), want.reshape(-1).view(np.uint32))
+
+
 def test_tiled_and_permute_cases():
     exprs = [build_case(name, placeholder) for name in sorted(TILED_CASES) if name != "transpose_3000x4100"]
     exprs += [fn(placeholder) for fn, _ in PERMUTE_CASES.values()]

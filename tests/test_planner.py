@@ -47,6 +47,22 @@ def test_flat_kernel_streams_leaves_read_once():
     assert "*reinterpret_cast<const float4*>(a1 + " in source
 
 
+@pytest.mark.parametrize("widths, kind", [
+    ((4096, 4096), "pointwise.flat"),   # the split at a multiple of 4: float4 per lane, one branch per group
+    ((8, 12), "pointwise.flat"),
+    ((6, 10), "pointwise.scalar"),      # a group of 4 would straddle the split
+    ((5, 11), "pointwise.scalar"),
+])
+def test_concat_along_the_last_axis(widths, kind):
+    a, b = widths
+    expr = porch.concat(placeholder([64, a]), placeholder([64, b]), 1) + 1.0
+    assert [k["kind"] for k in porch.plan(expr)["kernels"]] == [kind]
+    if kind == "pointwise.flat":
+        source = porch.kernel_source(expr, 0)
+        assert source.count("__builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(") == 2
+        assert "make_float4(" in source
+
+
 def test_shared_reductions_are_materialised_once():
     """softmax over a non-last axis cannot be one row program; its max is
     still computed once (the reference computes it twice)."""
