@@ -23,6 +23,8 @@
 //                    words, so the row is read once;
 //   reduce.column    one lane per output, sequential fold over a non-last
 //                    axis with lanes along the contiguous output dimension;
+//   reduce.column_softmax  the same layout folding a softmax's max and sum
+//                    (relative to a moving anchor) in one read;
 //   gemm             LDS-tiled v_mfma_f32_32x32x2f32 with the elementwise
 //                    epilogue applied to the accumulators before the store;
 //   gemm.rows,       products with a few rows (or columns), streaming the
@@ -139,6 +141,13 @@ namespace porch::cg {
     };
 
     kernel_code emit_column_reduce(const column_reduce_request& request);
+    // Softmax statistics along a non-last axis in one read of the producer
+    // (emit_reduce.cpp): per output column the max M and S = sum exp(f - M).
+    // partial_slot < 0: the pass over `request.producer` (with
+    // request.parts > 1: [3][parts][outputs] partial triples to `out`, else
+    // M and S as [2][outputs]); partial_slot >= 0: the combination of such
+    // partials (request.shape = {parts, outputs}) into [2][outputs].
+    kernel_code emit_column_softmax(const column_reduce_request& request, int partial_slot);
     // How many chunks to split the reduced axis into (1: no split): about
     // four workgroups per compute unit, chunks of at least 32, and only for
     // reductions of at least 2^20 values over an axis of at least 256.

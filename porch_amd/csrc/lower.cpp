@@ -290,7 +290,7 @@ namespace porch::cg {
             knode load;
             load.op = kop::load;
             load.slot = bound_it->second.slot;
-            load.index = lin;
+            load.index = bound_it->second.offset != 0 ? add_constant(lin, bound_it->second.offset) : lin;
             load.box = box;
             return out.add(load);
         }
@@ -314,6 +314,7 @@ namespace porch::cg {
             load.op = kop::load;
             load.slot = bound_it->second.slot;
             load.index = linearize(coords, n.out);
+            if (bound_it->second.offset != 0) load.index = add_constant(load.index, bound_it->second.offset);
             load.box = box;
             return out.add(load);
         }

@@ -94,6 +94,7 @@ namespace porch::cg {
         enum class kind { slot, row_value };
         kind what = kind::slot;
         int slot = -1; // kernel argument holding the node's contiguous values
+        int64_t offset = 0; // ... from this element of the slot on
         int row = -1;  // row reduction index
     };
 

@@ -30,10 +30,23 @@ namespace porch::plan {
             graph_plan& plan;
             int compute_units;
             std::map<int, int> temp_of;
+            // Element offset of a node's values within its temporary (0
+            // unless several nodes share one: the column softmax's max
+            // and sum).
+            std::map<int, int64_t> offset_of;
             cg::index_width width;
+
+            // The nodes that read each node.
+            std::vector<std::vector<int>> users;
 
             builder(const ir::graph& graph, graph_plan& target, int cus)
                 : g(graph), plan(target), compute_units(cus) {
+                users.resize(g.nodes.size());
+                for (size_t i = 0; i < g.nodes.size(); ++i) {
+                    const ir::node& n = g.nodes[i];
+                    if (n.lhs >= 0) users[static_cast<size_t>(n.lhs)].push_back(static_cast<int>(i));
+                    if (n.rhs >= 0 && n.rhs != n.lhs) users[static_cast<size_t>(n.rhs)].push_back(static_cast<int>(i));
+                }
                 int64_t largest = 0;
                 for (const ir::node& n : g.nodes) {
                     largest = std::max(largest, ir::numel(n.out));
@@ -66,6 +79,8 @@ namespace porch::plan {
                     cg::binding b;
                     b.what = cg::binding::kind::slot;
                     b.slot = g.n_inputs + temp;
+                    const auto off = offset_of.find(node);
+                    if (off != offset_of.end()) b.offset = off->second;
                     low.bound[node] = b;
                 }
             }
@@ -94,6 +109,14 @@ namespace porch::plan {
             arg_ref ensure_temp(int id) {
                 auto found = temp_of.find(id);
                 if (found != temp_of.end()) return {arg_ref::kind::temp, found->second};
+                // The max of a softmax along a non-last axis comes with its
+                // sum, from one read of the values.
+                const int paired_sum = column_softmax_sum(id);
+                if (paired_sum >= 0) {
+                    ensure_temp(paired_sum);
+                    found = temp_of.find(id);
+                    if (found != temp_of.end()) return {arg_ref::kind::temp, found->second};
+                }
                 const int t = static_cast<int>(plan.temp_elems.size());
                 plan.temp_elems.push_back(ir::numel(g.at(id).out));
                 arg_ref dest{arg_ref::kind::temp, t};
@@ -443,9 +466,96 @@ namespace porch::plan {
             }
 
             // ---------------------------------------------------------
+            // softmax along a non-last axis
+            // ---------------------------------------------------------
+            // For a max node M = max(f, axis, keepdim) along a non-last
+            // axis that is read only as exp(f - broadcast(M)), itself summed
+            // along the same axis with keepdim (softmax's form, ops.cpp):
+            // that sum node, else -1.  M then matters only through
+            // exp(f - M), so the order-free max serves (emit_column_softmax).
+            int column_softmax_sum(int max_id) const {
+                const ir::node& m = g.at(max_id);
+                if (m.kind != ir::op::max || !m.keepdim) return -1;
+                const ir::node& f = g.at(m.lhs);
+                if (f.out.size() < 2 || static_cast<size_t>(m.axis) + 1 == f.out.size()) return -1;
+                auto only_user = [&](int x) {
+                    const std::vector<int>& u = users[static_cast<size_t>(x)];
+                    return u.size() == 1 ? u[0] : -1;
+                };
+                const int b = only_user(max_id);
+                if (b < 0 || g.at(b).kind != ir::op::broadcast || g.at(b).out != f.out) return -1;
+                const int d = only_user(b);
+                if (d < 0 || g.at(d).kind != ir::op::subtract || g.at(d).lhs != m.lhs || g.at(d).rhs != b) return -1;
+                const int e = only_user(d);
+                if (e < 0 || g.at(e).kind != ir::op::exp) return -1;
+                for (const int sum : users[static_cast<size_t>(e)]) {
+                    const ir::node& sn = g.at(sum);
+                    if (sn.kind == ir::op::sum && sn.lhs == e && sn.axis == m.axis && sn.keepdim && sum != g.root())
+                        return sum;
+                }
+                return -1;
+            }
+
+            // The sum node of that form into temporary `dest`, with its max
+            // beside it: M at [0, outputs), S at [outputs, 2 outputs).
+            bool try_column_softmax(int id, arg_ref dest) {
+                if (dest.what != arg_ref::kind::temp) return false;
+                const ir::node& n = g.at(id);
+                if (n.kind != ir::op::sum) return false;
+                const ir::node& e = g.at(n.lhs);
+                if (e.kind != ir::op::exp) return false;
+                const ir::node& d = g.at(e.lhs);
+                if (d.kind != ir::op::subtract || d.rhs < 0 || g.at(d.rhs).kind != ir::op::broadcast) return false;
+                const int max_id = g.at(d.rhs).lhs;
+                if (column_softmax_sum(max_id) != id || temp_of.count(max_id)) return false;
+                const int f = g.at(max_id).lhs;
+                std::set<int> inner;
+                boundaries(f, inner, {}, false);
+                for (const int b : inner) ensure_temp(b);
+                const std::vector<int64_t>& shape = g.at(f).out;
+                cg::kexpr k;
+                cg::lowering low(g, k, shape);
+                bind_inputs(low);
+                cg::column_reduce_request r;
+                r.expr = &k;
+                r.producer = low.at(f, low.identity());
+                r.shape = shape;
+                r.axis = static_cast<size_t>(n.axis);
+                r.n_slots = n_slots();
+                r.width = width;
+                const int64_t outputs = ir::numel(n.out);
+                const int64_t parts = cg::column_reduce_parts(r, compute_units);
+                plan.temp_elems[static_cast<size_t>(dest.index)] = 2 * outputs;
+                if (parts < 2) {
+                    add_step(cg::emit_column_softmax(r, -1), dest);
+                }
+                else {
+                    r.parts = parts;
+                    const int partial = static_cast<int>(plan.temp_elems.size());
+                    plan.temp_elems.push_back(3 * parts * outputs);
+                    add_step(cg::emit_column_softmax(r, -1), {arg_ref::kind::temp, partial});
+                    cg::column_reduce_request c = r;
+                    c.shape = {parts, outputs};
+                    c.axis = 0;
+                    c.parts = 1;
+                    c.n_slots = n_slots();
+                    // each strand merges at most 4 parts, as for the column
+                    // reductions' second pass
+                    c.max_cols = 64;
+                    while (c.max_cols > 1 && (256 / c.max_cols) * 4 < parts) c.max_cols /= 2;
+                    add_step(cg::emit_column_softmax(c, g.n_inputs + partial), dest);
+                }
+                temp_of[max_id] = dest.index;
+                offset_of[max_id] = 0;
+                offset_of[id] = outputs;
+                return true;
+            }
+
+            // ---------------------------------------------------------
             // other reductions, pointwise
             // ---------------------------------------------------------
             void emit_reduction(int id, arg_ref dest) {
+                if (try_column_softmax(id, dest)) return;
                 const ir::node& n = g.at(id);
                 std::set<int> inner;
                 boundaries(n.lhs, inner, {}, false);

@@ -1,0 +1,167 @@
+"""Softmax along a non-last axis (kernel kinds reduce.column_softmax and
+reduce.column_softmax_combine): the column max and the column sum of
+exp(x - max) from one read of x, then the elementwise quotient.
+
+The reference reads x twice for them (a max, then a sum of exp(x - max),
+src/ops.cpp:12-17 over src/tensor.cpp:896-962); here each lane folds a
+running max and a sum relative to an anchor that stays within 1 below it.
+Bars: within 1e-6 relative of the oracle on finite columns (or 2 ulp where
+the result is far below the column max), NaN exactly where the oracle has
+NaN; through assert_softmax_close on the transpose (the softmax of x over
+axis 0 is that of x^T over axis 1), which also holds the result to a
+float64 softmax.  CPU: the planner's choice, bounds, and values of the
+kernels run on the CPU.  GPU: full sizes, wide-range and special columns.
+"""
+
+import numpy as np
+import pytest
+
+import porch_amd as porch
+from oracle import host
+from tests.helpers import assert_softmax_close, placeholder
+from tests.kernel_emu import emulate as emu
+
+needs_clang = pytest.mark.skipif(not emu.available(), reason="host clang++ from ROCm is required")
+
+
+def _kinds(expr):
+    return [k["kind"] for k in porch.plan(expr)["kernels"]]
+
+
+def special_columns(rows, cols, seed):
+    """[rows, cols] with special columns first: a NaN, a +inf, all -inf,
+    -inf mixed in, signed zeros only, a rising and a falling ramp over
+    [-300, 300] (the anchor moves at every unit step), a sawtooth; the rest
+    N(0, 9)."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    x[rows // 3, 0] = np.nan
+    x[rows // 2, 1] = np.inf
+    x[:, 2] = -np.inf
+    x[::7, 3] = -np.inf
+    x[:, 4] = np.where(np.arange(rows) % 2 == 0, 0.0, -0.0)
+    x[:, 5] = np.linspace(-300.0, 300.0, rows)
+    x[:, 6] = np.linspace(300.0, -300.0, rows)
+    x[:, 7] = (np.arange(rows) % 97) * 0.5 + np.arange(rows) * 1e-2
+    return x
+
+
+def check_columns(out, x, oracle):
+    """`out` = softmax(x, 0) against the oracle's result `oracle` and, on
+    the finite columns, assert_softmax_close over the transpose."""
+    out = np.asarray(out, np.float32).reshape(x.shape)
+    oracle = np.asarray(oracle, np.float32).reshape(x.shape)
+    assert np.array_equal(np.isnan(out), np.isnan(oracle))
+    finite = np.isfinite(x).all(axis=0)
+    xt = np.ascontiguousarray(x[:, finite].T)
+    assert_softmax_close(np.ascontiguousarray(out[:, finite].T), placeholder(list(xt.shape), xt.reshape(-1)), xt)
+    ok = ~np.isnan(oracle)
+    np.testing.assert_allclose(out[ok], oracle[ok], rtol=1e-6, atol=1e-37)
+
+
+@pytest.mark.parametrize("shape, axis, kinds, temps", [
+    ([4096, 4096], 0, ["reduce.column_softmax", "reduce.column_softmax_combine", "pointwise.flat"],
+     [2 * 4096, 3 * 64 * 4096]),
+    ([65536, 256], 0, ["reduce.column_softmax", "reduce.column_softmax_combine", "pointwise.flat"],
+     [2 * 256, 3 * 1024 * 256]),
+    ([300, 500], 0, ["reduce.column_softmax", "pointwise.flat"], [2 * 500]),
+    ([8, 300, 64], 1, ["reduce.column_softmax", "pointwise.flat"], [2 * 8 * 64]),
+    ([100, 7, 33], 0, ["reduce.column_softmax", "pointwise.scalar"], [2 * 7 * 33]),
+])
+def test_plan(shape, axis, kinds, temps):
+    expr = porch.softmax(placeholder(shape), axis)
+    plan = porch.plan(expr, compile=True)
+    assert [k["kind"] for k in plan["kernels"]] == kinds
+    assert plan["temps"] == temps
+
+
+def test_last_axis_keeps_the_row_program():
+    assert _kinds(porch.softmax(placeholder([300, 500]), 1)) == ["row"]
+
+
+def test_a_max_read_elsewhere_is_not_fused():
+    # the column max is also an output term: it must be the reference's
+    # max (exact NaN and signed-zero rules), so it stays a column reduction
+    x = placeholder([300, 500])
+    expr = porch.softmax(x, 0) + porch.broadcast_to(porch.max(x, 0, True), [300, 500])
+    kinds = _kinds(expr)
+    assert "reduce.column_softmax" not in kinds and "reduce.column" in kinds
+    # the sum as the graph's result has no temporary to hold the max beside it
+    e = porch.exp(x - porch.broadcast_to(porch.max(x, 0, True), [300, 500]))
+    assert _kinds(porch.sum(e, 0, True)) == ["reduce.column", "reduce.column"]
+    # read by anything else it takes the fused pair
+    assert _kinds(porch.sum(e, 0, True) * 2.0) == ["reduce.column_softmax", "pointwise.flat"]
+
+
+@needs_clang
+@pytest.mark.parametrize("shape, axis, scale", [
+    ([300, 500], 0, 3.0),
+    ([8, 300, 64], 1, 3.0),
+    ([4096, 256], 0, 3.0),   # axis split in parts, then the combine
+    ([1030, 260], 0, 40.0),  # wide range: the anchor moves many times
+    ([100, 7, 33], 0, 3.0),
+])
+def test_emulated_values(shape, axis, scale):
+    rng = np.random.default_rng(sum(shape))
+    x = (rng.standard_normal(int(np.prod(shape))) * scale).astype(np.float32)
+    expr = porch.softmax(placeholder(shape, x), axis)
+    assert "reduce.column_softmax" in _kinds(expr)
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=600))
+    got = emu.evaluate(expr, [x], timeout=600).reshape(-1)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+    # the emulation's exp is the host's, so values are held to the
+    # oracle within 1e-6 (2 ulp where tiny)
+    ok = np.abs(got.astype(np.float64) - ref) <= 1e-6 * np.abs(ref) + 2 * np.spacing(np.abs(ref))
+    assert ok.all(), (np.flatnonzero(~ok)[:8], got[~ok][:8], ref[~ok][:8])
+
+
+@needs_clang
+def test_emulated_special_columns():
+    x = special_columns(1200, 64, 5)
+    expr = porch.softmax(placeholder(list(x.shape), x.reshape(-1)), 0)
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=600))
+    got = emu.evaluate(expr, [x.reshape(-1)], timeout=600).reshape(x.shape)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(x.shape)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.isnan(got[:, :3]).all()             # NaN, +inf, all -inf: NaN columns
+    assert not np.isnan(got[:, 3:]).any()
+    ok = ~np.isnan(ref)
+    assert np.all(np.abs(got[ok].astype(np.float64) - ref[ok]) <= 1e-6 * np.abs(ref[ok]) + 2 * np.spacing(np.abs(ref[ok])))
+
+
+# -- GPU -----------------------------------------------------------------------
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape, axis", [([4096, 4096], 0), ([65536, 256], 0), ([6000, 200], 0), ([8, 3000, 64], 1),
+                                         ([100, 7, 33], 0)])
+def test_softmax_over_a_non_last_axis(gpu, shape, axis):
+    rng = np.random.default_rng(sum(shape) + axis)
+    x = (rng.standard_normal(int(np.prod(shape))) * 3).astype(np.float32)
+    t = gpu.tensor(shape, x)
+    expr = gpu.softmax(t, axis)
+    assert "reduce.column_softmax" in _kinds(expr)
+    out = gpu.materialize(expr).cpu().reshape(-1)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+    assert np.all(np.abs(out - ref) <= 1e-6 * np.abs(ref)), np.max(np.abs(out - ref) / np.abs(ref))
+    if len(shape) == 2:
+        check_columns(out, x.reshape(shape), ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1200, 70000])
+def test_special_and_wide_range_columns(gpu, rows):
+    """NaN, +inf, -inf and signed-zero columns, ramps and a sawtooth (the
+    anchor moving at each unit step), N(0, 9) elsewhere; 70000 rows split
+    the axis into parts combined by the second kernel."""
+    x = special_columns(rows, 64, rows)
+    t = gpu.tensor(list(x.shape), x.reshape(-1))
+    expr = gpu.softmax(t, 0)
+    kinds = _kinds(expr)
+    assert kinds[0] == "reduce.column_softmax"
+    assert ("reduce.column_softmax_combine" in kinds) == (rows == 70000)
+    out = gpu.materialize(expr).cpu().reshape(x.shape)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(x.shape)
+    assert np.isnan(out[:, :3]).all() and not np.isnan(out[:, 3:]).any()
+    check_columns(out, x, ref)
+    assert np.allclose(out[:, 3:].astype(np.float64).sum(axis=0), 1.0, atol=2e-5)

@@ -65,9 +65,15 @@ def test_concat_along_the_last_axis(widths, kind):
 
 def test_shared_reductions_are_materialised_once():
     """softmax over a non-last axis cannot be one row program; its max is
-    still computed once (the reference computes it twice)."""
+    still computed once (the reference computes it twice): with its sum in
+    one kernel, or, where the max is also read elsewhere, as its own column
+    reduction feeding both."""
     x = placeholder([64, 32])
     plan = porch.plan(porch.softmax(x, 0))
+    assert [k["kind"] for k in plan["kernels"]] == ["reduce.column_softmax", "pointwise.flat"]
+    assert plan["temps"] == [2 * 32]  # the max and the sum side by side
+    m = porch.broadcast_to(porch.max(x, 0, True), [64, 32])
+    plan = porch.plan(porch.softmax(x, 0) * m)
     kinds = [k["kind"] for k in plan["kernels"]]
     assert kinds.count("reduce.column") == 2, kinds  # max and sum, once each
     assert len(plan["temps"]) == 2
