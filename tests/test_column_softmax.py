@@ -116,6 +116,24 @@ def test_emulated_values(shape, axis, scale):
 
 
 @needs_clang
+@pytest.mark.parametrize("rows", [300, 20000])
+def test_emulated_softmax_of_an_expression(rows):
+    # the folded values computed per row (temporaries named by the emitter
+    # inside each row's block), with and without parts
+    rng = np.random.default_rng(rows)
+    x = rng.standard_normal(rows * 64).astype(np.float32)
+    y = rng.standard_normal(rows * 64).astype(np.float32)
+    tx, ty = placeholder([rows, 64], x), placeholder([rows, 64], y)
+    expr = porch.softmax(porch.maximum(tx, 0.0) * 3.0 - ty, 0)
+    assert ("reduce.column_softmax_combine" in _kinds(expr)) == (rows == 20000)
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=600))
+    got = emu.evaluate(expr, [x, y], timeout=600).reshape(-1)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+    ok = np.abs(got.astype(np.float64) - ref) <= 1e-6 * np.abs(ref) + 2 * np.spacing(np.abs(ref))
+    assert ok.all(), (np.flatnonzero(~ok)[:8], got[~ok][:8], ref[~ok][:8])
+
+
+@needs_clang
 def test_emulated_special_columns():
     x = special_columns(1200, 64, 5)
     expr = porch.softmax(placeholder(list(x.shape), x.reshape(-1)), 0)
