@@ -183,3 +183,28 @@ def test_special_and_wide_range_columns(gpu, rows):
     assert np.isnan(out[:, :3]).all() and not np.isnan(out[:, 3:]).any()
     check_columns(out, x, ref)
     assert np.allclose(out[:, 3:].astype(np.float64).sum(axis=0), 1.0, atol=2e-5)
+
+
+@pytest.mark.gpu
+def test_random_shapes_and_axes(gpu):
+    """Seeded shapes of rank 2 to 4 and every non-last axis: lengths across
+    the split threshold, output counts that do and do not fill 128-bit
+    lanes, N(0, 9) values."""
+    rng = np.random.default_rng(2026)
+    seen = set()
+    for trial in range(24):
+        rank = int(rng.integers(2, 5))
+        shape = [int(rng.integers(1, 12)) for _ in range(rank)]
+        axis = int(rng.integers(0, rank - 1))
+        shape[axis] = int(rng.choice([3, 257, 1000, 5000, 40000]))
+        shape[-1] = int(rng.choice([1, 3, 4, 64, 130]))
+        x = (rng.standard_normal(int(np.prod(shape))) * 3).astype(np.float32)
+        expr = gpu.softmax(gpu.tensor(shape, x), axis)
+        kinds = _kinds(expr)
+        seen.update(kinds)
+        print("column softmax", trial, shape, axis, kinds, flush=True)
+        out = gpu.materialize(expr).cpu().reshape(-1)
+        ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+        ok = np.abs(out.astype(np.float64) - ref) <= 1e-6 * np.abs(ref) + 2 * np.spacing(np.abs(ref))
+        assert ok.all(), (trial, shape, axis, np.flatnonzero(~ok)[:4], out[~ok][:4], ref[~ok][:4])
+    assert {"reduce.column_softmax", "reduce.column_softmax_combine"} <= seen

@@ -188,3 +188,63 @@ def test_fuzz_products_bit_exact(gpu):
         assert np.max(np.abs(ref)) < LIMIT
         out = gpu.materialize(expr).cpu().reshape(expr.shape())
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, gpu.plan(expr))
+
+
+def random_lopsided_product(rng, make):
+    """A matmul with one short side or few tiles over a long K (the
+    few-row, few-column and split-K kernels), operands as in
+    random_product, with a random epilogue (a bias row among them)."""
+    form = int(rng.integers(0, 3))
+    if form == 0:    # a few rows: gemm.rows (+ gemm.combine)
+        m, k, n = int(rng.integers(1, 17)), int(rng.integers(64, 3000)), int(rng.integers(256, 1200))
+    elif form == 1:  # a few columns: gemm.cols
+        m, k, n = int(rng.integers(64, 3000)), int(rng.integers(1, 1500)), int(rng.integers(1, 5))
+    else:            # few 128 x 128 tiles over K >= 1024: split over K
+        m, k, n = int(rng.integers(17, 260)), int(rng.integers(1024, 3000)), int(rng.integers(32, 300))
+
+    def operand(rows, cols):
+        f = int(rng.integers(0, 3))
+        if f == 0:
+            return porch.tensor_expr(make([rows, cols], rng))
+        if f == 1:
+            return porch.transpose(porch.tensor_expr(make([cols, rows], rng)))
+        return porch.tensor_expr(make([rows, cols], rng)) * 2.0 - 1.0
+
+    expr = porch.matmul(operand(m, k), operand(k, n))
+    epi = int(rng.integers(0, 3))
+    if epi == 1:
+        expr = porch.relu(expr + porch.broadcast_to(porch.tensor_expr(make([1, n], rng)), [m, n])) - 0.5
+    elif epi == 2:
+        expr = porch.maximum(expr, porch.tensor_expr(make([m, n], rng))) * 2.0
+    return expr
+
+
+def test_lopsided_products_reach_their_kernels():
+    rng = np.random.default_rng(17)
+    kinds = set()
+    for _ in range(30):
+        plan = porch.plan(random_lopsided_product(rng, integer_leaf), compile=True)
+        kinds.update(k["kind"] for k in plan["kernels"])
+    assert {"gemm.rows", "gemm.cols", "gemm.combine", "gemm.mfma"} <= kinds
+
+
+@pytest.mark.gpu
+def test_fuzz_lopsided_products_bit_exact(gpu):
+    # integer leaves in [-3, 3]: |sums| <= 9 * 3000 < 2^24, exact in any order
+    rng = np.random.default_rng(123)
+
+    def device_leaf(shape, rng):
+        values = rng.integers(-3, 4, size=int(np.prod(shape))).astype(np.float32)
+        return gpu.tensor(shape, values)
+
+    kinds = set()
+    for trial in range(30):
+        expr = random_lopsided_product(rng, device_leaf)
+        plan = gpu.plan(expr)
+        kinds.update(k["kind"] for k in plan["kernels"])
+        print("lopsided product", trial, expr.shape(), [k["kind"] for k in plan["kernels"]], flush=True)
+        ref = host.evaluate(expr)
+        assert np.max(np.abs(ref)) < LIMIT
+        out = gpu.materialize(expr).cpu().reshape(expr.shape())
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, plan)
+    assert {"gemm.rows", "gemm.cols", "gemm.combine", "gemm.mfma"} <= kinds
