@@ -1,8 +1,8 @@
 // Softmax-shaped row programs over long rows (more than 32768 values), read
 // from memory once.  The row program row_request describes (a max of f, a
 // sum of exp(f - that max), an elementwise output) runs with each row split
-// into parts of at most 16384 values (as even as whole chunks of 1024
-// allow), one part per 256-lane workgroup held in registers (up to 64
+// into parts of at most 16384 values (as even as whole float4s allow),
+// one part per 256-lane workgroup held in registers (up to 64
 // values per lane).  Each part publishes its partial (max m, sum s of
 // exp(f - m)) as one 64-bit word; every part of a row then combines the
 // row's words, M = max of the m and S = sum of s exp(m - M), and writes its
@@ -49,8 +49,7 @@
 namespace porch::cg {
     namespace {
 
-        // At most 16 chunks of 1024 values per part (64 values per lane);
-        // a row's parts are as even as whole chunks allow.
+        // At most 16 chunks of 1024 values per part (64 values per lane).
         constexpr int64_t max_chunks = 16;
         // Workgroups resident per compute unit (the register budget allows
         // two at 225 VGPRs).
@@ -65,6 +64,7 @@ namespace porch::cg {
         struct split_shape {
             int64_t parts = 0;
             int64_t chunks = 0; // chunks of 1024 values (4 per lane) per part
+            int64_t span = 0;   // values per part (a multiple of 4; the last part may hold fewer)
             int64_t groups = 0; // row groups per XCD per round
             int64_t grid = 0;
             int64_t rounds = 0;
@@ -110,7 +110,11 @@ namespace porch::cg {
             for (size_t dd = 0; dd + 1 < rank; ++dd)
                 if (leaf.index.w[dd] % 4 != 0) return sh;
             const int64_t parts = (length + max_chunks * 1024 - 1) / (max_chunks * 1024);
-            const int64_t chunks = (length + parts * 1024 - 1) / (parts * 1024);
+            // Parts as even as whole float4s allow, their last chunk partly
+            // used: with parts of whole chunks, 49156 values gave parts of
+            // 13, 13, 13 and 9 chunks, and every round waited on a 13.
+            const int64_t span = (length + 4 * parts - 1) / (4 * parts) * 4;
+            const int64_t chunks = (span + 1023) / 1024;
             const int64_t resident = groups_per_cu * static_cast<int64_t>(std::max(r.compute_units, 8));
             const int64_t groups = resident / (8 * parts);
             if (groups < 1) return sh;
@@ -118,6 +122,7 @@ namespace porch::cg {
             for (size_t dd = 0; dd + 1 < rank; ++dd) rows *= r.shape[dd];
             sh.parts = parts;
             sh.chunks = chunks;
+            sh.span = span;
             sh.groups = groups;
             sh.grid = 8 * parts * groups;
             sh.rounds = (rows + 8 * groups - 1) / (8 * groups);
@@ -197,9 +202,15 @@ namespace porch::cg {
         auto chunk_loop = [&](const std::string& indent, const std::string& body) {
             std::string c = indent + "#pragma unroll\n";
             c += indent + "for (int j = 0; j < " + std::to_string(sh.chunks) + "; ++j) {\n";
-            c += indent + "    const " + T + " " + qc + " = (" + T + ")part * " + std::to_string(sh.chunks * 1024) +
+            c += indent + "    const " + T + " " + qc + " = (" + T + ")part * " + std::to_string(sh.span) +
                  " + j * 1024 + tl * 4;\n";
-            c += indent + "    if (" + qc + " < " + L + ") {\n" + body + indent + "    }\n";
+            // inside the part (where its span is not whole chunks) and the row
+            std::string inside;
+            if (sh.span != sh.chunks * 1024) inside = "j * 1024 + tl * 4 < " + std::to_string(sh.span);
+            if (sh.parts * sh.span != length)
+                inside += std::string(inside.empty() ? "" : " && ") + qc + " < " + L;
+            if (inside.empty()) inside = "true";
+            c += indent + "    if (" + inside + ") {\n" + body + indent + "    }\n";
             c += indent + "}\n";
             return c;
         };
