@@ -187,7 +187,7 @@ namespace porch::cg {
     kernel_code emit_gemm_combine(const gemm_request& request, int64_t chunks, int partial_slot);
 
     // Products with one short side (emit_gemm_skinny.cpp).  A few rows
-    // (m <= 32, n >= 256): `gemm_few_rows_partials` floats of partial
+    // (m <= 16, n >= 256): `gemm_few_rows_partials` floats of partial
     // products over `gemm_few_rows_chunks` chunks of K (0 partials: one
     // chunk, the first kernel writes the result), then emit_gemm_combine.
     bool gemm_few_rows(const gemm_request& request);

@@ -2,9 +2,10 @@
 //
 // The one-output-per-lane K loop (gemm.scalar) gives a vector-matrix
 // product [1, 4096] @ [4096, 4096] 16 workgroups and 182 us; the MFMA tiles
-// need 32 rows or columns.  Two forms instead:
+// of 128 x 128 spend most of their work on padding when one side is a few
+// rows or columns.  Two forms instead:
 //
-//   gemm.rows     few rows (m <= 32, n >= 256): one wave per 256 columns
+//   gemm.rows     few rows (m <= 16, n >= 256): one wave per 256 columns
 //                 of B and a chunk of K, each lane holding m x 4
 //                 accumulators for its four columns, A's values read as
 //                 wave-uniform scalars; the chunks' partial products go to a
