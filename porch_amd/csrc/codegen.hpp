@@ -194,7 +194,8 @@ namespace porch::cg {
     int64_t gemm_few_rows_partials(const gemm_request& request);
     int64_t gemm_few_rows_chunks(const gemm_request& request);
     kernel_code emit_gemm_few_rows(const gemm_request& request);
-    // A few columns (n <= 4, m >= 64): one wave per output row.
+    // A few columns (n <= 4 over 64 rows or more, n <= 8 over 2048 rows or
+    // more): one wave per 1, 2 or 4 output rows.
     bool gemm_few_cols(const gemm_request& request);
     kernel_code emit_gemm_few_cols(const gemm_request& request);
 

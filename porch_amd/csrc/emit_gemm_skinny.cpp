@@ -12,9 +12,11 @@
 //                 temporary [chunks, batch, m, n] that gemm.combine sums
 //                 per output, applying the epilogue.  With one chunk
 //                 the first kernel applies the epilogue itself.
-//   gemm.cols     few columns (n <= 4, m >= 64): one wave per output row,
-//                 lanes along K reading A with 128-bit loads, n
-//                 accumulators per lane and a butterfly per output.
+//   gemm.cols     few columns (n <= 4 over 64 rows or more, n <= 8 over 2048
+//                 or more): one wave per 1, 2 or 4 output rows (which share
+//                 each load of B), lanes along K reading A with 128-bit
+//                 loads, n accumulators per row and lane and a butterfly
+//                 per output.
 //
 // Sums run in other orders than the reference's sequential K loop, within
 // the matmul's tolerance (an accumulation-bound per element).
@@ -32,6 +34,7 @@ namespace porch::cg {
         // and 32 rows of 4096 x 4096, 17-20 against 28-40 us at 1024).
         constexpr int64_t max_rows = 16;
         constexpr int64_t max_cols = 4;
+        constexpr int64_t max_cols_many_rows = 8;
         constexpr int64_t block_cols = 256; // columns per wave in gemm.rows
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
@@ -199,7 +202,12 @@ namespace porch::cg {
         return kc;
     }
 
-    bool gemm_few_cols(const gemm_request& r) { return r.n <= max_cols && r.m >= 64 && big_enough(r); }
+    bool gemm_few_cols(const gemm_request& r) {
+        // 5 to 8 columns only over many rows (measured at 4096 rows: 23 us
+        // at 8 columns against 31 us for the split MFMA kernel)
+        return ((r.n <= max_cols && r.m >= 64) || (r.n <= max_cols_many_rows && r.batch * r.m >= 2048)) &&
+               big_enough(r);
+    }
 
     kernel_code emit_gemm_few_cols(const gemm_request& r) {
         if (!gemm_few_cols(r)) throw std::logic_error("emit_gemm_few_cols: not a few-column product");
@@ -207,53 +215,84 @@ namespace porch::cg {
         const char* T = r.width.type();
         const std::string batch = r.batched ? "qb" : "";
         const std::string N = std::to_string(r.n);
-        const int64_t rows = r.batch * r.m;
+        const std::string M = std::to_string(r.m);
+        // Rows per wave: B is read once per wave, so the wave's rows share
+        // each load of it (with one row per wave, every wave reread all of
+        // B from the L2: n x 64 MB over [4096, 4096] @ [4096, n]), against
+        // fewer waves to hide the loads' latency.  Measured on
+        // [4096, 4096] @ [4096, n] (1, 2, 4 or 8 rows a wave): n = 1, 2
+        // fastest with 1 (12.8, 13.2 us), n = 4 with 2 (15.3 against 19.6
+        // us with 1), n = 8 with 4 (23.2 against 33.8 with 2).
+        const int64_t R = r.n <= 2 ? 1 : (r.n <= 4 ? 2 : 4);
+        const std::string RS = std::to_string(R);
+        const int64_t row_groups = (r.m + R - 1) / R; // per batch entry
+        const int64_t groups = r.batch * row_groups;
 
         kernel_code kc;
         kc.kind = "gemm.cols";
         kc.name = "porch_gemm";
         kc.n_slots = r.n_slots;
         kc.block = 256;
-        kc.grid_x = static_cast<unsigned>(std::min<int64_t>((rows + 3) / 4, 16 * std::max(r.compute_units, 8)));
+        kc.grid_x = static_cast<unsigned>(std::min<int64_t>((groups + 3) / 4, 16 * std::max(r.compute_units, 8)));
 
         std::string& s = kc.source;
         s = kernel_prologue(r.n_slots, T);
         s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" + kernel_params(r.n_slots) + ") {\n";
         s += "    const int lane = threadIdx.x & 63;\n";
-        s += "    for (idx_t row = (idx_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < " + std::to_string(rows) +
-             "; row += (idx_t)gridDim.x * 4) {\n";
-        if (r.batched) s += "        const idx_t qb = row / " + std::to_string(r.m) + ";\n";
-        s += "        const idx_t q0 = row % " + std::to_string(r.m) + ";\n";
-        s += "        float acc[" + N + "];\n";
-        s += "        #pragma unroll\n        for (int j = 0; j < " + N + "; ++j) acc[j] = 0.0f;\n";
+        s += "    for (idx_t grp = (idx_t)blockIdx.x * 4 + (threadIdx.x >> 6); grp < " + std::to_string(groups) +
+             "; grp += (idx_t)gridDim.x * 4) {\n";
+        s += "        const idx_t qb = grp / " + std::to_string(row_groups) + ";\n";
+        if (!r.batched) s += "        (void)qb;\n";
+        s += "        const idx_t q00 = (grp % " + std::to_string(row_groups) + ") * " + RS + ";\n";
+        s += "        float acc[" + RS + "][" + N + "];\n";
+        s += "        #pragma unroll\n        for (int r = 0; r < " + RS + "; ++r)\n";
+        s += "            #pragma unroll\n            for (int j = 0; j < " + N + "; ++j) acc[r][j] = 0.0f;\n";
         const std::string bslot = "a" + std::to_string(r.b.slot);
         if (vec) {
             s += "        for (idx_t kq = lane * 4; kq < " + std::to_string(r.k) + "; kq += 256) {\n";
-            s += "            const porch_v4f w = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a" +
+            s += "            float av[" + RS + "][4];\n";
+            s += "            #pragma unroll\n            for (int r = 0; r < " + RS + "; ++r) {\n";
+            s += "                const idx_t q0 = q00 + r;\n";
+            s += "                porch_v4f w = {0.0f, 0.0f, 0.0f, 0.0f};\n";
+            s += "                if (q0 < " + M + ") w = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a" +
                  std::to_string(r.a.slot) + " + " + operand_index(r.a, "q0", "kq", batch) + "));\n";
-            s += "            const float av[4] = {w.x, w.y, w.z, w.w};\n";
+            s += "                av[r][0] = w.x; av[r][1] = w.y; av[r][2] = w.z; av[r][3] = w.w;\n";
+            s += "            }\n";
             s += "            #pragma unroll\n            for (int e = 0; e < 4; ++e)\n";
-            s += "                #pragma unroll\n                for (int j = 0; j < " + N + "; ++j)\n";
-            s += "                    acc[j] = __builtin_fmaf(av[e], " + bslot + "[" +
-                 operand_index(r.b, "kq + e", "j", batch) + "], acc[j]);\n";
+            s += "                #pragma unroll\n                for (int j = 0; j < " + N + "; ++j) {\n";
+            s += "                    const float b = " + bslot + "[" + operand_index(r.b, "kq + e", "j", batch) + "];\n";
+            s += "                    #pragma unroll\n                    for (int r = 0; r < " + RS + "; ++r)\n";
+            s += "                        acc[r][j] = __builtin_fmaf(av[r][e], b, acc[r][j]);\n";
+            s += "                }\n";
             s += "        }\n";
         }
         else {
             s += "        for (idx_t kk = lane; kk < " + std::to_string(r.k) + "; kk += 64) {\n";
-            s += "            const float av = a" + std::to_string(r.a.slot) + "[" + operand_index(r.a, "q0", "kk", batch) +
-                 "];\n";
-            s += "            #pragma unroll\n            for (int j = 0; j < " + N + "; ++j)\n";
-            s += "                acc[j] = __builtin_fmaf(av, " + bslot + "[" + operand_index(r.b, "kk", "j", batch) +
-                 "], acc[j]);\n";
+            s += "            #pragma unroll\n            for (int j = 0; j < " + N + "; ++j) {\n";
+            s += "                const float b = " + bslot + "[" + operand_index(r.b, "kk", "j", batch) + "];\n";
+            s += "                #pragma unroll\n                for (int r = 0; r < " + RS + "; ++r) {\n";
+            s += "                    const idx_t q0 = q00 + r;\n";
+            s += "                    const float av = q0 < " + M + " ? a" + std::to_string(r.a.slot) + "[" +
+                 operand_index(r.a, "q0", "kk", batch) + "] : 0.0f;\n";
+            s += "                    acc[r][j] = __builtin_fmaf(av, b, acc[r][j]);\n";
+            s += "                }\n";
+            s += "            }\n";
             s += "        }\n";
         }
-        s += "        #pragma unroll\n        for (int j = 0; j < " + N + "; ++j)\n";
-        s += "            for (int d = 32; d >= 1; d >>= 1) acc[j] += __shfl_xor(acc[j], d, 64);\n";
+        s += "        #pragma unroll\n        for (int r = 0; r < " + RS + "; ++r)\n";
+        s += "            #pragma unroll\n            for (int j = 0; j < " + N + "; ++j)\n";
+        s += "                for (int d = 32; d >= 1; d >>= 1) acc[r][j] += __shfl_xor(acc[r][j], d, 64);\n";
         s += "        if (lane == 0) {\n";
-        s += "            #pragma unroll\n            for (int j = 0; j < " + N + "; ++j) {\n";
-        s += "                const idx_t q1 = j;\n";
-        s += "                const float acc_v = acc[j];\n";
-        s += epilogue_store(r, "acc_v", "row * " + N + " + q1", "                ");
+        s += "            #pragma unroll\n            for (int r = 0; r < " + RS + "; ++r) {\n";
+        s += "                const idx_t q0 = q00 + r;\n";
+        s += "                if (q0 < " + M + ") {\n";
+        s += "                    const idx_t row = qb * " + M + " + q0;\n";
+        s += "                    #pragma unroll\n                    for (int j = 0; j < " + N + "; ++j) {\n";
+        s += "                        const idx_t q1 = j;\n";
+        s += "                        const float acc_v = acc[r][j];\n";
+        s += epilogue_store(r, "acc_v", "row * " + N + " + q1", "                        ");
+        s += "                    }\n";
+        s += "                }\n";
         s += "            }\n        }\n    }\n}\n";
         return kc;
     }

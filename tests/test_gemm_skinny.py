@@ -1,6 +1,7 @@
 """Matmuls with one short side (kernel kinds gemm.rows, gemm.combine,
 gemm.cols): a few rows (a vector times a matrix, a small batch of rows) or a
-few columns (a matrix times a vector); and matmuls whose tiles leave most of
+few columns (a matrix times a vector; up to 8 columns over many rows, one
+wave holding 1, 2 or 4 rows); and matmuls whose tiles leave most of
 the machine idle over a long K (gemm.mfma split over K, then gemm.combine).
 
 Bars: bit for bit on integer data (every partial sum exact, whatever the
@@ -62,6 +63,15 @@ CASES = {
     "three columns, odd K, bias": (
         ([5000, 701], [701, 3]), lambda a, b: porch.matmul(a, b) + 2.0, lambda a, b: a @ b, lambda p: p + 2.0,
         ["gemm.cols"]),
+    "eight columns over many rows": (
+        ([2048, 700], [700, 8]), lambda a, b: porch.matmul(a, b) * 0.5 + 1.0, lambda a, b: a @ b,
+        lambda p: p * 0.5 + 1.0, ["gemm.cols"]),
+    "six columns, batched, ragged row groups": (
+        ([2, 1101, 512], [2, 512, 6]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.cols"]),
+    "three columns, ragged row pairs, transposed B": (
+        ([1001, 300], [3, 300]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+        lambda p: p, ["gemm.cols"]),
     "columns, transposed A": (
         ([1024, 2000], [1024, 2]), lambda a, b: porch.matmul(porch.transpose(a), b), lambda a, b: a.T @ b,
         lambda p: p, ["gemm.cols"]),
@@ -154,7 +164,9 @@ def test_emulated_split_k_with_a_bias_is_exact():
 @pytest.mark.parametrize("name", ["rows, ragged columns", "rows, transposed B", "rows, batched",
                                   "rows, one chunk", "three columns, odd K, bias", "columns, transposed A",
                                   "split K, ragged K, relu epilogue", "split K, transposed A",
-                                  "split K, five rows", "split K, eight columns"])
+                                  "split K, five rows", "split K, eight columns",
+                                  "eight columns over many rows", "six columns, batched, ragged row groups",
+                                  "three columns, ragged row pairs, transposed B"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
     xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
