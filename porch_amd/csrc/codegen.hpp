@@ -29,8 +29,11 @@
 //                    epilogue applied to the accumulators before the store;
 //   gemm.rows,       products with a few rows (or columns), streaming the
 //   gemm.cols        long operand once;
-//   gemm.combine     the sum of K-chunk partial products (gemm.rows, or the
-//                    MFMA kernel split over K), with the epilogue.
+//   gemm.narrow      7 to 32 columns over many rows: v_mfma_f32_16x16x4f32
+//                    blocks fed straight from 128-bit loads of A;
+//   gemm.combine     the sum of K-chunk partial products (gemm.rows,
+//                    gemm.narrow, or the MFMA kernel split over K), with the
+//                    epilogue.
 
 #include "lower.hpp"
 
@@ -198,5 +201,11 @@ namespace porch::cg {
     // more): one wave per 1, 2 or 4 output rows.
     bool gemm_few_cols(const gemm_request& request);
     kernel_code emit_gemm_few_cols(const gemm_request& request);
+    // Up to 32 columns over 1024 rows or more (A rows contiguous along K):
+    // one wave per 32 rows and a chunk of K on 16x16x4 MFMA blocks, the
+    // chunks' partial products summed by emit_gemm_combine.
+    bool gemm_narrow(const gemm_request& request);
+    int64_t gemm_narrow_chunks(const gemm_request& request);
+    kernel_code emit_gemm_narrow(const gemm_request& request);
 
 } // namespace porch::cg

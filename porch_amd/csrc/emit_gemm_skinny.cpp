@@ -17,6 +17,12 @@
 //                 each load of B), lanes along K reading A with 128-bit
 //                 loads, n accumulators per row and lane and a butterfly
 //                 per output.
+//   gemm.narrow   up to 32 columns over many rows: one wave per 32 rows and
+//                 a chunk of K, v_mfma_f32_16x16x4f32 blocks fed straight
+//                 from 128-bit loads of A (lane l reads row l % 16, k in
+//                 4 (l / 16) .. +3, one MFMA per k of the four), B read per
+//                 lane from the L2; partial products of the chunks summed by
+//                 gemm.combine.
 //
 // Sums run in other orders than the reference's sequential K loop, within
 // the matmul's tolerance (an accumulation-bound per element).
@@ -36,6 +42,12 @@ namespace porch::cg {
         constexpr int64_t max_cols = 4;
         constexpr int64_t max_cols_many_rows = 8;
         constexpr int64_t block_cols = 256; // columns per wave in gemm.rows
+        // gemm.cols is faster up to 6 columns (17.6 and 18.2 against 19.4
+        // and 19.2 us at 5 and 6 over 4096 rows; at 8 20.4 against 23.1)
+        constexpr int64_t narrow_min_cols = 7;
+        constexpr int64_t narrow_max_cols = 32;
+        constexpr int64_t narrow_min_rows = 1024; // rows of A over all batch entries
+        constexpr int narrow_depth = 4;           // steps of K whose loads are issued together
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
 
@@ -86,6 +98,40 @@ namespace porch::cg {
             epilogue_emitter(em, r, names_of(r), acc);
             const std::string v = em.emit(r.epilogue)[0];
             return body + indent + "out[" + o + "] = " + v + ";\n";
+        }
+
+        struct narrow_shape {
+            int64_t rb = 0;     // 16-row MFMA blocks per wave
+            int64_t nb = 0;     // 16-column MFMA blocks
+            int64_t tiles = 0;  // row tiles of 16 rb rows per batch entry
+            int64_t chunks = 0; // K chunks
+            int64_t chunk = 0;  // K per chunk, a multiple of 16
+        };
+
+        narrow_shape narrow_plan(const gemm_request& r) {
+            narrow_shape sh;
+            if (r.n < narrow_min_cols || r.n > narrow_max_cols || r.batch * r.m < narrow_min_rows || !a_vector(r) ||
+                !big_enough(r))
+                return sh;
+            sh.rb = 2;
+            sh.nb = (r.n + 15) / 16;
+            sh.tiles = (r.m + 16 * sh.rb - 1) / (16 * sh.rb);
+            // About four waves per compute unit (measured on [4096, 4096]
+            // @ [4096, n], n = 4 .. 32: 20.0-24.1 us with the combine, 19.6-
+            // 27.4 at eight, 21.7-38.1 at sixteen), the partial products
+            // (chunks x m x n) at most 1/16 of A (m x K), chunks a multiple
+            // of the loop's 64 values of K (10 chunks of 416 at n = 24:
+            // 33.7 us, against 19.6 with 8 of 512).
+            const int64_t waves = 4 * std::max(r.compute_units, 8);
+            const int64_t batch_k = 16 * narrow_depth;
+            int64_t chunks = (waves + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
+            chunks = std::min(chunks, std::max<int64_t>(1, r.k / (16 * r.n)));
+            chunks = std::min(chunks, std::max<int64_t>(1, r.k / batch_k));
+            int64_t chunk = (r.k + chunks - 1) / chunks;
+            chunk = (chunk + batch_k - 1) / batch_k * batch_k;
+            sh.chunks = (r.k + chunk - 1) / chunk;
+            sh.chunk = chunk;
+            return sh;
         }
 
     } // namespace
@@ -207,7 +253,8 @@ namespace porch::cg {
 
     bool gemm_few_cols(const gemm_request& r) {
         // 5 to 8 columns only over many rows (measured at 4096 rows: 23 us
-        // at 8 columns against 31 us for the split MFMA kernel)
+        // at 8 columns against 31 us for the split MFMA kernel); the
+        // planner takes gemm.narrow first where A allows it
         return ((r.n <= max_cols && r.m >= 64) || (r.n <= max_cols_many_rows && r.batch * r.m >= 2048)) &&
                big_enough(r);
     }
@@ -300,6 +347,131 @@ namespace porch::cg {
         s += "                    }\n";
         s += "                }\n";
         s += "            }\n        }\n    }\n}\n";
+        return kc;
+    }
+
+    bool gemm_narrow(const gemm_request& r) { return narrow_plan(r).rb > 0; }
+
+    int64_t gemm_narrow_chunks(const gemm_request& r) { return narrow_plan(r).chunks; }
+
+    kernel_code emit_gemm_narrow(const gemm_request& r) {
+        const narrow_shape sh = narrow_plan(r);
+        if (sh.rb == 0) throw std::logic_error("emit_gemm_narrow: not a narrow product");
+        const bool final = sh.chunks == 1;
+        const char* T = r.width.type();
+        const std::string batch = r.batched ? "qb" : "";
+        const std::string M = std::to_string(r.m);
+        const std::string N = std::to_string(r.n);
+        const std::string K = std::to_string(r.k);
+        const std::string RB = std::to_string(sh.rb);
+        const std::string NB = std::to_string(sh.nb);
+        const int64_t tiles = r.batch * sh.tiles;
+        const int64_t waves = tiles * sh.chunks;
+
+        kernel_code kc;
+        kc.kind = "gemm.narrow";
+        kc.name = "porch_gemm";
+        kc.n_slots = r.n_slots;
+        kc.block = 256;
+        kc.grid_x = static_cast<unsigned>((waves + 3) / 4);
+
+        std::string& s = kc.source;
+        s = kernel_prologue(r.n_slots, T);
+        s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" + kernel_params(r.n_slots) + ") {\n";
+        s += "    const int lane = threadIdx.x & 63;\n";
+        s += "    const int li = lane & 15;\n    const int lg = lane >> 4;\n";
+        // waves of one chunk are adjacent: they share its rows of B
+        s += "    const idx_t wid = (idx_t)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
+        s += "    if (wid >= " + std::to_string(waves) + ") return;\n";
+        s += "    const idx_t ks = wid / " + std::to_string(tiles) + ";\n";
+        s += "    const idx_t tile = wid % " + std::to_string(tiles) + ";\n";
+        s += "    const idx_t qb = tile / " + std::to_string(sh.tiles) + ";\n";
+        if (!r.batched) s += "    (void)qb;\n";
+        s += "    const idx_t r0 = (tile % " + std::to_string(sh.tiles) + ") * " + std::to_string(16 * sh.rb) + ";\n";
+        s += "    const idx_t k0 = ks * " + std::to_string(sh.chunk) + ";\n";
+        s += "    const idx_t k1 = k0 + " + std::to_string(sh.chunk) + " < " + K + " ? k0 + " +
+             std::to_string(sh.chunk) + " : (idx_t)" + K + ";\n";
+        s += "    porch_v4f acc[" + RB + "][" + NB + "];\n";
+        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
+        s += "        #pragma unroll\n        for (int j = 0; j < " + NB + "; ++j) acc[i][j] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+        // Rows past m and columns past n are read at m - 1 and n - 1: they
+        // feed only outputs that are not stored, so the loads need no
+        // guard (guarded loads became one branch each, with every step
+        // waiting for all of its loads).
+        s += "    idx_t qa[" + RB + "];\n";
+        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i) {\n";
+        s += "        const idx_t q0 = r0 + i * 16 + li;\n";
+        s += "        qa[i] = q0 < " + M + " ? q0 : (idx_t)" + std::to_string(r.m - 1) + ";\n";
+        s += "    }\n";
+        s += "    idx_t qc[" + NB + "];\n";
+        s += "    #pragma unroll\n    for (int j = 0; j < " + NB + "; ++j) {\n";
+        s += "        const idx_t q1 = j * 16 + li;\n";
+        s += "        qc[j] = q1 < " + N + " ? q1 : (idx_t)" + std::to_string(r.n - 1) + ";\n";
+        s += "    }\n";
+        // One step of 16 values of K: lane l holds k = kq + e, kq = kk +
+        // 4 (l / 16), of its A row and B column; MFMA e takes value e of
+        // every lane.  The loads of D steps are issued before their MFMAs.
+        // `tail`: the last, partial step of K, where k past it is read at
+        // its last 4 values and both operands are zeroed (zeroing one would
+        // turn an infinity in the other into NaN).
+        auto steps = [&](int D, bool tail, const std::string& ind) {
+            std::string t;
+            const std::string Ds = std::to_string(D);
+            t += ind + "porch_v4f av[" + Ds + "][" + RB + "];\n";
+            t += ind + "float bv[" + Ds + "][" + NB + "][4];\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + Ds + "; ++d) {\n";
+            t += ind + "    const idx_t kq = kk + d * 16 + lg * 4;\n";
+            if (tail) {
+                t += ind + "    const bool kin = kq < k1;\n";
+                t += ind + "    const idx_t kr = kin ? kq : k1 - 4;\n";
+            }
+            const std::string kr = tail ? "kr" : "kq";
+            t += ind + "    #pragma unroll\n" + ind + "    for (int i = 0; i < " + RB + "; ++i) {\n";
+            t += ind + "        const idx_t q0 = qa[i];\n";
+            t += ind + "        av[d][i] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a" +
+                 std::to_string(r.a.slot) + " + " + operand_index(r.a, "q0", kr, batch) + "));\n";
+            if (tail) t += ind + "        if (!kin) av[d][i] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+            t += ind + "    }\n";
+            t += ind + "    #pragma unroll\n" + ind + "    for (int j = 0; j < " + NB + "; ++j) {\n";
+            t += ind + "        const idx_t q1 = qc[j];\n";
+            t += ind + "        #pragma unroll\n" + ind + "        for (int e = 0; e < 4; ++e) {\n";
+            t += ind + "            bv[d][j][e] = a" + std::to_string(r.b.slot) + "[" +
+                 operand_index(r.b, kr + " + e", "q1", batch) + "];\n";
+            if (tail) t += ind + "            if (!kin) bv[d][j][e] = 0.0f;\n";
+            t += ind + "        }\n" + ind + "    }\n" + ind + "}\n";
+            // left to itself the scheduler sinks each load to its MFMA,
+            // waiting for it there
+            t += ind + "__builtin_amdgcn_sched_barrier(0);\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + Ds + "; ++d)\n";
+            t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
+            t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
+            t += ind + "            #pragma unroll\n" + ind + "            for (int j = 0; j < " + NB + "; ++j)\n";
+            t += ind + "                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[d][i][e], bv[d][j][e], acc[i][j], 0, 0, 0);\n";
+            return t;
+        };
+        const int D = narrow_depth;
+        s += "    idx_t kk = k0;\n";
+        s += "    for (; kk + " + std::to_string(16 * D) + " <= k1; kk += " + std::to_string(16 * D) + ") {\n" +
+             steps(D, false, "        ") + "    }\n";
+        if (sh.chunk % (16 * D) != 0 || r.k % (16 * D) != 0)
+            s += "    for (; kk + 16 <= k1; kk += 16) {\n" + steps(1, false, "        ") + "    }\n";
+        if (r.k % 16 != 0) s += "    if (kk < k1) {\n" + steps(1, true, "        ") + "    }\n";
+        // accumulator value v of lane l: row 4 (l / 16) + v, column l % 16
+        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
+        s += "        #pragma unroll\n        for (int j = 0; j < " + NB + "; ++j)\n";
+        s += "            #pragma unroll\n            for (int v = 0; v < 4; ++v) {\n";
+        s += "                const idx_t q0 = r0 + i * 16 + lg * 4 + v;\n";
+        s += "                const idx_t q1 = j * 16 + li;\n";
+        s += "                if (q0 < " + M + " && q1 < " + N + ") {\n";
+        const std::string o = std::string(r.batched ? "(qb * " + M + " + q0)" : "q0") + " * " + N + " + q1";
+        if (final) {
+            s += "                    const float acc_v = acc[i][j][v];\n";
+            s += epilogue_store(r, "acc_v", o, "                    ");
+        }
+        else {
+            s += "                    out[ks * " + std::to_string(r.batch * r.m * r.n) + " + " + o + "] = acc[i][j][v];\n";
+        }
+        s += "                }\n            }\n}\n";
         return kc;
     }
 

@@ -290,6 +290,20 @@ namespace porch::plan {
                     add_step(cg::emit_gemm_combine(c, cg::gemm_few_rows_chunks(r), g.n_inputs + t), dest);
                     return true;
                 }
+                if (cg::gemm_narrow(r)) {
+                    const int64_t chunks = cg::gemm_narrow_chunks(r);
+                    if (chunks == 1) {
+                        add_step(cg::emit_gemm_narrow(r), dest);
+                        return true;
+                    }
+                    const int t = static_cast<int>(plan.temp_elems.size());
+                    plan.temp_elems.push_back(chunks * r.batch * r.m * r.n);
+                    add_step(cg::emit_gemm_narrow(r), {arg_ref::kind::temp, t});
+                    cg::gemm_request c = r;
+                    c.n_slots = n_slots();
+                    add_step(cg::emit_gemm_combine(c, chunks, g.n_inputs + t), dest);
+                    return true;
+                }
                 if (cg::gemm_few_cols(r)) {
                     add_step(cg::emit_gemm_few_cols(r), dest);
                     return true;

@@ -8,8 +8,8 @@
 // not the point (the oracle checks those); addresses are.
 //
 // Emulated: thread/block indices, __syncthreads (a barrier over the
-// block's threads), wave64 __shfl_xor, __shfl, __ballot, DPP row patterns and
-// v_mfma_f32_32x32x2f32 (barriers
+// block's threads), wave64 __shfl_xor, __shfl, __ballot, DPP row patterns,
+// v_mfma_f32_32x32x2f32 and v_mfma_f32_16x16x4f32 (barriers
 // over the wave's 64 threads, operand layouts as on gfx950), raw buffer
 // stores (range-checked against the resource's size), LDS arrays
 // (function-local statics, shared by the block's threads; blocks run one
@@ -116,6 +116,29 @@ namespace emu {
         return out;
     }
 
+    typedef float v4 __attribute__((ext_vector_type(4)));
+
+    // v_mfma_f32_16x16x4f32: lane l holds A[l % 16][l / 16] and
+    // B[l / 16][l % 16]; accumulator register v of lane l is
+    // C[4 (l / 16) + v][l % 16].
+    inline v4 mfma_16x16x4(float a, float b, v4 c) {
+        const int w = wave();
+        const int l = lane();
+        wave_a[w][l] = a;
+        wave_b[w][l] = b;
+        wave_barrier[w]->arrive_and_wait();
+        v4 out = c;
+        for (int v = 0; v < 4; ++v) {
+            const int i = 4 * (l / 16) + v;
+            const int j = l % 16;
+            float sum = 0.0f;
+            for (int kk = 0; kk < 4; ++kk) sum += wave_a[w][16 * kk + i] * wave_b[w][16 * kk + j];
+            out[v] = c[v] + sum;
+        }
+        wave_barrier[w]->arrive_and_wait();
+        return out;
+    }
+
     // A raw buffer resource (stride 0): stores at byte offsets at or past
     // num_records are dropped, as the hardware's range check does.
     struct buffer_rsrc {
@@ -146,11 +169,13 @@ namespace emu {
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
+#define __builtin_amdgcn_sched_barrier(a) ((void)0)
 #define __builtin_amdgcn_s_sleep(n) std::this_thread::yield()
 #define __HIP_MEMORY_SCOPE_AGENT 0
 #define __hip_atomic_load(p, order, scope) __atomic_load_n((p), (order))
 #define __hip_atomic_store(p, v, order, scope) __atomic_store_n((p), (v), (order))
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, x, y, z) emu::mfma_32x32x2((a), (b), (c))
+#define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) emu::mfma_16x16x4((a), (b), (c))
 #define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu::update_dpp((src), (ctrl))
 #define __builtin_amdgcn_make_buffer_rsrc(p, stride, num, flags) \
     emu::buffer_rsrc{reinterpret_cast<char*>(p), static_cast<uint32_t>(num)}

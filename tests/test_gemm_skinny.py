@@ -1,8 +1,10 @@
 """Matmuls with one short side (kernel kinds gemm.rows, gemm.combine,
-gemm.cols): a few rows (a vector times a matrix, a small batch of rows) or a
-few columns (a matrix times a vector; up to 8 columns over many rows, one
-wave holding 1, 2 or 4 rows); and matmuls whose tiles leave most of
-the machine idle over a long K (gemm.mfma split over K, then gemm.combine).
+gemm.cols, gemm.narrow): a few rows (a vector times a matrix, a small batch
+of rows) or a few columns (a matrix times a vector; up to 8 columns over
+many rows, one wave holding 1, 2 or 4 rows; 7 to 32 columns over 1024 rows
+or more on 16x16x4 MFMA blocks, split over K); and matmuls whose tiles leave
+most of the machine idle over a long K (gemm.mfma split over K, then
+gemm.combine).
 
 Bars: bit for bit on integer data (every partial sum exact, whatever the
 order); on real data within the accumulation bound (K - 1) u sum |a b| per
@@ -65,7 +67,28 @@ CASES = {
         ["gemm.cols"]),
     "eight columns over many rows": (
         ([2048, 700], [700, 8]), lambda a, b: porch.matmul(a, b) * 0.5 + 1.0, lambda a, b: a @ b,
-        lambda p: p * 0.5 + 1.0, ["gemm.cols"]),
+        lambda p: p * 0.5 + 1.0, ["gemm.narrow", "gemm.combine"]),
+    "seven columns over many rows, A transposed": (
+        ([700, 2048], [700, 7]), lambda a, b: porch.matmul(porch.transpose(a), b), lambda a, b: a.T @ b,
+        lambda p: p, ["gemm.cols"]),
+    "narrow, sixteen columns": (
+        ([4096, 1024], [1024, 16]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.narrow", "gemm.combine"]),
+    "narrow, ragged rows and columns, K tail, relu": (
+        ([1100, 1036], [1036, 20]), lambda a, b: porch.relu(porch.matmul(a, b) - 2.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p - 2.0, 0.0), ["gemm.narrow", "gemm.combine"]),
+    "narrow, one chunk, epilogue in the kernel": (
+        ([2048, 256], [256, 32]), lambda a, b: porch.matmul(a, b) * 0.5 + 1.0, lambda a, b: a @ b,
+        lambda p: p * 0.5 + 1.0, ["gemm.narrow"]),
+    "narrow, batched, ragged row tiles": (
+        ([3, 700, 512], [3, 512, 24]), lambda a, b: porch.batched_matmul(a, b) + 1.0, lambda a, b: a @ b,
+        lambda p: p + 1.0, ["gemm.narrow"]),
+    "narrow, batched, split K": (
+        ([2, 600, 2048], [2, 2048, 24]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b,
+        lambda p: p, ["gemm.narrow", "gemm.combine"]),
+    "narrow, transposed B": (
+        ([2048, 516], [12, 516]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+        lambda p: p, ["gemm.narrow", "gemm.combine"]),
     "six columns, batched, ragged row groups": (
         ([2, 1101, 512], [2, 512, 6]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.cols"]),
@@ -166,7 +189,11 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "split K, ragged K, relu epilogue", "split K, transposed A",
                                   "split K, five rows", "split K, eight columns",
                                   "eight columns over many rows", "six columns, batched, ragged row groups",
-                                  "three columns, ragged row pairs, transposed B"])
+                                  "three columns, ragged row pairs, transposed B",
+                                  "seven columns over many rows, A transposed",
+                                  "narrow, ragged rows and columns, K tail, relu",
+                                  "narrow, one chunk, epilogue in the kernel", "narrow, batched, ragged row tiles",
+                                  "narrow, transposed B"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
     xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
@@ -218,3 +245,49 @@ def test_epilogue_reading_an_input_bit_exact(gpu, shape):
     assert _kinds(expr) == BIAS_SHAPES[shape]
     out = gpu.materialize(expr).cpu().reshape(m, n)
     assert np.array_equal(out, host.evaluate(expr).reshape(m, n))
+
+
+@pytest.mark.parametrize("shape, chunks", [
+    ((4096, 4096, 16), 8),   # 128 row tiles of 32: 1024 waves, 8 chunks of 512
+    ((4096, 1024, 16), 4),   # partials at most 1/16 of A: 1024 / (16 x 16) chunks
+    ((1100, 1036, 20), 3),   # 35 row tiles; 1036 / 320 -> 3 chunks of 384 (a multiple of 64)
+    ((2048, 256, 32), 1),    # too short a K to split: the epilogue in the kernel
+])
+def test_narrow_chunks(shape, chunks):
+    m, k, n = shape
+    plan = porch.plan(porch.matmul(placeholder([m, k]), placeholder([k, n])))
+    kinds = [x["kind"] for x in plan["kernels"]]
+    assert kinds == (["gemm.narrow", "gemm.combine"] if chunks > 1 else ["gemm.narrow"])
+    waves = -(-m // 32) * chunks
+    assert plan["kernels"][0]["grid"][0] == -(-waves // 4)
+    assert plan["temps"] == ([chunks * m * n] if chunks > 1 else [])
+
+
+def test_narrow_bounds():
+    # below 7 columns gemm.cols, above 32 or below 1024 rows the MFMA tiles
+    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 6]))) == ["gemm.cols"]
+    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 7])))[0] == "gemm.narrow"
+    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 32])))[0] == "gemm.narrow"
+    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 33])))[0] == "gemm.mfma"
+    assert _kinds(porch.matmul(placeholder([1000, 4096]), placeholder([4096, 16])))[0] == "gemm.mfma"
+    # K not a multiple of 4: A's rows cannot be read as float4s
+    assert _kinds(porch.matmul(placeholder([4096, 1030]), placeholder([1030, 16])))[0] == "gemm.mfma"
+
+
+@pytest.mark.gpu
+def test_narrow_infinities_in_the_k_tail(gpu):
+    """Infinities in the last rows of B (K = 1036: a partial last step of 16,
+    whose lanes past K read the last 4 values and zero both operands): the
+    outputs are inf or NaN exactly where the oracle's are, in any summation
+    order (integer data, zeros in A giving 0 x inf)."""
+    m, k, n = 1100, 1036, 20
+    a, b = _ints([m, k], 31), _ints([k, n], 32)
+    b[k - 1, :] = np.inf
+    b[k - 2, 3] = -np.inf
+    b[k - 5, 7] = np.inf
+    expr = porch.matmul(gpu.tensor([m, k], a), gpu.tensor([k, n], b))
+    assert _kinds(expr) == ["gemm.narrow", "gemm.combine"]
+    out = gpu.materialize(expr).cpu().reshape(m, n)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
+    assert np.isinf(ref).any() and np.isnan(ref).any()
+    assert np.array_equal(out, ref, equal_nan=True)
