@@ -201,7 +201,7 @@ namespace porch::cg {
     // more): one wave per 1, 2 or 4 output rows.
     bool gemm_few_cols(const gemm_request& request);
     kernel_code emit_gemm_few_cols(const gemm_request& request);
-    // Up to 32 columns over 1024 rows or more (A rows contiguous along K):
+    // 7 to 32 columns over 128 rows or more (A rows contiguous along K):
     // one wave per 32 rows and a chunk of K on 16x16x4 MFMA blocks, the
     // chunks' partial products summed by emit_gemm_combine.
     bool gemm_narrow(const gemm_request& request);

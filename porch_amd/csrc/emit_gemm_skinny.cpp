@@ -17,7 +17,7 @@
 //                 each load of B), lanes along K reading A with 128-bit
 //                 loads, n accumulators per row and lane and a butterfly
 //                 per output.
-//   gemm.narrow   up to 32 columns over many rows: one wave per 32 rows and
+//   gemm.narrow   7 to 32 columns over 128 rows or more: one wave per 32 rows and
 //                 a chunk of K, v_mfma_f32_16x16x4f32 blocks fed straight
 //                 from 128-bit loads of A (lane l reads row l % 16, k in
 //                 4 (l / 16) .. +3, one MFMA per k of the four), B read per
@@ -46,7 +46,9 @@ namespace porch::cg {
         // and 19.2 us at 5 and 6 over 4096 rows; at 8 20.4 against 23.1)
         constexpr int64_t narrow_min_cols = 7;
         constexpr int64_t narrow_max_cols = 32;
-        constexpr int64_t narrow_min_rows = 1024; // rows of A over all batch entries
+        // rows of A over all batch entries (at 128 rows of 4096 x 4096 with
+        // 32 columns: 8.7 us against 12.6 for the split MFMA kernel)
+        constexpr int64_t narrow_min_rows = 128;
         constexpr int narrow_depth = 4;           // steps of K whose loads are issued together
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
@@ -118,15 +120,19 @@ namespace porch::cg {
             sh.tiles = (r.m + 16 * sh.rb - 1) / (16 * sh.rb);
             // About four waves per compute unit (measured on [4096, 4096]
             // @ [4096, n], n = 4 .. 32: 20.0-24.1 us with the combine, 19.6-
-            // 27.4 at eight, 21.7-38.1 at sixteen), the partial products
-            // (chunks x m x n) at most 1/16 of A (m x K), chunks a multiple
-            // of the loop's 64 values of K (10 chunks of 416 at n = 24:
-            // 33.7 us, against 19.6 with 8 of 512).
+            // 27.4 at eight, 21.7-38.1 at sixteen); the partial products
+            // (chunks x m x n) at most 1/4 of A (m x K) and at most 32
+            // chunks (on 128 to 1024 rows: 1/16 of A left too few waves,
+            // [256, 4096] @ [4096, 32] 17.9 us against 8.7, and 64 chunks
+            // made the combine dear, 4.9 us at [512, 4096] @ [4096, 16]);
+            // chunks a multiple of the loop's 64 values of K (10 chunks of
+            // 416 at n = 24: 33.7 us, against 19.6 with 8 of 512).
             const int64_t waves = 4 * std::max(r.compute_units, 8);
             const int64_t batch_k = 16 * narrow_depth;
             int64_t chunks = (waves + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
-            chunks = std::min(chunks, std::max<int64_t>(1, r.k / (16 * r.n)));
+            chunks = std::min(chunks, std::max<int64_t>(1, r.k / (4 * r.n)));
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / batch_k));
+            chunks = std::min<int64_t>(chunks, 32);
             int64_t chunk = (r.k + chunks - 1) / chunks;
             chunk = (chunk + batch_k - 1) / batch_k * batch_k;
             sh.chunks = (r.k + chunk - 1) / chunk;

@@ -1,7 +1,7 @@
 """Matmuls with one short side (kernel kinds gemm.rows, gemm.combine,
 gemm.cols, gemm.narrow): a few rows (a vector times a matrix, a small batch
 of rows) or a few columns (a matrix times a vector; up to 8 columns over
-many rows, one wave holding 1, 2 or 4 rows; 7 to 32 columns over 1024 rows
+many rows, one wave holding 1, 2 or 4 rows; 7 to 32 columns over 128 rows
 or more on 16x16x4 MFMA blocks, split over K); and matmuls whose tiles leave
 most of the machine idle over a long K (gemm.mfma split over K, then
 gemm.combine).
@@ -78,10 +78,10 @@ CASES = {
         ([1100, 1036], [1036, 20]), lambda a, b: porch.relu(porch.matmul(a, b) - 2.0), lambda a, b: a @ b,
         lambda p: np.maximum(p - 2.0, 0.0), ["gemm.narrow", "gemm.combine"]),
     "narrow, one chunk, epilogue in the kernel": (
-        ([2048, 256], [256, 32]), lambda a, b: porch.matmul(a, b) * 0.5 + 1.0, lambda a, b: a @ b,
+        ([2048, 120], [120, 32]), lambda a, b: porch.matmul(a, b) * 0.5 + 1.0, lambda a, b: a @ b,
         lambda p: p * 0.5 + 1.0, ["gemm.narrow"]),
     "narrow, batched, ragged row tiles": (
-        ([3, 700, 512], [3, 512, 24]), lambda a, b: porch.batched_matmul(a, b) + 1.0, lambda a, b: a @ b,
+        ([3, 700, 96], [3, 96, 24]), lambda a, b: porch.batched_matmul(a, b) + 1.0, lambda a, b: a @ b,
         lambda p: p + 1.0, ["gemm.narrow"]),
     "narrow, batched, split K": (
         ([2, 600, 2048], [2, 2048, 24]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b,
@@ -111,7 +111,7 @@ CASES = {
         ([5, 1030], [1030, 200]), lambda a, b: porch.matmul(a, b) * 2.0, lambda a, b: a @ b, lambda p: p * 2.0,
         ["gemm.mfma", "gemm.combine"]),
     "split K, eight columns": (
-        ([600, 1024], [1024, 8]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ([100, 1024], [1024, 8]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.mfma", "gemm.combine"]),
     "vector times a narrow matrix": (
         ([1, 4096], [4096, 100]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
@@ -249,9 +249,11 @@ def test_epilogue_reading_an_input_bit_exact(gpu, shape):
 
 @pytest.mark.parametrize("shape, chunks", [
     ((4096, 4096, 16), 8),   # 128 row tiles of 32: 1024 waves, 8 chunks of 512
-    ((4096, 1024, 16), 4),   # partials at most 1/16 of A: 1024 / (16 x 16) chunks
-    ((1100, 1036, 20), 3),   # 35 row tiles; 1036 / 320 -> 3 chunks of 384 (a multiple of 64)
-    ((2048, 256, 32), 1),    # too short a K to split: the epilogue in the kernel
+    ((1100, 1036, 20), 9),   # 35 row tiles: 30 chunks for the waves, 12 for partials at most 1/4
+                             # of A, of 87 -> 128 values of K (a multiple of 64): 9 chunks
+    ((2048, 256, 32), 2),    # partials at most 1/4 of A: 256 / (4 x 32) chunks
+    ((512, 4096, 16), 32),   # 16 row tiles: 64 chunks for the waves, at most 32
+    ((2048, 120, 32), 1),    # too short a K to split: the epilogue in the kernel
 ])
 def test_narrow_chunks(shape, chunks):
     m, k, n = shape
@@ -264,12 +266,13 @@ def test_narrow_chunks(shape, chunks):
 
 
 def test_narrow_bounds():
-    # below 7 columns gemm.cols, above 32 or below 1024 rows the MFMA tiles
+    # below 7 columns gemm.cols, above 32 or below 128 rows the MFMA tiles
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 6]))) == ["gemm.cols"]
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 7])))[0] == "gemm.narrow"
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 32])))[0] == "gemm.narrow"
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 33])))[0] == "gemm.mfma"
-    assert _kinds(porch.matmul(placeholder([1000, 4096]), placeholder([4096, 16])))[0] == "gemm.mfma"
+    assert _kinds(porch.matmul(placeholder([128, 4096]), placeholder([4096, 16])))[0] == "gemm.narrow"
+    assert _kinds(porch.matmul(placeholder([127, 4096]), placeholder([4096, 16])))[0] == "gemm.mfma"
     # K not a multiple of 4: A's rows cannot be read as float4s
     assert _kinds(porch.matmul(placeholder([4096, 1030]), placeholder([1030, 16])))[0] == "gemm.mfma"
 
