@@ -31,9 +31,11 @@
 //   gemm.cols        long operand once;
 //   gemm.narrow      7 to 32 columns over many rows: v_mfma_f32_16x16x4f32
 //                    blocks fed straight from 128-bit loads of A;
+//   gemm.wide        8 to 32 (64) rows over many columns: the same blocks
+//                    fed from 128-bit loads of B;
 //   gemm.combine     the sum of K-chunk partial products (gemm.rows,
-//                    gemm.narrow, or the MFMA kernel split over K), with the
-//                    epilogue.
+//                    gemm.narrow, gemm.wide, or the MFMA kernel split over
+//                    K), with the epilogue.
 
 #include "lower.hpp"
 
@@ -207,5 +209,12 @@ namespace porch::cg {
     bool gemm_narrow(const gemm_request& request);
     int64_t gemm_narrow_chunks(const gemm_request& request);
     kernel_code emit_gemm_narrow(const gemm_request& request);
+    // 8 to 32 rows over 256 columns or more (B rows contiguous along N; up
+    // to 64 where the chunks fill four waves per compute unit):
+    // one wave per 64 columns and a chunk of K on 16x16x4 MFMA blocks, the
+    // chunks' partial products summed by emit_gemm_combine.
+    bool gemm_wide(const gemm_request& request);
+    int64_t gemm_wide_chunks(const gemm_request& request);
+    kernel_code emit_gemm_wide(const gemm_request& request);
 
 } // namespace porch::cg

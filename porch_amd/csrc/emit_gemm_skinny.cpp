@@ -23,6 +23,11 @@
 //                 4 (l / 16) .. +3, one MFMA per k of the four), B read per
 //                 lane from the L2; partial products of the chunks summed by
 //                 gemm.combine.
+//   gemm.wide     the same blocks the other way round, few rows (up to 64)
+//                 over many columns: one wave per 64 columns and a chunk of
+//                 K, lane l reading B's row k = l / 16 at columns 4 (l % 16)
+//                 .. + 3 with one 128-bit load, so that MFMA e covers the
+//                 16 columns 4 (l % 16) + e; A read per lane from the L2.
 //
 // Sums run in other orders than the reference's sequential K loop, within
 // the matmul's tolerance (an accumulation-bound per element).
@@ -30,6 +35,7 @@
 #include "emit_gemm.hpp"
 
 #include <algorithm>
+#include <functional>
 #include <stdexcept>
 
 namespace porch::cg {
@@ -50,6 +56,15 @@ namespace porch::cg {
         // 32 columns: 8.7 us against 12.6 for the split MFMA kernel)
         constexpr int64_t narrow_min_rows = 128;
         constexpr int narrow_depth = 4;           // steps of K whose loads are issued together
+        // gemm.wide from 8 rows (gemm.rows: 19.0 against 22.0 us at 4 rows
+        // of [4096, 4096], 24.0 against 22.4 at 8) to 64 (42.8 against 47.6
+        // us for the split MFMA kernel; the MFMAs, 4 per row block and
+        // 128-bit load of B, take over from there)
+        constexpr int64_t wide_min_rows = 8;
+        constexpr int64_t wide_max_rows = 64;
+        // steps of 4 values of K whose loads are issued together (16
+        // measured no faster, 2 to 7 % slower from 24 rows)
+        constexpr int wide_depth = 8;
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
 
@@ -138,6 +153,69 @@ namespace porch::cg {
             sh.chunks = (r.k + chunk - 1) / chunk;
             sh.chunk = chunk;
             return sh;
+        }
+
+        struct wide_shape {
+            int64_t rb = 0;     // 16-row MFMA blocks
+            int64_t tiles = 0;  // 64-column tiles per batch entry
+            int64_t chunks = 0; // K chunks
+            int64_t chunk = 0;  // K per chunk, a multiple of 4 wide_depth
+        };
+
+        wide_shape wide_plan(const gemm_request& r) {
+            wide_shape sh;
+            if (r.m < wide_min_rows || r.m > wide_max_rows || r.n < 256 || !b_vector(r) || !big_enough(r)) return sh;
+            sh.rb = (r.m + 15) / 16;
+            sh.tiles = (r.n + 63) / 64;
+            // About four waves per compute unit (two or eight: 6-60 % and
+            // 4-13 % slower on [m, 4096] @ [4096, 4096]), partials (chunks x
+            // m x n) at most 1/4 of B (K x n), at most 32 chunks.
+            const int64_t waves = 4 * std::max(r.compute_units, 8);
+            const int64_t batch_k = 4 * wide_depth;
+            int64_t chunks = (waves + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
+            chunks = std::min(chunks, std::max<int64_t>(1, r.k / (4 * r.m)));
+            chunks = std::min(chunks, std::max<int64_t>(1, r.k / batch_k));
+            chunks = std::min<int64_t>(chunks, 32);
+            int64_t chunk = (r.k + chunks - 1) / chunks;
+            chunk = (chunk + batch_k - 1) / batch_k * batch_k;
+            sh.chunks = (r.k + chunk - 1) / chunk;
+            sh.chunk = chunk;
+            // Over 32 rows a wave's 3 or 4 row blocks of MFMAs are long: only
+            // with the full four waves per CU ([48, 2048] @ [2048, 2048] in
+            // 320 waves: 28.9 us against 19.9 for the split MFMA kernel).
+            if (r.m > 32 && r.batch * sh.tiles * sh.chunks < waves) return wide_shape{};
+            return sh;
+        }
+
+        // Emitted code, at indent `ind`, for operand register set `set`
+        // (names suffixed with it) holding D steps.
+        using set_text = std::function<std::string(const std::string& set, int D, const std::string& ind)>;
+        // ... loading D steps from K offset `kbase` (`tail`: the last,
+        // partial step, lanes past K zeroing both operands).
+        using load_text = std::function<std::string(const std::string& set, int D, bool tail, const std::string& kbase,
+                                                    const std::string& ind)>;
+
+        // The K loop of gemm.narrow and gemm.wide over [k0, k1): batches of
+        // D steps of `step_k` values, each batch's loads issued together
+        // ahead of its MFMAs; then single steps (`singles`) and a partial
+        // last step (`tail`).  sched_barrier keeps the loads ahead: left to
+        // itself the scheduler sinks each load to its MFMA and waits there.
+        // (Software-pipelining the batches over two register sets, the next
+        // batch's loads issued before this batch's MFMAs, was no faster.)
+        std::string batched_k_loop(int D, int64_t step_k, bool singles, bool tail, const set_text& declare,
+                                   const load_text& loads, const set_text& mfmas) {
+            const std::string in2 = "        ";
+            auto batch = [&](int d, bool t) {
+                return declare("R", d, in2) + loads("R", d, t, "kk", in2) + in2 + "__builtin_amdgcn_sched_barrier(0);\n" +
+                       mfmas("R", d, in2);
+            };
+            const std::string S = std::to_string(step_k * D);
+            const std::string one = std::to_string(step_k);
+            std::string s = "    idx_t kk = k0;\n";
+            s += "    for (; kk + " + S + " <= k1; kk += " + S + ") {\n" + batch(D, false) + "    }\n";
+            if (singles) s += "    for (; kk + " + one + " <= k1; kk += " + one + ") {\n" + batch(1, false) + "    }\n";
+            if (tail) s += "    if (kk < k1) {\n" + batch(1, true) + "    }\n";
+            return s;
         }
 
     } // namespace
@@ -414,19 +492,24 @@ namespace porch::cg {
         s += "        const idx_t q1 = j * 16 + li;\n";
         s += "        qc[j] = q1 < " + N + " ? q1 : (idx_t)" + std::to_string(r.n - 1) + ";\n";
         s += "    }\n";
-        // One step of 16 values of K: lane l holds k = kq + e, kq = kk +
+        // One step of 16 values of K: lane l holds k = kq + e, kq = kbase +
         // 4 (l / 16), of its A row and B column; MFMA e takes value e of
-        // every lane.  The loads of D steps are issued before their MFMAs.
-        // `tail`: the last, partial step of K, where k past it is read at
-        // its last 4 values and both operands are zeroed (zeroing one would
-        // turn an infinity in the other into NaN).
-        auto steps = [&](int D, bool tail, const std::string& ind) {
-            std::string t;
+        // every lane.  In the tail, k past K is read at its last 4 values
+        // and both operands are zeroed (zeroing one would turn an infinity
+        // in the other into NaN).
+        const std::string aslot = "a" + std::to_string(r.a.slot);
+        const std::string bslot = "a" + std::to_string(r.b.slot);
+        const set_text declare = [&](const std::string& set, int D, const std::string& ind) {
             const std::string Ds = std::to_string(D);
-            t += ind + "porch_v4f av[" + Ds + "][" + RB + "];\n";
-            t += ind + "float bv[" + Ds + "][" + NB + "][4];\n";
-            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + Ds + "; ++d) {\n";
-            t += ind + "    const idx_t kq = kk + d * 16 + lg * 4;\n";
+            return ind + "porch_v4f av" + set + "[" + Ds + "][" + RB + "];\n" + ind + "float bv" + set + "[" + Ds + "][" +
+                   NB + "][4];\n";
+        };
+        const load_text loads = [&](const std::string& set, int D, bool tail, const std::string& kbase,
+                                    const std::string& ind) {
+            std::string t;
+            const std::string av = "av" + set, bv = "bv" + set;
+            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d) {\n";
+            t += ind + "    const idx_t kq = " + kbase + " + d * 16 + lg * 4;\n";
             if (tail) {
                 t += ind + "    const bool kin = kq < k1;\n";
                 t += ind + "    const idx_t kr = kin ? kq : k1 - 4;\n";
@@ -434,34 +517,31 @@ namespace porch::cg {
             const std::string kr = tail ? "kr" : "kq";
             t += ind + "    #pragma unroll\n" + ind + "    for (int i = 0; i < " + RB + "; ++i) {\n";
             t += ind + "        const idx_t q0 = qa[i];\n";
-            t += ind + "        av[d][i] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a" +
-                 std::to_string(r.a.slot) + " + " + operand_index(r.a, "q0", kr, batch) + "));\n";
-            if (tail) t += ind + "        if (!kin) av[d][i] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+            t += ind + "        " + av + "[d][i] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + aslot +
+                 " + " + operand_index(r.a, "q0", kr, batch) + "));\n";
+            if (tail) t += ind + "        if (!kin) " + av + "[d][i] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
             t += ind + "    }\n";
             t += ind + "    #pragma unroll\n" + ind + "    for (int j = 0; j < " + NB + "; ++j) {\n";
             t += ind + "        const idx_t q1 = qc[j];\n";
             t += ind + "        #pragma unroll\n" + ind + "        for (int e = 0; e < 4; ++e) {\n";
-            t += ind + "            bv[d][j][e] = a" + std::to_string(r.b.slot) + "[" +
-                 operand_index(r.b, kr + " + e", "q1", batch) + "];\n";
-            if (tail) t += ind + "            if (!kin) bv[d][j][e] = 0.0f;\n";
+            t += ind + "            " + bv + "[d][j][e] = " + bslot + "[" + operand_index(r.b, kr + " + e", "q1", batch) +
+                 "];\n";
+            if (tail) t += ind + "            if (!kin) " + bv + "[d][j][e] = 0.0f;\n";
             t += ind + "        }\n" + ind + "    }\n" + ind + "}\n";
-            // left to itself the scheduler sinks each load to its MFMA,
-            // waiting for it there
-            t += ind + "__builtin_amdgcn_sched_barrier(0);\n";
-            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + Ds + "; ++d)\n";
+            return t;
+        };
+        const set_text mfmas = [&](const std::string& set, int D, const std::string& ind) {
+            std::string t;
+            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d)\n";
             t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
             t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
             t += ind + "            #pragma unroll\n" + ind + "            for (int j = 0; j < " + NB + "; ++j)\n";
-            t += ind + "                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[d][i][e], bv[d][j][e], acc[i][j], 0, 0, 0);\n";
+            t += ind + "                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[d][i][e], bv" + set +
+                 "[d][j][e], acc[i][j], 0, 0, 0);\n";
             return t;
         };
-        const int D = narrow_depth;
-        s += "    idx_t kk = k0;\n";
-        s += "    for (; kk + " + std::to_string(16 * D) + " <= k1; kk += " + std::to_string(16 * D) + ") {\n" +
-             steps(D, false, "        ") + "    }\n";
-        if (sh.chunk % (16 * D) != 0 || r.k % (16 * D) != 0)
-            s += "    for (; kk + 16 <= k1; kk += 16) {\n" + steps(1, false, "        ") + "    }\n";
-        if (r.k % 16 != 0) s += "    if (kk < k1) {\n" + steps(1, true, "        ") + "    }\n";
+        s += batched_k_loop(narrow_depth, 16, sh.chunk % (16 * narrow_depth) != 0 || r.k % (16 * narrow_depth) != 0,
+                            r.k % 16 != 0, declare, loads, mfmas);
         // accumulator value v of lane l: row 4 (l / 16) + v, column l % 16
         s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
         s += "        #pragma unroll\n        for (int j = 0; j < " + NB + "; ++j)\n";
@@ -476,6 +556,116 @@ namespace porch::cg {
         }
         else {
             s += "                    out[ks * " + std::to_string(r.batch * r.m * r.n) + " + " + o + "] = acc[i][j][v];\n";
+        }
+        s += "                }\n            }\n}\n";
+        return kc;
+    }
+
+    bool gemm_wide(const gemm_request& r) { return wide_plan(r).rb > 0; }
+
+    int64_t gemm_wide_chunks(const gemm_request& r) { return wide_plan(r).chunks; }
+
+    kernel_code emit_gemm_wide(const gemm_request& r) {
+        const wide_shape sh = wide_plan(r);
+        if (sh.rb == 0) throw std::logic_error("emit_gemm_wide: not a wide product");
+        const bool final = sh.chunks == 1;
+        const char* T = r.width.type();
+        const std::string batch = r.batched ? "qb" : "";
+        const std::string M = std::to_string(r.m);
+        const std::string N = std::to_string(r.n);
+        const std::string K = std::to_string(r.k);
+        const std::string RB = std::to_string(sh.rb);
+        const int64_t tiles = r.batch * sh.tiles;
+        const int64_t waves = tiles * sh.chunks;
+
+        kernel_code kc;
+        kc.kind = "gemm.wide";
+        kc.name = "porch_gemm";
+        kc.n_slots = r.n_slots;
+        kc.block = 256;
+        kc.grid_x = static_cast<unsigned>((waves + 3) / 4);
+
+        std::string& s = kc.source;
+        s = kernel_prologue(r.n_slots, T);
+        s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" + kernel_params(r.n_slots) + ") {\n";
+        s += "    const int lane = threadIdx.x & 63;\n";
+        s += "    const int li = lane & 15;\n    const int lg = lane >> 4;\n";
+        // waves of one chunk are adjacent: they share its columns of A
+        s += "    const idx_t wid = (idx_t)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
+        s += "    if (wid >= " + std::to_string(waves) + ") return;\n";
+        s += "    const idx_t ks = wid / " + std::to_string(tiles) + ";\n";
+        s += "    const idx_t tile = wid % " + std::to_string(tiles) + ";\n";
+        s += "    const idx_t qb = tile / " + std::to_string(sh.tiles) + ";\n";
+        if (!r.batched) s += "    (void)qb;\n";
+        s += "    const idx_t c0 = (tile % " + std::to_string(sh.tiles) + ") * 64;\n";
+        s += "    const idx_t k0 = ks * " + std::to_string(sh.chunk) + ";\n";
+        s += "    const idx_t k1 = k0 + " + std::to_string(sh.chunk) + " < " + K + " ? k0 + " +
+             std::to_string(sh.chunk) + " : (idx_t)" + K + ";\n";
+        // acc[i][e]: rows 16 i + 4 (l / 16) + v, column c0 + 4 (l % 16) + e
+        s += "    porch_v4f acc[" + RB + "][4];\n";
+        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
+        s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) acc[i][e] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+        // Rows past m are read at m - 1 and columns past n at n - 4: they
+        // feed only outputs that are not stored.
+        s += "    idx_t qa[" + RB + "];\n";
+        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i) {\n";
+        s += "        const idx_t q0 = i * 16 + li;\n";
+        s += "        qa[i] = q0 < " + M + " ? q0 : (idx_t)" + std::to_string(r.m - 1) + ";\n";
+        s += "    }\n";
+        s += "    const idx_t qc = c0 + li * 4 < " + N + " ? c0 + li * 4 : (idx_t)" + std::to_string(r.n - 4) + ";\n";
+        // One step: 4 values of K, lane l holding k = kbase + l / 16.  In
+        // the tail, lanes past K read its last value and zero both
+        // operands.
+        const std::string aslot = "a" + std::to_string(r.a.slot);
+        const std::string bslot = "a" + std::to_string(r.b.slot);
+        const set_text declare = [&](const std::string& set, int D, const std::string& ind) {
+            const std::string Ds = std::to_string(D);
+            return ind + "porch_v4f bv" + set + "[" + Ds + "];\n" + ind + "float av" + set + "[" + Ds + "][" + RB + "];\n";
+        };
+        const load_text loads = [&](const std::string& set, int D, bool tail, const std::string& kbase,
+                                    const std::string& ind) {
+            std::string t;
+            const std::string av = "av" + set, bv = "bv" + set;
+            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d) {\n";
+            t += ind + "    const idx_t kq = " + kbase + " + d * 4 + lg;\n";
+            if (tail) {
+                t += ind + "    const bool kin = kq < k1;\n";
+                t += ind + "    const idx_t kr = kin ? kq : k1 - 1;\n";
+            }
+            const std::string kr = tail ? "kr" : "kq";
+            t += ind + "    " + bv + "[d] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                 operand_index(r.b, kr, "qc", batch) + "));\n";
+            if (tail) t += ind + "    if (!kin) " + bv + "[d] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+            t += ind + "    #pragma unroll\n" + ind + "    for (int i = 0; i < " + RB + "; ++i) {\n";
+            t += ind + "        const idx_t q0 = qa[i];\n";
+            t += ind + "        " + av + "[d][i] = " + aslot + "[" + operand_index(r.a, "q0", kr, batch) + "];\n";
+            if (tail) t += ind + "        if (!kin) " + av + "[d][i] = 0.0f;\n";
+            t += ind + "    }\n" + ind + "}\n";
+            return t;
+        };
+        const set_text mfmas = [&](const std::string& set, int D, const std::string& ind) {
+            std::string t;
+            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d)\n";
+            t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
+            t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
+            t += ind + "            acc[i][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[d][i], bv" + set +
+                 "[d][e], acc[i][e], 0, 0, 0);\n";
+            return t;
+        };
+        s += batched_k_loop(wide_depth, 4, r.k % (4 * wide_depth) != 0, r.k % 4 != 0, declare, loads, mfmas);
+        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
+        s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e)\n";
+        s += "            #pragma unroll\n            for (int v = 0; v < 4; ++v) {\n";
+        s += "                const idx_t q0 = i * 16 + lg * 4 + v;\n";
+        s += "                const idx_t q1 = c0 + li * 4 + e;\n";
+        s += "                if (q0 < " + M + " && q1 < " + N + ") {\n";
+        const std::string o = std::string(r.batched ? "(qb * " + M + " + q0)" : "q0") + " * " + N + " + q1";
+        if (final) {
+            s += "                    const float acc_v = acc[i][e][v];\n";
+            s += epilogue_store(r, "acc_v", o, "                    ");
+        }
+        else {
+            s += "                    out[ks * " + std::to_string(r.batch * r.m * r.n) + " + " + o + "] = acc[i][e][v];\n";
         }
         s += "                }\n            }\n}\n";
         return kc;

@@ -274,6 +274,20 @@ namespace porch::plan {
                 r.n_slots = n_slots();
                 r.width = width;
                 r.compute_units = compute_units;
+                if (cg::gemm_wide(r)) {
+                    const int64_t chunks = cg::gemm_wide_chunks(r);
+                    if (chunks == 1) {
+                        add_step(cg::emit_gemm_wide(r), dest);
+                        return true;
+                    }
+                    const int t = static_cast<int>(plan.temp_elems.size());
+                    plan.temp_elems.push_back(chunks * r.batch * r.m * r.n);
+                    add_step(cg::emit_gemm_wide(r), {arg_ref::kind::temp, t});
+                    cg::gemm_request c = r;
+                    c.n_slots = n_slots();
+                    add_step(cg::emit_gemm_combine(c, chunks, g.n_inputs + t), dest);
+                    return true;
+                }
                 if (cg::gemm_few_rows(r)) {
                     // A few rows: chunks of K in parallel, their partial
                     // products summed by a second kernel (none with one chunk).

@@ -1,6 +1,7 @@
 """Matmuls with one short side (kernel kinds gemm.rows, gemm.combine,
-gemm.cols, gemm.narrow): a few rows (a vector times a matrix, a small batch
-of rows) or a few columns (a matrix times a vector; up to 8 columns over
+gemm.cols, gemm.narrow, gemm.wide): a few rows (a vector times a matrix, a
+small batch of rows; 8 to 64 rows over 256 columns or more on 16x16x4 MFMA
+blocks, split over K) or a few columns (a matrix times a vector; up to 8 columns over
 many rows, one wave holding 1, 2 or 4 rows; 7 to 32 columns over 128 rows
 or more on 16x16x4 MFMA blocks, split over K); and matmuls whose tiles leave
 most of the machine idle over a long K (gemm.mfma split over K, then
@@ -46,7 +47,25 @@ CASES = {
         ["gemm.rows", "gemm.combine"]),
     "eight rows, relu epilogue": (
         ([8, 2048], [2048, 1024]), lambda a, b: porch.relu(porch.matmul(a, b) - 1.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p - 1.0, 0.0), ["gemm.wide", "gemm.combine"]),
+    "seven rows, relu epilogue": (
+        ([7, 2048], [2048, 1024]), lambda a, b: porch.relu(porch.matmul(a, b) - 1.0), lambda a, b: a @ b,
         lambda p: np.maximum(p - 1.0, 0.0), ["gemm.rows", "gemm.combine"]),
+    "wide, thirty-two rows": (
+        ([32, 1024], [1024, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.wide", "gemm.combine"]),
+    "wide, ragged rows and columns, K tail, relu": (
+        ([20, 203], [203, 300]), lambda a, b: porch.relu(porch.matmul(a, b) + 1.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p + 1.0, 0.0), ["gemm.wide", "gemm.combine"]),
+    "wide, one chunk, epilogue in the kernel": (
+        ([32, 100], [100, 256]), lambda a, b: porch.matmul(a, b) * 0.5 - 1.0, lambda a, b: a @ b,
+        lambda p: p * 0.5 - 1.0, ["gemm.wide"]),
+    "wide, batched": (
+        ([2, 24, 516], [2, 516, 512]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.wide", "gemm.combine"]),
+    "wide, transposed A": (
+        ([300, 32], [300, 1024]), lambda a, b: porch.matmul(porch.transpose(a), b), lambda a, b: a.T @ b,
+        lambda p: p, ["gemm.wide", "gemm.combine"]),
     "rows, ragged columns": (
         ([3, 777], [777, 1003]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.rows", "gemm.combine"]),
@@ -99,7 +118,7 @@ CASES = {
         ([1024, 2000], [1024, 2]), lambda a, b: porch.matmul(porch.transpose(a), b), lambda a, b: a.T @ b,
         lambda p: p, ["gemm.cols"]),
     "split K": (
-        ([64, 4096], [4096, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ([96, 4096], [4096, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.mfma", "gemm.combine"]),
     "split K, ragged K, relu epilogue": (
         ([40, 1030], [1030, 200]), lambda a, b: porch.relu(porch.matmul(a, b) + 1.0), lambda a, b: a @ b,
@@ -131,13 +150,13 @@ def test_short_sided_products_take_the_skinny_kernels(name):
 
 
 def test_wide_products_keep_mfma():
-    assert _kinds(porch.matmul(placeholder([64, 512]), placeholder([512, 1024]))) == ["gemm.mfma"]  # short K
+    assert _kinds(porch.matmul(placeholder([96, 512]), placeholder([512, 1024]))) == ["gemm.mfma"]  # short K
     assert _kinds(porch.matmul(placeholder([1024, 4096]), placeholder([4096, 2048]))) == ["gemm.mfma"]  # many tiles
     assert _kinds(porch.matmul(placeholder([8, 64]), placeholder([64, 64]))) == ["gemm.scalar"]
 
 
 @pytest.mark.parametrize("shape, chunks", [
-    ((64, 4096, 4096), 16),  # 32 tiles: 16 chunks of 256 give 512 workgroups
+    ((96, 4096, 4096), 16),  # 32 tiles: 16 chunks of 256 give 512 workgroups
     ((40, 1030, 200), 5),    # 65 K-steps, 2 tiles: the largest divisor with 8 steps a chunk
     ((512, 1024, 512), 8),   # 16 tiles: 64 K-steps in 8 chunks
 ])
@@ -154,7 +173,8 @@ def test_split_k_chunks(shape, chunks):
 # the epilogue (the combine where there is one) loads it at the output's
 # coordinates.
 BIAS_SHAPES = {
-    (8, 2048, 1024): ["gemm.rows", "gemm.combine"],
+    (8, 2048, 1024): ["gemm.wide", "gemm.combine"],
+    (4, 2048, 1024): ["gemm.rows", "gemm.combine"],
     (40, 1030, 200): ["gemm.mfma", "gemm.combine"],
     (3000, 300, 2): ["gemm.cols"],
 }
@@ -193,7 +213,8 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "seven columns over many rows, A transposed",
                                   "narrow, ragged rows and columns, K tail, relu",
                                   "narrow, one chunk, epilogue in the kernel", "narrow, batched, ragged row tiles",
-                                  "narrow, transposed B"])
+                                  "narrow, transposed B", "wide, ragged rows and columns, K tail, relu",
+                                  "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
     xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
@@ -290,6 +311,57 @@ def test_narrow_infinities_in_the_k_tail(gpu):
     b[k - 5, 7] = np.inf
     expr = porch.matmul(gpu.tensor([m, k], a), gpu.tensor([k, n], b))
     assert _kinds(expr) == ["gemm.narrow", "gemm.combine"]
+    out = gpu.materialize(expr).cpu().reshape(m, n)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
+    assert np.isinf(ref).any() and np.isnan(ref).any()
+    assert np.array_equal(out, ref, equal_nan=True)
+
+
+@pytest.mark.parametrize("shape, chunks", [
+    ((32, 4096, 4096), 16),  # 64 column tiles: 16 chunks for four waves a CU
+    ((20, 203, 300), 2),     # partials at most 1/4 of B: 203 / (4 x 20) chunks
+    ((8, 8192, 256), 32),    # 4 column tiles: 256 chunks for the waves, at most 32
+    ((32, 100, 256), 1),     # too short a K to split: the epilogue in the kernel
+])
+def test_wide_chunks(shape, chunks):
+    m, k, n = shape
+    plan = porch.plan(porch.matmul(placeholder([m, k]), placeholder([k, n])))
+    kinds = [x["kind"] for x in plan["kernels"]]
+    assert kinds == (["gemm.wide", "gemm.combine"] if chunks > 1 else ["gemm.wide"])
+    waves = -(-n // 64) * chunks
+    assert plan["kernels"][0]["grid"][0] == -(-waves // 4)
+    assert plan["temps"] == ([chunks * m * n] if chunks > 1 else [])
+
+
+def test_wide_bounds():
+    # from 8 to 32 rows over 256 columns or more (64 with enough waves), B's
+    # rows read as float4s
+    assert _kinds(porch.matmul(placeholder([7, 4096]), placeholder([4096, 4096])))[0] == "gemm.rows"
+    assert _kinds(porch.matmul(placeholder([8, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([64, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([65, 4096]), placeholder([4096, 4096])))[0] == "gemm.mfma"
+    # over 32 rows only with four waves per CU (64 tiles x 16 chunks here, 32 x 10 below)
+    assert _kinds(porch.matmul(placeholder([48, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([48, 2048]), placeholder([2048, 2048])))[0] == "gemm.mfma"
+    assert _kinds(porch.matmul(placeholder([64, 512]), placeholder([512, 1024])))[0] == "gemm.mfma"
+    assert _kinds(porch.matmul(placeholder([32, 4096]), placeholder([4096, 252])))[0] == "gemm.mfma"
+    assert _kinds(porch.matmul(placeholder([16, 4096]), placeholder([4096, 254])))[0] == "gemm.mfma"
+    # B transposed: its rows along N are not contiguous
+    assert _kinds(porch.matmul(placeholder([32, 4096]), porch.transpose(placeholder([4096, 4096]))))[0] == "gemm.mfma"
+
+
+@pytest.mark.gpu
+def test_wide_infinities_in_the_k_tail(gpu):
+    """Infinities in the last rows of B (K = 203: a partial last step of 4,
+    whose lanes past K read the last value and zero both operands): inf or
+    NaN exactly where the oracle has them, in any summation order."""
+    m, k, n = 20, 203, 300
+    a, b = _ints([m, k], 41), _ints([k, n], 42)
+    b[k - 1, :] = np.inf
+    b[k - 2, 5] = -np.inf
+    b[k - 3, 9] = np.inf
+    expr = porch.matmul(gpu.tensor([m, k], a), gpu.tensor([k, n], b))
+    assert _kinds(expr) == ["gemm.wide", "gemm.combine"]
     out = gpu.materialize(expr).cpu().reshape(m, n)
     ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
     assert np.isinf(ref).any() and np.isnan(ref).any()
