@@ -192,15 +192,19 @@ def test_fuzz_products_bit_exact(gpu):
 
 def random_lopsided_product(rng, make):
     """A matmul with one short side or few tiles over a long K (the
-    few-row, few-column and split-K kernels), operands as in
+    few-row, few-column, narrow, wide and split-K kernels), operands as in
     random_product, with a random epilogue (a bias row among them)."""
-    form = int(rng.integers(0, 3))
-    if form == 0:    # a few rows: gemm.rows (+ gemm.combine)
+    form = int(rng.integers(0, 5))
+    if form == 0:    # a few rows: gemm.rows or gemm.wide (+ gemm.combine)
         m, k, n = int(rng.integers(1, 17)), int(rng.integers(64, 3000)), int(rng.integers(256, 1200))
     elif form == 1:  # a few columns: gemm.cols
         m, k, n = int(rng.integers(64, 3000)), int(rng.integers(1, 1500)), int(rng.integers(1, 5))
-    else:            # few 128 x 128 tiles over K >= 1024: split over K
+    elif form == 2:  # few 128 x 128 tiles over K >= 1024: split over K
         m, k, n = int(rng.integers(17, 260)), int(rng.integers(1024, 3000)), int(rng.integers(32, 300))
+    elif form == 3:  # 7 to 32 columns, K a multiple of 4: gemm.narrow where A's rows are contiguous
+        m, k, n = int(rng.integers(128, 3000)), 4 * int(rng.integers(1, 700)), int(rng.integers(7, 33))
+    else:            # 8 to 32 rows, N a multiple of 4: gemm.wide where B's rows are contiguous
+        m, k, n = int(rng.integers(8, 33)), int(rng.integers(16, 3000)), 4 * int(rng.integers(64, 300))
 
     def operand(rows, cols):
         f = int(rng.integers(0, 3))
@@ -222,10 +226,10 @@ def random_lopsided_product(rng, make):
 def test_lopsided_products_reach_their_kernels():
     rng = np.random.default_rng(17)
     kinds = set()
-    for _ in range(30):
+    for _ in range(40):
         plan = porch.plan(random_lopsided_product(rng, integer_leaf), compile=True)
         kinds.update(k["kind"] for k in plan["kernels"])
-    assert {"gemm.rows", "gemm.cols", "gemm.combine", "gemm.mfma"} <= kinds
+    assert {"gemm.rows", "gemm.cols", "gemm.narrow", "gemm.wide", "gemm.combine", "gemm.mfma"} <= kinds
 
 
 @pytest.mark.gpu
@@ -238,7 +242,7 @@ def test_fuzz_lopsided_products_bit_exact(gpu):
         return gpu.tensor(shape, values)
 
     kinds = set()
-    for trial in range(30):
+    for trial in range(40):
         expr = random_lopsided_product(rng, device_leaf)
         plan = gpu.plan(expr)
         kinds.update(k["kind"] for k in plan["kernels"])
@@ -247,4 +251,4 @@ def test_fuzz_lopsided_products_bit_exact(gpu):
         assert np.max(np.abs(ref)) < LIMIT
         out = gpu.materialize(expr).cpu().reshape(expr.shape())
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, plan)
-    assert {"gemm.rows", "gemm.cols", "gemm.combine", "gemm.mfma"} <= kinds
+    assert {"gemm.rows", "gemm.cols", "gemm.narrow", "gemm.wide", "gemm.combine", "gemm.mfma"} <= kinds
