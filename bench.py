@@ -16,7 +16,9 @@ over x fp32 [4096, 4096]): HBM GB/s of algorithmic bytes (all of x read, the
 output written).  The other workloads are reported beside it under
 "configs", each with its roofline fraction and JIT latency, followed by three
 workloads of the IR extensions (a batched transpose and a head permute via
-permute, and a batched matmul with an epilogue).  The host
+permute, and a batched matmul with an epilogue) and two products with one
+short side (16 columns, 32 rows: a kernel split over K and its combine,
+timed from the first kernel's start to the second's end).  The host
 evaluator (the oracle, OpenMP) is timed on this machine's cores as the CPU
 baseline.
 
@@ -67,6 +69,10 @@ WORK = {
     "batched_matmul": ("mfma", 2 * 32 * 1024 ** 3),
     "attention_scores": ("mfma", 2 * 16 * 4096 * 64 * 4096),
     "vocab_softmax": ("hbm", 2 * 512 * 262144 * 4),
+    # A and B read once, C written (the partial products between the two
+    # kernels are not algorithmic bytes)
+    "narrow_product": ("hbm", (4096 * 4096 + 4096 * 16 + 4096 * 16) * 4),
+    "wide_product": ("hbm", (32 * 4096 + 4096 * 4096 + 32 * 4096) * 4),
 }
 DESCRIPTION = {
     "elementwise": "(a + b) * 2 - 1, a, b fp32 [1048576]",
@@ -80,13 +86,16 @@ DESCRIPTION = {
     "batched_matmul": "relu(batched_matmul(A, B) + bcast(bias)) - 0.5, A, B fp32 [32,1024,1024]",
     "attention_scores": "batched_matmul(q, k) * 0.125, q fp32 [16,4096,64], k fp32 [16,64,4096]",
     "vocab_softmax": "softmax(x, 1), x fp32 [512,262144]",
+    "narrow_product": "A @ B, A fp32 [4096,4096], B fp32 [4096,16]",
+    "wide_product": "A @ B, A fp32 [32,4096], B fp32 [4096,4096]",
 }
 # Minimum length of each workload's untimed warm-up (see run_config).
 WARM_SECONDS = 0.25
 # Input copies rotated through so that a step never re-reads cached data.
 ROTATION = {"elementwise": 48, "view_chain": 8, "softmax": 4, "logistic_rowsum": 6,
             "matmul_epilogue": 1, "copy": 2, "batched_transpose": 4, "heads_permute": 2,
-            "batched_matmul": 1, "attention_scores": 1, "vocab_softmax": 1}
+            "batched_matmul": 1, "attention_scores": 1, "vocab_softmax": 1, "narrow_product": 8,
+            "wide_product": 8}
 # Counter summaries (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) per workload.
 PROFILES = os.path.join(ROOT, "profiles")
 
@@ -503,7 +512,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--configs", default="elementwise,view_chain,softmax,logistic_rowsum,matmul_epilogue,"
-                                             "batched_transpose,heads_permute,batched_matmul")
+                                             "batched_transpose,heads_permute,batched_matmul,narrow_product,"
+                                             "wide_product")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--jit-probe", default=None, help=argparse.SUPPRESS)
     parser.add_argument("--controls", type=int, default=0, metavar="LAUNCHES",

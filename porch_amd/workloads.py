@@ -81,6 +81,10 @@ def config_inputs(name: str, size: dict | None = None) -> list[np.ndarray]:
         return [synth.uniform(m * k, 501, -1.0, 1.0) / np.float32(64.0),
                 synth.uniform(k * n, 502, -1.0, 1.0) / np.float32(64.0),
                 synth.normal(n, 503, 0.0, 0.01)]
+    if name in ("narrow_product", "wide_product"):
+        m, k, n = s["m"], s["k"], s["n"]
+        seed = 1001 if name == "narrow_product" else 1011
+        return [synth.uniform(m * k, seed, -1.0, 1.0), synth.uniform(k * n, seed + 1, -1.0, 1.0)]
     raise ValueError(name)
 
 
@@ -96,6 +100,9 @@ CONFIG_SIZES = {
     "batched_matmul": {"batch": 32, "m": 1024, "k": 1024, "n": 1024},
     "attention_scores": {"batch": 16, "m": 4096, "k": 64, "n": 4096},
     "vocab_softmax": {"rows": 512, "cols": 262144},
+    # products with one short side: 16 columns (gemm.narrow), 32 rows (gemm.wide)
+    "narrow_product": {"m": 4096, "k": 4096, "n": 16},
+    "wide_product": {"m": 32, "k": 4096, "n": 4096},
 }
 
 
@@ -126,6 +133,8 @@ def config_shapes(name: str, size: dict | None = None) -> list[list[int]]:
         return [[b, m, k], [b, k, n]]
     if name == "vocab_softmax":
         return [[s["rows"], s["cols"]]]
+    if name in ("narrow_product", "wide_product"):
+        return [[s["m"], s["k"]], [s["k"], s["n"]]]
     raise ValueError(name)
 
 
@@ -173,4 +182,7 @@ def config_graph(name: str, tensors, size: dict | None = None):
     if name == "vocab_softmax":
         (x,) = tensors
         return porch.softmax(x, 1)
+    if name in ("narrow_product", "wide_product"):
+        a, b = tensors
+        return porch.matmul(a, b)
     raise ValueError(name)
