@@ -366,3 +366,21 @@ def test_wide_infinities_in_the_k_tail(gpu):
     ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
     assert np.isinf(ref).any() and np.isnan(ref).any()
     assert np.array_equal(out, ref, equal_nan=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind, m, k, n", [("gemm.narrow", 1100, 1036, 20), ("gemm.wide", 20, 203, 300)])
+def test_clamped_edge_rows_and_columns(gpu, kind, m, k, n):
+    """Rows past m and columns past n of the last tiles are read at the last
+    row (column) and feed only outputs that are not stored: a NaN in A's
+    last row and an infinity in B's last column reach exactly the outputs
+    the oracle gives them (integer data, zeros in A giving 0 x inf = NaN)."""
+    a, b = _ints([m, k], 51), _ints([k, n], 52)
+    a[m - 1, 3] = np.nan
+    b[7, n - 1] = np.inf
+    expr = porch.matmul(gpu.tensor([m, k], a), gpu.tensor([k, n], b))
+    assert _kinds(expr)[0] == kind
+    out = gpu.materialize(expr).cpu().reshape(m, n)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
+    assert np.isnan(ref[m - 1]).all() and not np.isnan(ref[: m - 1, : n - 1]).any()
+    assert np.array_equal(out, ref, equal_nan=True)
