@@ -225,7 +225,10 @@ namespace porch::plan {
                 const arg_ref t = ensure_temp(id);
                 cg::gemm_operand op;
                 op.slot = g.n_inputs + t.index;
-                op.offset = 0;
+                // the column softmax's sum sits after its max in their
+                // shared temporary
+                const auto off = offset_of.find(id);
+                op.offset = off != offset_of.end() ? off->second : 0;
                 op.stride_batch = rank == 3 ? shape[1] * shape[2] : 0;
                 op.stride_row = shape[rank - 1];
                 op.stride_col = 1;

@@ -116,6 +116,44 @@ def test_emulated_values(shape, axis, scale):
 
 
 @needs_clang
+@pytest.mark.parametrize("batched", [False, True])
+def test_emulated_sum_read_straight_by_a_product(batched):
+    """The column sum of exp(x - max) shares its temporary with the max
+    (the max first, the sum after it); a product that takes the sum as an
+    operand must read the sum's half.  A plan that read the max instead
+    was off by orders of magnitude."""
+    rng = np.random.default_rng(31 + batched)
+    if batched:
+        xs, ws, axis = [4, 300, 50], [4, 50, 64], 1
+    else:
+        xs, ws, axis = [300, 500], [500, 64], 0
+    x = (rng.standard_normal(int(np.prod(xs))) * 3).astype(np.float32)
+    w = rng.uniform(-1, 1, int(np.prod(ws))).astype(np.float32)
+    tx, tw = placeholder(xs, x), placeholder(ws, w)
+    m = porch.broadcast_to(porch.max(tx, axis, True), xs)
+    s = porch.sum(porch.exp(tx - m), axis, True)
+    if batched:
+        # [4, 1, 50] @ [4, 50, 64]
+        expr = porch.batched_matmul(s, tw)
+    else:
+        expr = porch.matmul(s, tw)
+    kinds = _kinds(expr)
+    assert kinds[0] == "reduce.column_softmax", kinds
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=600))
+    got = emu.evaluate(expr, [x, w], timeout=600).reshape(-1)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+    # float64 restatement: the sums are held to 1e-6 by the kernel, the
+    # product over K <= 500 terms adds K * eps of the absolute terms
+    x64 = x.astype(np.float64).reshape(xs)
+    s64 = np.exp(x64 - x64.max(axis=axis, keepdims=True)).sum(axis=axis, keepdims=True)
+    w64 = w.astype(np.float64).reshape(ws)
+    exact = (s64 @ w64).reshape(-1)
+    bound = (np.abs(s64) @ np.abs(w64)).reshape(-1) * (2e-6 + ws[-2] * 2 ** -24)
+    assert np.all(np.abs(got - exact) <= bound), np.max(np.abs(got - exact) / bound)
+    assert np.all(np.abs(ref - exact) <= bound)
+
+
+@needs_clang
 @pytest.mark.parametrize("rows", [300, 20000])
 def test_emulated_softmax_of_an_expression(rows):
     # the folded values computed per row (temporaries named by the emitter
