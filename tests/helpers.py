@@ -168,3 +168,79 @@ def assert_softmax_close(out, t, values, rel=1e-6):
     bar = np.broadcast_to((rel + drift)[:, None], shape)
     ok = (rel_err(out[finite], ref[finite]) <= bar[finite]) | (_ulps(out[finite], ref[finite]) <= 2)
     assert ok.all(), ("vs oracle", float(drift.max()), rel_err(out[finite], ref[finite]).max())
+
+
+def check_matmul_epilogue_every_output(out, a, b, bias, m, k, n):
+    """`out` = relu(A @ B + bias) - 0.5 over every one of its m x n outputs,
+    against a float64 GEMM of the same float32 operands (the reference
+    computes every output through its K loop, src/tensor.cpp:684-721):
+
+    1. the product before the epilogue, recovered from the output where
+       relu passed it (out + 0.5 is exact in float64): within the
+       accumulation bound K * eps * sum_k |a_ik| |b_kj| plus the rounding of
+       the final subtraction (half an ulp of 0.5); where relu clamped it
+       (out == -0.5), the exact value is at most that bound above zero;
+    2. the final result within 1e-4 relative, and 5e-6 absolute.
+
+    Returns (max |delta| of the product, max |delta| / bound)."""
+    am = np.asarray(a, np.float32).reshape(m, k).astype(np.float64)
+    bm = np.asarray(b, np.float32).reshape(k, n).astype(np.float64)
+    bias64 = np.asarray(bias, np.float32).reshape(1, n).astype(np.float64)
+    out = np.asarray(out, np.float32).reshape(m, n)
+    assert np.isfinite(out).all()
+    exact_v = am @ bm + bias64
+    bound = k * float(np.finfo(np.float32).eps) * (np.abs(am) @ np.abs(bm)) + np.abs(bias64) * 2.0 ** -23
+    half_ulp = 2.0 ** -25
+    o64 = out.astype(np.float64)
+    passed = o64 > -0.5
+    v = o64 + 0.5
+    delta = np.where(passed, np.abs(v - exact_v), np.maximum(exact_v, 0.0))
+    frac = delta / (bound + half_ulp)
+    assert np.all(frac <= 1.0), (float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
+    assert np.all(o64 >= -0.5)
+    exact = np.maximum(exact_v, 0.0) - 0.5
+    err = np.abs(o64 - exact)
+    rel = err / np.maximum(np.abs(exact), 1e-30)
+    assert rel.max() <= 1e-4, (float(rel.max()), np.unravel_index(rel.argmax(), rel.shape))
+    assert err.max() < 5e-6, float(err.max())
+    return float(delta.max()), float(frac.max())
+
+
+def division_operands(count, seed):
+    """float32 pairs (l, r) for division: edge operands first (signed
+    zeros, infinities, NaN, the smallest and largest denormals and normals,
+    FLT_MAX, quotients that overflow to infinity or underflow into the
+    denormals or to zero, exact quotients), every pairing of a set of
+    specials, then random values of log-uniform magnitude over the whole
+    binary32 range with random signs."""
+    f = np.float32
+    tiny, dmax = f(np.finfo(np.float32).smallest_subnormal), f(np.finfo(np.float32).tiny) - f(np.finfo(np.float32).smallest_subnormal)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, -1.0, 3.0, tiny, -tiny, dmax,
+                         np.finfo(np.float32).tiny, np.finfo(np.float32).max, -np.finfo(np.float32).max,
+                         1e-30, 7e37], np.float32)
+    pl, pr = np.meshgrid(specials, specials, indexing="ij")
+    fixed_l = [f(1e38), f(1e-38), f(3e-39), f(6.0), f(1.0), f(1.0), f(2.0), f(1e-45), f(5e-39)]
+    fixed_r = [f(1e-5), f(1e5), f(7.0), f(3.0), f(3.0), f(0.1), f(3.0 ** 10), f(2.0), f(0.5)]
+    rng = np.random.default_rng(seed)
+    n = max(count - pl.size - len(fixed_l), 0)
+
+    def random_values(k):
+        bits = rng.integers(0, 0xFF, k, dtype=np.uint32) << np.uint32(23)
+        bits |= rng.integers(0, 1 << 23, k, dtype=np.uint32)
+        bits |= rng.integers(0, 2, k, dtype=np.uint32) << np.uint32(31)
+        return bits.view(np.float32)
+
+    lhs = np.concatenate([pl.reshape(-1), np.array(fixed_l, np.float32), random_values(n)])
+    rhs = np.concatenate([pr.reshape(-1), np.array(fixed_r, np.float32), random_values(n)])
+    return lhs[:count].astype(np.float32), rhs[:count].astype(np.float32)
+
+
+def assert_bits_or_both_nan(got, expected):
+    """Bit-for-bit equality, except that any NaN matches any NaN."""
+    got = np.asarray(got, np.float32).reshape(-1)
+    expected = np.asarray(expected, np.float32).reshape(-1)
+    assert got.shape == expected.shape
+    both_nan = np.isnan(got) & np.isnan(expected)
+    bad = (got.view(np.uint32) != expected.view(np.uint32)) & ~both_nan
+    idx = np.flatnonzero(bad)
+    assert idx.size == 0, (idx.size, idx[:6], got[idx[:6]], expected[idx[:6]])

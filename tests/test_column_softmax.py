@@ -246,3 +246,27 @@ def test_random_shapes_and_axes(gpu):
         ok = np.abs(out.astype(np.float64) - ref) <= 1e-6 * np.abs(ref) + 2 * np.spacing(np.abs(ref))
         assert ok.all(), (trial, shape, axis, np.flatnonzero(~ok)[:4], out[~ok][:4], ref[~ok][:4])
     assert {"reduce.column_softmax", "reduce.column_softmax_combine"} <= seen
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batched", [False, True])
+def test_sum_read_straight_by_a_product(gpu, batched):
+    """The column sum of exp(x - max) as a product's operand: the product
+    reads the sum's half of the temporary it shares with the max."""
+    rng = np.random.default_rng(41 + batched)
+    xs, ws, axis = ([4, 3000, 50], [4, 50, 64], 1) if batched else ([3000, 500], [500, 64], 0)
+    x = (rng.standard_normal(int(np.prod(xs))) * 3).astype(np.float32)
+    w = rng.uniform(-1, 1, int(np.prod(ws))).astype(np.float32)
+    tx, tw = gpu.tensor(xs, x), gpu.tensor(ws, w)
+    s = gpu.sum(gpu.exp(tx - gpu.broadcast_to(gpu.max(tx, axis, True), xs)), axis, True)
+    expr = gpu.batched_matmul(s, tw) if batched else gpu.matmul(s, tw)
+    assert _kinds(expr)[0] == "reduce.column_softmax"
+    got = gpu.materialize(expr).cpu().reshape(-1)
+    x64 = x.astype(np.float64).reshape(xs)
+    s64 = np.exp(x64 - x64.max(axis=axis, keepdims=True)).sum(axis=axis, keepdims=True)
+    w64 = w.astype(np.float64).reshape(ws)
+    exact = (s64 @ w64).reshape(-1)
+    bound = (np.abs(s64) @ np.abs(w64)).reshape(-1) * (2e-6 + ws[-2] * 2 ** -24)
+    assert np.all(np.abs(got - exact) <= bound), np.max(np.abs(got - exact) / bound)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+    assert np.all(np.abs(ref - exact) <= bound)

@@ -14,8 +14,8 @@ import pytest
 
 import porch_amd as porch
 from oracle import host
-from tests.helpers import (build, check_kat, config_graph, config_inputs, config_shapes,
-                           kat_cases, kat_input_values, placeholder)
+from tests.helpers import (assert_bits_or_both_nan, build, check_kat, config_graph, config_inputs, config_shapes,
+                           division_operands, kat_cases, kat_input_values, placeholder)
 
 CASES, ERRORS = kat_cases()
 
@@ -212,3 +212,44 @@ def test_maximum_minimum_follow_the_reference_ternary_on_nan():
     # l > r ? l : r  -> any comparison with NaN is false -> r
     assert hi[0] == 2.0 and np.isnan(hi[1]) and hi[2] == 0.0 and not np.signbit(hi[2])
     assert lo[0] == 2.0 and np.isnan(lo[1]) and lo[2] == 0.0 and not np.signbit(lo[2])
+
+
+def _quotients(lhs, rhs):
+    with np.errstate(all="ignore"):
+        return np.divide(lhs, rhs, dtype=np.float32), np.divide(np.float32(1.0), rhs, dtype=np.float32)
+
+
+def test_divide_and_reciprocal_are_ieee_binary32():
+    """l / r and reciprocal(r) = 1.0f / r (src/tensor.cpp:659-667,864)
+    against numpy's correctly rounded binary32 division, bit for bit (NaN
+    as NaN): every pairing of signed zeros, infinities, NaN, denormals,
+    FLT_MAX and FLT_MIN, quotients that overflow and underflow, and random
+    operands over the whole range."""
+    lhs, rhs = division_operands(1 << 16, 5)
+    tl, tr = placeholder([lhs.size], lhs), placeholder([rhs.size], rhs)
+    q, inv = _quotients(lhs, rhs)
+    assert_bits_or_both_nan(host.evaluate(tl / tr), q)
+    assert_bits_or_both_nan(host.evaluate(porch.reciprocal(tr)), inv)
+    # the underflowing and overflowing cases are among them
+    assert np.isinf(q).sum() > 50 and ((q != 0) & (np.abs(q) < np.finfo(np.float32).tiny)).sum() > 50
+    # a divisor broadcast along rows
+    rows = 37
+    l2 = lhs[: rows * 256].reshape(rows, 256)
+    r2 = rhs[-256:].reshape(1, 256)
+    t2 = host.evaluate(placeholder([rows, 256], l2) / porch.broadcast_to(placeholder([1, 256], r2), [rows, 256]))
+    assert_bits_or_both_nan(t2, _quotients(l2, np.broadcast_to(r2, l2.shape))[0])
+
+
+def test_divide_planted_reciprocal_product_is_caught():
+    """The check above rejects a division written as l * (1.0f / r): that
+    differs from l / r in the last bit on many operands."""
+    lhs, rhs = division_operands(1 << 16, 5)
+    q, inv = _quotients(lhs, rhs)
+    with np.errstate(all="ignore"):
+        planted = (lhs * inv).astype(np.float32)
+    with pytest.raises(AssertionError):
+        assert_bits_or_both_nan(planted, q)
+    # and a division that flushes denormal results to zero
+    flushed = np.where(np.abs(q) < np.finfo(np.float32).tiny, np.float32(0.0) * np.sign(q), q).astype(np.float32)
+    with pytest.raises(AssertionError):
+        assert_bits_or_both_nan(flushed, q)
