@@ -1,69 +1,148 @@
-// porch::tensor / porch::tensor_expr — lazy IR recording and
-// materialisation (reference src/tensor.cpp:62-122, 1070-1511).
+// porch::tensor / porch::tensor_expr: lazy IR recording and
+// materialisation, behind the reference's public declarations
+// (include/porch/tensor.hpp; behaviour of src/tensor.cpp:1070-1511).
 //
-// Differences from the reference, all source-compatible:
+// A tensor's state is a layout, a placement and a value cell: device values
+// (with a host copy made on demand), or a recorded graph that produces them
+// on first use.  Differences from the reference, all source-compatible:
 //   * input nodes own a handle to the tensor they read, so an expression
 //     stays valid after the tensors it was built from go out of scope (the
 //     reference stores a raw `const tensor*`, src/tensor.cpp:50);
-//   * a lazy tensor that has already materialised is referenced by its
-//     storage instead of re-inlining (and recomputing) its expression;
-//   * the host mirror is allocated on the first data()/cpu() call, not
-//     zero-filled at every materialisation (src/tensor.cpp:1019,1073-1075).
+//   * once a recorded graph has run, it is dropped (releasing the tensors
+//     it read), and expressions over the tensor read its values instead of
+//     re-inlining and recomputing the graph;
+//   * no host mirror is allocated at materialisation (the reference
+//     zero-fills one each time, src/tensor.cpp:1019,1073-1075): data()
+//     fetches one on first use, and cpu() copies straight from the device
+//     into the vector it returns when no mirror exists;
+//   * indexing restricts the tensor's strided view of its storage one
+//     subscript at a time (integers fix an axis, ranges narrow it).
 
 #include "internal.hpp"
 #include "planner.hpp"
 
 #include "porch/tensor.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <memory>
 #include <mutex>
 #include <optional>
+#include <span>
 #include <stdexcept>
 #include <unordered_map>
 
 namespace porch {
 
-    struct realized_storage {
-        realized_storage(hip_jit::device_buffer buffer, std::vector<float32_t> values,
-                         bool current)
-            : device_values(std::move(buffer)), host(std::move(values)),
-              host_current(current) {}
+    using node_ptr = std::shared_ptr<const tensor_expr::node>;
 
-        hip_jit::device_buffer device_values;
-        std::vector<float32_t> host;
-        bool host_current = false;
-        std::mutex host_mutex;
-    };
+    namespace {
 
-    struct lazy_materialization {
-        explicit lazy_materialization(std::shared_ptr<const tensor_expr::node> e)
-            : expression(std::move(e)) {}
+        // Values resident in device memory.  The host copy is either given
+        // at construction (the values a tensor was built from) or fetched
+        // from the device on first request and kept; a fetched copy is
+        // left uninitialised until the transfer fills it.
+        class resident_values {
+          public:
+            explicit resident_values(hip_jit::device_buffer memory) : memory_(std::move(memory)) {}
+            resident_values(hip_jit::device_buffer memory, std::vector<float32_t> host)
+                : memory_(std::move(memory)), given_(std::move(host)), host_(given_), host_ready_(true) {}
 
-        std::shared_ptr<realized_storage> storage();
+            [[nodiscard]] const hip_jit::device_buffer& memory() const noexcept { return memory_; }
 
-        std::shared_ptr<const tensor_expr::node> expression;
-        std::once_flag once;
-        std::shared_ptr<realized_storage> realized;
-        std::atomic<bool> done{false};
-    };
+            // The first `count` values in host memory.
+            std::span<const float32_t> host(size_t count) {
+                std::scoped_lock hold{fetch_};
+                if (!host_ready_) {
+                    fetched_.reset(new float32_t[count]);
+                    const std::span<float32_t> target{fetched_.get(), count};
+                    hip_jit::copy_to_host(memory_, target);
+                    host_ = target;
+                    host_ready_ = true;
+                }
+                return host_;
+            }
+
+            // The first `count` values as a new vector: from the host copy
+            // if there is one, else transferred straight into the vector
+            // (no host copy is kept).
+            std::vector<float32_t> copy(size_t count) {
+                {
+                    std::scoped_lock hold{fetch_};
+                    if (host_ready_) return {host_.begin(), host_.end()};
+                }
+                std::vector<float32_t> out(count);
+                hip_jit::copy_to_host(memory_, out);
+                return out;
+            }
+
+          private:
+            hip_jit::device_buffer memory_;
+            std::mutex fetch_;
+            std::vector<float32_t> given_;
+            std::unique_ptr<float32_t[]> fetched_;
+            std::span<const float32_t> host_;
+            bool host_ready_ = false;
+        };
+
+        using values_ptr = std::shared_ptr<resident_values>;
+
+        values_ptr run_graph(const node_ptr& root);
+
+        // What a tensor handle stands for: device values, or a recorded
+        // graph that produces them on first use.  The graph runs once,
+        // on whichever thread asks first; a run that throws leaves it
+        // recorded, so the next use runs it again.  Once the values exist
+        // the graph is dropped, releasing the tensors it read.
+        class value_cell {
+          public:
+            explicit value_cell(values_ptr values) : values_(std::move(values)), ready_(true) {}
+            explicit value_cell(node_ptr graph) : graph_(std::move(graph)) {}
+
+            values_ptr get() {
+                if (ready_.load(std::memory_order_acquire)) return values_;
+                std::scoped_lock hold{run_};
+                if (!ready_.load(std::memory_order_relaxed)) {
+                    values_ = run_graph(pending());
+                    ready_.store(true, std::memory_order_release);
+                    std::scoped_lock hold_graph{graph_lock_};
+                    graph_.reset();
+                }
+                return values_;
+            }
+
+            // The recorded graph while its values do not exist yet, else
+            // null.  Never waits for a run in progress.
+            [[nodiscard]] node_ptr pending() const {
+                if (ready_.load(std::memory_order_acquire)) return nullptr;
+                std::scoped_lock hold{graph_lock_};
+                return graph_;
+            }
+
+          private:
+            std::mutex run_;
+            mutable std::mutex graph_lock_;
+            node_ptr graph_;
+            values_ptr values_;
+            std::atomic<bool> ready_{false};
+        };
+
+    } // namespace
 
     struct tensor::state {
         tensor_layout layout;
         device placement;
-        std::shared_ptr<realized_storage> realized;
-        std::shared_ptr<lazy_materialization> lazy;
-        // Strided storage: the values gathered in row-major order, made once
-        // on first data().
-        std::once_flag dense_once;
-        std::shared_ptr<realized_storage> dense;
+        value_cell cell;
+        // Over strided storage: the viewed values gathered into row-major
+        // order on the device, on the first data() call.
+        std::mutex gather_lock;
+        values_ptr gathered;
 
-        state(tensor_layout l, device p) : layout(std::move(l)), placement(p) {}
-
-        [[nodiscard]] std::shared_ptr<realized_storage> storage() const {
-            if (realized != nullptr) return realized;
-            return lazy->storage();
-        }
+        state(tensor_layout l, device p, values_ptr v)
+            : layout(std::move(l)), placement(p), cell(std::move(v)) {}
+        state(tensor_layout l, device p, node_ptr graph)
+            : layout(std::move(l)), placement(p), cell(std::move(graph)) {}
     };
 
     namespace detail {
@@ -105,8 +184,6 @@ namespace porch {
 
     namespace {
 
-        using node_ptr = std::shared_ptr<const tensor_expr::node>;
-
         node_ptr make_node(ir::op kind, node_ptr lhs = nullptr, node_ptr rhs = nullptr) {
             auto n = std::make_shared<tensor_expr::node>();
             n->kind = kind;
@@ -115,24 +192,37 @@ namespace porch {
             return n;
         }
 
-        index_t normalize_index(index_t index, index_t extent) {
-            if (index < 0) index += extent;
-            if (index < 0 || index >= extent)
-                throw std::out_of_range("tensor index is out of bounds");
-            return index;
+        // A strided view of flat storage: the element at coordinates
+        // (c_0, ..., c_{r-1}) sits at `base + sum c_d * step[d]`.
+        struct strided_view {
+            index_t base = 0;
+            std::vector<index_t> extent;
+            std::vector<index_t> step;
+        };
+
+        // Subscripting axis `axis` of `v` with an integer: the coordinate
+        // is fixed (counted from the end when negative) and the axis goes.
+        void fix_axis(strided_view& v, size_t axis, index_t at) {
+            const index_t n = v.extent[axis];
+            const index_t c = at < 0 ? at + n : at;
+            if (c < 0 || c >= n) throw std::out_of_range("tensor index is out of bounds");
+            v.base += c * v.step[axis];
+            v.extent.erase(v.extent.begin() + static_cast<std::ptrdiff_t>(axis));
+            v.step.erase(v.step.begin() + static_cast<std::ptrdiff_t>(axis));
         }
 
-        index_t normalize_slice_endpoint(index_t index, index_t extent) {
-            if (index < 0) index += extent;
-            if (index < 0) return 0;
-            if (index > extent) return extent;
-            return index;
-        }
-
-        size_t slice_length(index_t start, index_t stop, index_t step) {
-            if (step <= 0) throw std::invalid_argument("tensor slice step must be positive");
-            if (stop <= start) return 0;
-            return static_cast<size_t>((stop - start + step - 1) / step);
+        // Subscripting axis `axis` of `v` with a range: each endpoint is
+        // counted from the end when negative and clamped to [0, extent];
+        // the axis keeps every `r.step`-th coordinate from the first.
+        void narrow_axis(strided_view& v, size_t axis, const slice& r) {
+            if (r.step <= 0) throw std::invalid_argument("tensor slice step must be positive");
+            const index_t n = v.extent[axis];
+            const auto endpoint = [n](index_t e) { return std::clamp<index_t>(e < 0 ? e + n : e, 0, n); };
+            const index_t first = endpoint(r.start);
+            const index_t end = endpoint(r.stop);
+            v.base += first * v.step[axis];
+            v.extent[axis] = end > first ? (end - first - 1) / r.step + 1 : 0;
+            v.step[axis] *= r.step;
         }
 
         bool is_contiguous_layout(std::span<const index_t> shape,
@@ -231,16 +321,22 @@ namespace porch {
             }
         };
 
-        tensor make_realized(std::vector<index_t> shape, hip_jit::device_buffer buffer,
-                             std::vector<float32_t> host, bool host_current, device placement) {
-            auto st = std::make_shared<state_t>(tensor_layout{std::move(shape)}, placement);
-            st->realized = std::make_shared<realized_storage>(
-                std::move(buffer), std::move(host), host_current
+        tensor make_tensor(std::vector<index_t> shape, device placement, values_ptr values) {
+            return detail::tensor_access::make(
+                std::make_shared<state_t>(tensor_layout{std::move(shape)}, placement, std::move(values))
             );
-            return detail::tensor_access::make(std::move(st));
         }
 
-        tensor materialize_node(const node_ptr& root) {
+        struct graph_result {
+            values_ptr values;
+            std::vector<index_t> shape;
+            device placement;
+        };
+
+        // Plans the graph under `root` (cached by its structure), runs its
+        // kernels on the calling thread's stream over the device values of
+        // the tensors it reads, and returns the result's values.
+        graph_result run_graph_with_shape(const node_ptr& root) {
             const auto start = std::chrono::steady_clock::now();
             graph_builder b;
             (void)b.visit(root);
@@ -250,23 +346,22 @@ namespace porch {
             const ir::node& r = b.g.at(b.g.root());
             if (r.is_scalar)
                 throw std::invalid_argument("scalar expression cannot materialize to a tensor");
-            const size_t count = ir::checked_numel(r.out);
-            const device placement = *b.placement;
-            if (count == 0) {
-                return make_realized(r.out, hip_jit::device_buffer{}, {}, true, placement);
+            graph_result result{nullptr, r.out, *b.placement};
+            if (ir::checked_numel(r.out) == 0) {
+                result.values = std::make_shared<resident_values>(hip_jit::device_buffer{}, std::vector<float32_t>{});
+                return result;
             }
             const ir::graph compacted = ir::compact(b.g);
             bool hit = false;
             std::shared_ptr<plan::graph_plan> p = plan::lookup(compacted, &hit);
 
-            std::vector<std::shared_ptr<realized_storage>> storages;
+            // the inputs' values stay referenced until the launches are queued
+            std::vector<values_ptr> held;
             std::vector<rt::buffer_state*> buffers;
-            storages.reserve(b.inputs.size());
+            held.reserve(b.inputs.size());
             for (const tensor& t : b.inputs) {
-                storages.push_back(detail::tensor_access::state(t)->storage());
-                buffers.push_back(
-                    hip_jit::buffer_access::state(storages.back()->device_values).get()
-                );
+                held.push_back(detail::tensor_access::state(t)->cell.get());
+                buffers.push_back(hip_jit::buffer_access::state(held.back()->memory()).get());
             }
             std::shared_ptr<rt::buffer_state> out = plan::run(
                 *p, buffers,
@@ -274,9 +369,9 @@ namespace porch {
                     return std::make_shared<hip_jit::device_buffer_state>(bytes);
                 }
             );
-            hip_jit::device_buffer result = hip_jit::buffer_access::wrap(
+            result.values = std::make_shared<resident_values>(hip_jit::buffer_access::wrap(
                 std::static_pointer_cast<hip_jit::device_buffer_state>(out)
-            );
+            ));
             const double ms = rt::elapsed_ms(start);
             {
                 std::scoped_lock lock{rt::counters_mutex()};
@@ -289,8 +384,10 @@ namespace porch {
                     rt::counters().last_miss_ms = ms;
                 }
             }
-            return make_realized(r.out, std::move(result), {}, false, placement);
+            return result;
         }
+
+        values_ptr run_graph(const node_ptr& root) { return run_graph_with_shape(root).values; }
 
         std::vector<index_t> infer_shape(const node_ptr& root, bool* is_scalar,
                                          bool* has_input, device* placement) {
@@ -305,15 +402,6 @@ namespace porch {
         }
 
     } // namespace
-
-    std::shared_ptr<realized_storage> lazy_materialization::storage() {
-        std::call_once(once, [this] {
-            tensor materialized = materialize_node(expression);
-            realized = detail::tensor_access::state(materialized)->realized;
-            done.store(true, std::memory_order_release);
-        });
-        return realized;
-    }
 
     // ------------------------------------------------------------------
     // tensor_index, tensor_layout
@@ -363,24 +451,39 @@ namespace porch {
     tensor::tensor(std::shared_ptr<state> initial_state) noexcept
         : state_(std::move(initial_state)) {}
 
-    tensor::tensor(std::vector<index_t> shape, std::vector<float32_t> values, device placement)
-        : state_(std::make_shared<state>(tensor_layout{std::move(shape)}, placement)) {
-        if (values.size() != state_->layout.numel())
-            throw std::invalid_argument("tensor data size does not match shape");
-        hip_jit::device_buffer buffer = hip_jit::make_device_buffer(values);
-        state_->realized =
-            std::make_shared<realized_storage>(std::move(buffer), std::move(values), true);
+    namespace {
+        std::vector<index_t> checked_shape(std::vector<index_t> shape, size_t values) {
+            if (values != ir::checked_numel(shape))
+                throw std::invalid_argument("tensor data size does not match shape");
+            return shape;
+        }
+    } // namespace
+
+    tensor::tensor(std::vector<index_t> shape, std::vector<float32_t> values, device placement) {
+        shape = checked_shape(std::move(shape), values.size());
+        hip_jit::device_buffer memory = hip_jit::make_device_buffer(values);
+        state_ = std::make_shared<state>(
+            tensor_layout{std::move(shape)}, placement,
+            std::make_shared<resident_values>(std::move(memory), std::move(values))
+        );
     }
 
     tensor::tensor(std::vector<index_t> shape, std::vector<float32_t> values,
-                   cuda_jit::device_buffer device_values, device placement)
-        : state_(std::make_shared<state>(tensor_layout{std::move(shape)}, placement)) {
-        if (values.size() != state_->layout.numel())
-            throw std::invalid_argument("tensor data size does not match shape");
+                   cuda_jit::device_buffer device_values, device placement) {
+        shape = checked_shape(std::move(shape), values.size());
         if (device_values.size_bytes() < values.size() * sizeof(float32_t))
             throw std::invalid_argument("tensor device storage is too small");
-        state_->realized = std::make_shared<realized_storage>(
-            std::move(device_values), std::move(values), true
+        state_ = std::make_shared<state>(
+            tensor_layout{std::move(shape)}, placement,
+            std::make_shared<resident_values>(std::move(device_values), std::move(values))
+        );
+    }
+
+    tensor::tensor(tensor_layout layout, cuda_jit::device_buffer storage, device placement) {
+        if (storage.size_bytes() < storage_span(layout) * sizeof(float32_t))
+            throw std::invalid_argument("tensor device storage is too small");
+        state_ = std::make_shared<state>(
+            std::move(layout), placement, std::make_shared<resident_values>(std::move(storage))
         );
     }
 
@@ -395,102 +498,66 @@ namespace porch {
     size_t tensor::numel() const noexcept { return state_->layout.numel(); }
     device tensor::placement() const noexcept { return state_->placement; }
 
-    tensor::tensor(tensor_layout layout, cuda_jit::device_buffer storage, device placement)
-        : state_(std::make_shared<state>(std::move(layout), placement)) {
-        if (storage.size_bytes() < storage_span(state_->layout) * sizeof(float32_t))
-            throw std::invalid_argument("tensor device storage is too small");
-        state_->realized = std::make_shared<realized_storage>(
-            std::move(storage), std::vector<float32_t>{}, false
-        );
-    }
+    namespace {
+        // The device values holding a tensor's elements in row-major order:
+        // its own, or for a view over strided storage, a gathered copy made
+        // once.
+        values_ptr row_major_values(const tensor& t, state_t& st) {
+            if (st.layout.is_contiguous()) return st.cell.get();
+            std::scoped_lock hold{st.gather_lock};
+            if (st.gathered == nullptr) st.gathered = run_graph(detail::expr_access::root(tensor_expr{t}));
+            return st.gathered;
+        }
+    } // namespace
 
     std::span<const float32_t> tensor::data() const {
-        std::shared_ptr<realized_storage> storage;
-        if (state_->layout.is_contiguous()) {
-            storage = state_->storage();
-        }
-        else {
-            std::call_once(state_->dense_once, [this] {
-                const tensor dense = materialize(tensor_expr{*this});
-                state_->dense = detail::tensor_access::state(dense)->storage();
-            });
-            storage = state_->dense;
-        }
-        std::scoped_lock lock{storage->host_mutex};
-        if (!storage->host_current) {
-            storage->host.resize(numel());
-            hip_jit::copy_to_host(storage->device_values, storage->host);
-            storage->host_current = true;
-        }
-        return storage->host;
+        return row_major_values(*this, *state_)->host(numel());
     }
 
     std::vector<float32_t> tensor::cpu() const {
-        const std::span<const float32_t> host = data();
-        return {host.begin(), host.end()};
+        return row_major_values(*this, *state_)->copy(numel());
     }
 
     const cuda_jit::device_buffer& tensor::device_data() const {
-        return state_->storage()->device_values;
+        return state_->cell.get()->memory();
     }
 
     const tensor& tensor::realize() const {
-        (void)state_->storage();
+        (void)state_->cell.get();
         return *this;
     }
 
     void tensor::synchronize() const {
-        std::shared_ptr<realized_storage> storage = state_->storage();
+        const values_ptr values = state_->cell.get();
         std::shared_ptr<rt::stream> s = rt::current_stream();
-        if (!storage->device_values.empty()) {
-            hip_jit::buffer_access::state(storage->device_values)->before_read(s);
-        }
+        if (!values->memory().empty()) hip_jit::buffer_access::state(values->memory())->before_read(s);
         s->synchronize();
     }
 
     tensor_expr tensor::operator[](std::initializer_list<tensor_index> indices) const {
         if (indices.size() > rank()) throw std::invalid_argument("too many tensor indices");
-        std::vector<index_t> out_shape;
-        std::vector<index_t> out_strides;
-        index_t offset = storage_offset();
-        size_t dim = 0;
-        for (const tensor_index& index : indices) {
-            const index_t extent = shape()[dim];
-            const index_t stride = strides()[dim];
-            switch (index.kind_) {
-                case tensor_index::kind::index:
-                    offset += normalize_index(index.index_, extent) * stride;
-                    break;
-                case tensor_index::kind::slice: {
-                    const index_t start = normalize_slice_endpoint(index.slice_.start, extent);
-                    const index_t stop = normalize_slice_endpoint(index.slice_.stop, extent);
-                    const size_t length = slice_length(start, stop, index.slice_.step);
-                    offset += start * stride;
-                    out_shape.push_back(static_cast<index_t>(length));
-                    out_strides.push_back(stride * index.slice_.step);
-                    break;
-                }
-                case tensor_index::kind::all:
-                    out_shape.push_back(extent);
-                    out_strides.push_back(stride);
-                    break;
+        // Start from the tensor's own view of its storage and restrict it
+        // one subscript at a time; axes past the last subscript stay whole.
+        strided_view view{storage_offset(), {shape().begin(), shape().end()},
+                          {strides().begin(), strides().end()}};
+        size_t axis = 0; // the axis of `view` the next subscript applies to
+        for (const tensor_index& ix : indices) {
+            if (ix.kind_ == tensor_index::kind::index) {
+                fix_axis(view, axis, ix.index_);
+                continue;
             }
-            ++dim;
+            if (ix.kind_ == tensor_index::kind::slice) narrow_axis(view, axis, ix.slice_);
+            ++axis;
         }
-        for (; dim < rank(); ++dim) {
-            out_shape.push_back(shape()[dim]);
-            out_strides.push_back(strides()[dim]);
-        }
-        (void)ir::checked_numel(out_shape);
+        (void)ir::checked_numel(view.extent);
         auto n = std::make_shared<tensor_expr::node>();
         n->kind = ir::op::slice;
-        // Offsets and strides above are in storage elements: over strided
-        // storage the slice applies to the raw storage, not to the view.
-        n->lhs = is_contiguous() ? detail::expr_access::root(tensor_expr{*this})
-                                 : storage_node(*this);
-        n->shape = std::move(out_shape);
-        n->strides = std::move(out_strides);
-        n->offset = offset;
+        // The view's base and steps count storage elements, so over strided
+        // storage the slice reads the raw storage, not the tensor's view.
+        n->lhs = is_contiguous() ? detail::expr_access::root(tensor_expr{*this}) : storage_node(*this);
+        n->shape = std::move(view.extent);
+        n->strides = std::move(view.step);
+        n->offset = view.base;
         return detail::expr_access::make(std::move(n));
     }
 
@@ -502,23 +569,22 @@ namespace porch {
 
     tensor_expr::tensor_expr(const tensor& value) {
         const std::shared_ptr<state_t>& st = detail::tensor_access::state(value);
-        if (st->lazy != nullptr && !st->lazy->done.load(std::memory_order_acquire)) {
-            root_ = st->lazy->expression;
-            return;
-        }
-        if (!value.is_contiguous()) {
-            // Strided storage: the view is a slice of the raw storage.
-            const tensor_layout& layout = value.layout();
-            auto view = std::make_shared<tensor_expr::node>();
-            view->kind = ir::op::slice;
-            view->lhs = storage_node(value);
-            view->shape.assign(layout.shape().begin(), layout.shape().end());
-            view->strides.assign(layout.strides().begin(), layout.strides().end());
-            view->offset = layout.storage_offset();
-            root_ = std::move(view);
+        // a tensor whose graph has not run yet is inlined into this one
+        if (node_ptr graph = st->cell.pending()) {
+            root_ = std::move(graph);
             return;
         }
         root_ = storage_node(value);
+        if (value.is_contiguous()) return;
+        // over strided storage the tensor is a slice of the raw storage
+        const tensor_layout& layout = value.layout();
+        auto view = std::make_shared<tensor_expr::node>();
+        view->kind = ir::op::slice;
+        view->lhs = std::move(root_);
+        view->shape.assign(layout.shape().begin(), layout.shape().end());
+        view->strides.assign(layout.strides().begin(), layout.strides().end());
+        view->offset = layout.storage_offset();
+        root_ = std::move(view);
     }
 
     tensor_expr::tensor_expr(float32_t value) {
@@ -553,9 +619,7 @@ namespace porch {
         if (scalar)
             throw std::invalid_argument("scalar expression cannot convert to a tensor");
         (void)ir::checked_numel(s);
-        auto st = std::make_shared<state_t>(tensor_layout{std::move(s)}, placement);
-        st->lazy = std::make_shared<lazy_materialization>(root_);
-        return detail::tensor_access::make(std::move(st));
+        return detail::tensor_access::make(std::make_shared<state_t>(tensor_layout{std::move(s)}, placement, root_));
     }
 
     // ------------------------------------------------------------------
@@ -655,7 +719,8 @@ namespace porch {
     tensor_expr reciprocal(tensor_expr value) { return unary(ir::op::reciprocal, value); }
 
     tensor materialize(const tensor_expr& expression) {
-        return materialize_node(detail::expr_access::root(expression));
+        graph_result r = run_graph_with_shape(detail::expr_access::root(expression));
+        return make_tensor(std::move(r.shape), r.placement, std::move(r.values));
     }
 
     tensor_expr operator+(tensor_expr lhs, tensor_expr rhs) {
