@@ -482,48 +482,31 @@ class tensor:  # noqa: N801 - porch's spelling
             indices = (indices,)
         if len(indices) > self.rank():
             raise InvalidArgument("too many tensor indices")
-        shape = self.shape()
-        strides = self.strides()
-        out_shape: list[int] = []
-        out_strides: list[int] = []
-        offset = self.storage_offset()
-        for dim, index in enumerate(indices):
-            extent = shape[dim]
-            stride = strides[dim]
+        # restrict the tensor's strided view of its storage one subscript
+        # at a time; axes past the last subscript stay whole
+        base = self.storage_offset()
+        extent = list(self.shape())
+        step = list(self.strides())
+        axis = 0
+        for index in indices:
             if isinstance(index, builtins.slice):
-                start = 0 if index.start is None else index.start
-                stop = extent if index.stop is None else index.stop
-                step = 1 if index.step is None else index.step
-                index = slice(start, stop, step)
+                index = slice(0 if index.start is None else index.start,
+                              extent[axis] if index.stop is None else index.stop,
+                              1 if index.step is None else index.step)
             if isinstance(index, _All):
-                out_shape.append(extent)
-                out_strides.append(stride)
+                axis += 1
             elif isinstance(index, slice):
-                start = _normalize_endpoint(index.start, extent)
-                stop = _normalize_endpoint(index.stop, extent)
-                if index.step <= 0:
-                    raise InvalidArgument("tensor slice step must be positive")
-                length = 0 if stop <= start else (stop - start + index.step - 1) // index.step
-                offset += start * stride
-                out_shape.append(length)
-                out_strides.append(stride * index.step)
+                base += _narrow_axis(extent, step, axis, index)
+                axis += 1
             else:
-                i = int(index)
-                if i < 0:
-                    i += extent
-                if i < 0 or i >= extent:
-                    raise OutOfRange("tensor index is out of bounds")
-                offset += i * stride
-        for dim in range(len(indices), self.rank()):
-            out_shape.append(shape[dim])
-            out_strides.append(strides[dim])
-        # offsets and strides are in storage elements: over strided storage
-        # the slice applies to the raw storage, not to the view
+                base += _fix_axis(extent, step, axis, int(index))
+        # the base and steps count storage elements: over strided storage
+        # the slice reads the raw storage, not the tensor's view
         source = tensor_expr(self)._root if self.is_contiguous() else _storage_node(self)
         node = _Node("slice", source)
-        node.shape = out_shape
-        node.strides = out_strides
-        node.offset = offset
+        node.shape = extent
+        node.strides = step
+        node.offset = base
         return tensor_expr._wrap(node)
 
     # arithmetic records expressions
@@ -558,14 +541,30 @@ def _storage_node(value: "tensor") -> _Node:
     return node
 
 
-def _normalize_endpoint(index: int, extent: int) -> int:
-    if index < 0:
-        index += extent
-    if index < 0:
-        return 0
-    if index > extent:
-        return extent
-    return index
+def _fix_axis(extent: list, step: list, axis: int, at: int) -> int:
+    """Subscripts `axis` with an integer (counted from the end when
+    negative): removes the axis and returns the storage offset it adds."""
+    n = extent[axis]
+    c = at + n if at < 0 else at
+    if c < 0 or c >= n:
+        raise OutOfRange("tensor index is out of bounds")
+    offset = c * step[axis]
+    del extent[axis], step[axis]
+    return offset
+
+
+def _narrow_axis(extent: list, step: list, axis: int, r: "slice") -> int:
+    """Subscripts `axis` with a range: endpoints counted from the end when
+    negative and clamped to [0, extent]; keeps every r.step-th coordinate
+    from the first.  Returns the storage offset it adds."""
+    if r.step <= 0:
+        raise InvalidArgument("tensor slice step must be positive")
+    n = extent[axis]
+    first, end = (builtins.min(builtins.max(e + n if e < 0 else e, 0), n) for e in (r.start, r.stop))
+    offset = first * step[axis]
+    extent[axis] = (end - first - 1) // r.step + 1 if end > first else 0
+    step[axis] *= r.step
+    return offset
 
 
 class tensor_expr:  # noqa: N801 - porch's spelling
