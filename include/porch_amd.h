@@ -212,8 +212,15 @@ porch_status porch_materialize(const porch_graph* graph,
 #define PORCH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* porch_materialize into `out`, an existing buffer of at least the result's
- * size, allocating no device memory (no hipMalloc, hipFree or their async
- * forms, in the library or any routine it calls).  The same kernels run;
+ * size, allocating no memory once it has run once for the graph's
+ * structure on the calling thread and device: such a call makes no
+ * hipMalloc, hipFree, hipHostMalloc or hipModuleLoadData call, or their
+ * async forms, in the library or any routine it calls.  The first call for
+ * a structure (make it outside any HIP graph capture, as a warm-up) may:
+ * it compiles and loads the graph's kernels (hipModuleLoadData allocates
+ * code memory), may create the thread's stream, and on the first call on a
+ * device looks up the array's address, which makes the runtime load the
+ * array.  The same kernels run;
  * the graph's temporaries (memoised reductions, split-reduction partials,
  * materialised product operands) come from the fixed per-GPU array of
  * PORCH_NOALLOC_SCRATCH_BYTES, and a graph that needs more fails with
@@ -269,6 +276,13 @@ typedef struct porch_jit_stats {
     double last_hit_us;      /* last cache-hit materialize, call to return */
     uint64_t disk_hits;      /* code objects read from the on-disk cache */
     double disk_ms;          /* host time reading them */
+    /* Calls into libamdhip64 that allocate or release memory, counted from
+     * the start of the process (no reference counterpart). */
+    uint64_t device_allocs;  /* hipMallocAsync */
+    uint64_t device_frees;   /* hipFreeAsync */
+    uint64_t host_allocs;    /* hipHostMalloc (pinned staging chunks) */
+    uint64_t host_frees;     /* hipHostFree */
+    uint64_t module_loads;   /* hipModuleLoadData (device code memory) */
 } porch_jit_stats;
 
 porch_status porch_get_jit_stats(porch_jit_stats* stats);

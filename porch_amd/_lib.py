@@ -68,6 +68,11 @@ class JitStats(ctypes.Structure):
         ("last_hit_us", ctypes.c_double),
         ("disk_hits", ctypes.c_uint64),
         ("disk_ms", ctypes.c_double),
+        ("device_allocs", ctypes.c_uint64),
+        ("device_frees", ctypes.c_uint64),
+        ("host_allocs", ctypes.c_uint64),
+        ("host_frees", ctypes.c_uint64),
+        ("module_loads", ctypes.c_uint64),
     ]
 
 

@@ -445,6 +445,12 @@ porch_status porch_get_jit_stats(porch_jit_stats* stats) {
         stats->last_hit_us = c.last_hit_us;
         stats->disk_hits = c.disk_hits;
         stats->disk_ms = c.disk_ms;
+        const hip::allocation_calls a = hip::allocation_counts();
+        stats->device_allocs = a.device_allocs;
+        stats->device_frees = a.device_frees;
+        stats->host_allocs = a.host_allocs;
+        stats->host_frees = a.host_frees;
+        stats->module_loads = a.module_loads;
     });
 }
 

@@ -2,6 +2,7 @@
 
 #include <dlfcn.h>
 
+#include <atomic>
 #include <cstdlib>
 #include <mutex>
 #include <stdexcept>
@@ -21,6 +22,56 @@ namespace porch::hip {
         bool bind(void* library, F& slot, const char* name) {
             slot = reinterpret_cast<F>(dlsym(library, name));
             return slot != nullptr;
+        }
+
+        // Counting wrappers around the entry points that allocate: each
+        // adds one to its counter and calls the library's function.
+        struct counted_entry_points {
+            decltype(api::malloc_async) malloc_async = nullptr;
+            decltype(api::free_async) free_async = nullptr;
+            decltype(api::host_malloc) host_malloc = nullptr;
+            decltype(api::host_free) host_free = nullptr;
+            decltype(api::module_load_data) module_load_data = nullptr;
+            std::atomic<uint64_t> device_allocs{0}, device_frees{0}, host_allocs{0}, host_frees{0},
+                module_loads{0};
+        };
+        counted_entry_points& counted() {
+            static counted_entry_points* c = new counted_entry_points();
+            return *c;
+        }
+        error_t counting_malloc_async(void** ptr, size_t bytes, stream_t s) {
+            counted().device_allocs.fetch_add(1, std::memory_order_relaxed);
+            return counted().malloc_async(ptr, bytes, s);
+        }
+        error_t counting_free_async(void* ptr, stream_t s) {
+            counted().device_frees.fetch_add(1, std::memory_order_relaxed);
+            return counted().free_async(ptr, s);
+        }
+        error_t counting_host_malloc(void** ptr, size_t bytes, unsigned flags) {
+            counted().host_allocs.fetch_add(1, std::memory_order_relaxed);
+            return counted().host_malloc(ptr, bytes, flags);
+        }
+        error_t counting_host_free(void* ptr) {
+            counted().host_frees.fetch_add(1, std::memory_order_relaxed);
+            return counted().host_free(ptr);
+        }
+        error_t counting_module_load_data(module_t* module, const void* image) {
+            counted().module_loads.fetch_add(1, std::memory_order_relaxed);
+            return counted().module_load_data(module, image);
+        }
+
+        void count_allocations(api& t) {
+            counted_entry_points& c = counted();
+            c.malloc_async = t.malloc_async;
+            c.free_async = t.free_async;
+            c.host_malloc = t.host_malloc;
+            c.host_free = t.host_free;
+            c.module_load_data = t.module_load_data;
+            t.malloc_async = counting_malloc_async;
+            t.free_async = counting_free_async;
+            t.host_malloc = counting_host_malloc;
+            t.host_free = counting_host_free;
+            t.module_load_data = counting_module_load_data;
         }
 
         struct loaded {
@@ -116,6 +167,7 @@ namespace porch::hip {
                 ok &= bind(hip_library, t.get_error_name, "hipGetErrorName");
                 ok &= bind(hip_library, t.get_error_string, "hipGetErrorString");
                 result.runtime_ok = ok;
+                if (ok) count_allocations(t);
                 if (!ok) {
                     result.runtime_error =
                         "libamdhip64 lacks an entry point porch requires";
@@ -194,6 +246,17 @@ namespace porch::hip {
         catch (...) {
             return false;
         }
+    }
+
+    allocation_calls allocation_counts() noexcept {
+        const counted_entry_points& c = counted();
+        allocation_calls a;
+        a.device_allocs = c.device_allocs.load(std::memory_order_relaxed);
+        a.device_frees = c.device_frees.load(std::memory_order_relaxed);
+        a.host_allocs = c.host_allocs.load(std::memory_order_relaxed);
+        a.host_frees = c.host_frees.load(std::memory_order_relaxed);
+        a.module_loads = c.module_loads.load(std::memory_order_relaxed);
+        return a;
     }
 
     void check(error_t result, std::string_view operation) {

@@ -1,5 +1,7 @@
 #pragma once
 
+#include <cstdint>
+
 // Thin loader over the C ABI of libamdhip64 and libhiprtc (ROCm 7).  The
 // library resolves every entry point with dlsym at first use, so porch links
 // against neither and loads on machines without ROCm; such machines report
@@ -113,6 +115,17 @@ namespace porch::hip {
 
     // True when both libraries load with every symbol resolved.
     bool libraries_present() noexcept;
+
+    // Calls made through runtime() that allocate or release memory, counted
+    // from the start of the process.
+    struct allocation_calls {
+        uint64_t device_allocs = 0; // hipMallocAsync
+        uint64_t device_frees = 0;  // hipFreeAsync
+        uint64_t host_allocs = 0;   // hipHostMalloc
+        uint64_t host_frees = 0;    // hipHostFree
+        uint64_t module_loads = 0;  // hipModuleLoadData (code memory)
+    };
+    allocation_calls allocation_counts() noexcept;
 
     // Throws std::runtime_error("<operation> failed: <name>: <description>")
     // for a failing HIP call (reference src/cuda_jit.cpp:315-339 format).
