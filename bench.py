@@ -414,6 +414,43 @@ extern "C" __global__ void __launch_bounds__(256) porch_control_half(
         for (int r = 0; r < 4; ++r) y[g + (round * 4 + r) * count] = (porch_v2f){v[r].y + 1.0f, v[r].w + 1.0f};
     }
 }
+// Other launch shapes of the elementwise workload's arithmetic, (a + b) * 2 - 1
+// over 262144 float4 of each operand: `count` lanes (256 a workgroup), each
+// taking 262144 / count float4s, strided by the lane count ("grid") or
+// consecutive ("run"); with plain or non-temporal loads and stores.
+#define PORCH_EW_STEP(L, S)                                                                  \
+    {                                                                                      \
+        const porch_v4f x = L(reinterpret_cast<const porch_v4f*>(a0) + i);                 \
+        const porch_v4f y = L(reinterpret_cast<const porch_v4f*>(a1) + i);                 \
+        const porch_v4f r = (porch_v4f){((x.x + y.x) * 2.0f) - 1.0f, ((x.y + y.y) * 2.0f) - 1.0f, \
+                                        ((x.z + y.z) * 2.0f) - 1.0f, ((x.w + y.w) * 2.0f) - 1.0f}; \
+        S(r, reinterpret_cast<porch_v4f*>(out) + i);                                       \
+    }
+#define PORCH_PLAIN_LOAD(p) (*(p))
+#define PORCH_PLAIN_STORE(v, p) (*(p) = (v))
+#define PORCH_NT_STORE(v, p) __builtin_nontemporal_store((v), (p))
+#define PORCH_EW_GRID(name, L, S)                                                            \
+    extern "C" __global__ void __launch_bounds__(256) name(                                \
+        const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out, \
+        unsigned long long count) {                                                        \
+        for (unsigned i = blockIdx.x * 256u + threadIdx.x; i < 262144u; i += (unsigned)count) \
+            PORCH_EW_STEP(L, S)                                                            \
+    }
+#define PORCH_EW_RUN(name, per_lane, L, S)                                                   \
+    extern "C" __global__ void __launch_bounds__(256) name(                                \
+        const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out, \
+        unsigned long long count) {                                                        \
+        const unsigned g = blockIdx.x * 256u + threadIdx.x;                                \
+        _Pragma("unroll") for (unsigned j = 0; j < per_lane; ++j) {                        \
+            const unsigned i = (g / 64u) * (64u * per_lane) + j * 64u + (g % 64u);          \
+            PORCH_EW_STEP(L, S)                                                            \
+        }                                                                                  \
+    }
+PORCH_EW_GRID(porch_ew_grid_nt_plain, __builtin_nontemporal_load, PORCH_PLAIN_STORE)
+PORCH_EW_GRID(porch_ew_grid_plain_plain, PORCH_PLAIN_LOAD, PORCH_PLAIN_STORE)
+PORCH_EW_GRID(porch_ew_grid_nt_nt, __builtin_nontemporal_load, PORCH_NT_STORE)
+PORCH_EW_RUN(porch_ew_run2_nt_plain, 2u, __builtin_nontemporal_load, PORCH_PLAIN_STORE)
+PORCH_EW_RUN(porch_ew_run4_nt_plain, 4u, __builtin_nontemporal_load, PORCH_PLAIN_STORE)
 // A plain copy at a large size: `count` lanes, each copying four float4 of
 // a0 to out, strided by the lane count (non-temporal loads and stores).
 extern "C" __global__ void __launch_bounds__(256) porch_control_stream(
@@ -462,6 +499,26 @@ def controls(launches: int) -> int:
         porch.materialize(config_graph("elementwise", sets[i % copies]))
     porch.synchronize()
     log(f"controls: elementwise workload x {launches}")
+    # other launch shapes of the same arithmetic over the same buffers:
+    # (kernel, lanes); the grid is lanes / 256 workgroups
+    for kernel, lanes in (("porch_ew_grid_nt_plain", 262144), ("porch_ew_grid_nt_plain", 131072),
+                          ("porch_ew_grid_nt_plain", 65536), ("porch_ew_grid_nt_plain", 32768),
+                          ("porch_ew_grid_plain_plain", 262144), ("porch_ew_grid_nt_nt", 262144),
+                          ("porch_ew_run2_nt_plain", 131072), ("porch_ew_run4_nt_plain", 65536)):
+        for i in range(launches):
+            a, b = sets[i % copies]
+            ins = (ctypes.c_void_p * 2)(a.device_data().handle, b.device_data().handle)
+            _lib.check(_lib.lib.porch_launch_fused_elementwise(
+                data, size, kernel.encode(), ins, 2, outs[i % copies].device_data().handle, lanes))
+        porch.synchronize()
+        log(f"controls: {kernel} at {lanes // 256} workgroups x {launches}")
+    for i, (a, b) in enumerate(sets[:2]):
+        # the variants' values are the workload's bits (read from the device
+        # buffer: the kernels wrote it behind the tensor's host copy)
+        got = outs[i].device_data().download(n)
+        want = ((a.cpu() + b.cpu()) * np.float32(2.0) - np.float32(1.0)).astype(np.float32)
+        if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+            raise AssertionError("controls: an elementwise variant differs from the workload's arithmetic")
     del sets, outs
 
     # The view chain beside a coalesced kernel that moves the same bytes

@@ -58,7 +58,7 @@ namespace porch::cg {
             s += "extern \"C\" __global__ void __launch_bounds__(256) porch_pointwise(" +
                  kernel_params(r.n_slots) + ") {\n";
             s += "    for (idx_t f = (idx_t)blockIdx.x * 256 + threadIdx.x; f < " +
-                 std::to_string(count) + "; f += (idx_t)gridDim.x * 256) {\n";
+                 std::to_string(count) + "; f += " + std::to_string(int64_t{kc.grid_x} * 256) + ") {\n";
             const std::vector<bool> used = used_coordinates(*r.expr, r.root, rank);
             s += decompose("f", r.shape, used, T, "        ");
             std::string body;
@@ -145,8 +145,11 @@ namespace porch::cg {
             s = kernel_prologue(r.n_slots, T);
             s += "extern \"C\" __global__ void __launch_bounds__(256) porch_pointwise(" +
                  kernel_params(r.n_slots) + ") {\n";
+            // the stride is the launch's lane count, a constant: no
+            // implicit kernel argument is read, and a grid that covers every
+            // group runs the body once
             s += "    for (idx_t g = (idx_t)blockIdx.x * 256 + threadIdx.x; g < " +
-                 std::to_string(groups) + "; g += (idx_t)gridDim.x * 256) {\n";
+                 std::to_string(groups) + "; g += " + std::to_string(int64_t{kc.grid_x} * 256) + ") {\n";
             const std::string ind = "        ";
             s += ind + "const idx_t f = g * 4;\n";
             const std::vector<bool> used = used_coordinates(*r.expr, r.root, rank);
