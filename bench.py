@@ -14,13 +14,14 @@ the per-launch duration behind `roofline.achieved`).
 The headline line is the view chain (strided slices + transposes + concat
 over x fp32 [4096, 4096]): HBM GB/s of algorithmic bytes (all of x read, the
 output written).  The other workloads are reported beside it under
-"configs", each with its roofline fraction and JIT latency, followed by three
+"configs", each with its roofline fraction and JIT latency, followed by
 workloads of the IR extensions (a batched transpose and a head permute via
-permute, and a batched matmul with an epilogue) and two products with one
-short side (16 columns, 32 rows: a kernel split over K and its combine,
-timed from the first kernel's start to the second's end).  The host
-evaluator (the oracle, OpenMP) is timed on this machine's cores as the CPU
-baseline.
+permute, a batched matmul with an epilogue, attention scores q @ k^T over 16
+heads, a softmax over 262144-value rows) and two products with one short
+side (16 columns, 32 rows: a kernel split over K and its combine, timed from
+the first kernel's start to the second's end).  The host evaluator (the
+oracle, OpenMP) is timed on this machine's cores as the CPU baseline: 10 s of
+CPU work for the headline workload, 4 s for each other one.
 
 `roofline.traffic` is the HBM bytes per launch that rocprofv3's FETCH_SIZE
 and WRITE_SIZE counters read for the same kernel, scaled by what they read
@@ -569,8 +570,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--configs", default="elementwise,view_chain,softmax,logistic_rowsum,matmul_epilogue,"
-                                             "batched_transpose,heads_permute,batched_matmul,narrow_product,"
-                                             "wide_product")
+                                             "batched_transpose,heads_permute,batched_matmul,attention_scores,"
+                                             "vocab_softmax,narrow_product,wide_product")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--jit-probe", default=None, help=argparse.SUPPRESS)
     parser.add_argument("--controls", type=int, default=0, metavar="LAUNCHES",
@@ -606,7 +607,8 @@ def main() -> int:
             f"disk {r['jit_ms']['disk'] if r['jit_ms']['disk'] is None else round(r['jit_ms']['disk'], 2)} ms "
             f"hit {r['jit_ms']['hit']*1e3:.1f} us")
         if not args.no_cpu:
-            results[name]["cpu_baseline"] = cpu_baseline(name)
+            # 10 s of CPU work for the headline workload, 4 s for the others
+            results[name]["cpu_baseline"] = cpu_baseline(name, 10.0 if name == "view_chain" else 4.0)
             log(f"{name}: cpu {results[name]['cpu_baseline']['value']:.2f} "
                 f"{results[name]['cpu_baseline']['unit']} on {results[name]['cpu_baseline']['cores']} threads")
 
