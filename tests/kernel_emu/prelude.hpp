@@ -8,7 +8,10 @@
 // not the point (the oracle checks those); addresses are.
 //
 // Emulated: thread/block indices, __syncthreads (a barrier over the
-// block's threads), wave64 __shfl_xor, __shfl, __ballot, DPP row patterns,
+// block's threads), __builtin_amdgcn_wave_barrier (a barrier over the
+// wave's threads: on the GPU a wave's lanes run together and only the
+// compiler's ordering is at stake), wave64 __shfl_xor, __shfl, __ballot,
+// DPP row patterns,
 // v_mfma_f32_32x32x2f32 and v_mfma_f32_16x16x4f32 (barriers
 // over the wave's 64 threads, operand layouts as on gfx950), raw buffer
 // stores (range-checked against the resource's size), LDS arrays
@@ -42,6 +45,7 @@ namespace emu {
     inline int wave() { return static_cast<int>(thread_idx.x / 64); }
     inline int lane() { return static_cast<int>(thread_idx.x % 64); }
     inline void syncthreads() { block_barrier->arrive_and_wait(); }
+    inline void wave_sync() { wave_barrier[wave()]->arrive_and_wait(); }
 
     inline float shfl_xor(float v, int mask, int width) {
         const int w = wave();
@@ -170,6 +174,7 @@ namespace emu {
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
 #define __builtin_amdgcn_sched_barrier(a) ((void)0)
+#define __builtin_amdgcn_wave_barrier() emu::wave_sync()
 #define __builtin_amdgcn_s_sleep(n) std::this_thread::yield()
 #define __HIP_MEMORY_SCOPE_AGENT 0
 #define __hip_atomic_load(p, order, scope) __atomic_load_n((p), (order))

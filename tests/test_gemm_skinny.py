@@ -1,9 +1,11 @@
 """Matmuls with one short side (kernel kinds gemm.rows, gemm.combine,
-gemm.cols, gemm.narrow, gemm.wide): a few rows (a vector times a matrix, a
-small batch of rows; 8 to 64 rows over 256 columns or more on 16x16x4 MFMA
-blocks, split over K) or a few columns (a matrix times a vector; up to 8 columns over
-many rows, one wave holding 1, 2 or 4 rows; 7 to 32 columns over 128 rows
-or more on 16x16x4 MFMA blocks, split over K); and matmuls whose tiles leave
+gemm.cols, gemm.narrow, gemm.narrow_rows, gemm.wide): a few rows (a vector
+times a matrix, a small batch of rows; 8 to 64 rows over 256 columns or more
+on 16x16x4 MFMA blocks, split over K) or a few columns (a matrix times a
+vector; up to 8 columns over many rows, one wave holding 1, 2 or 4 rows; 7
+to 32 columns over 128 rows or more on 16x16x4 MFMA blocks, split over K;
+7 to 16 columns over 4096 rows or more and K >= 2048, one workgroup per 16
+rows over all of K, A's rows staged through LDS); and matmuls whose tiles leave
 most of the machine idle over a long K (gemm.mfma split over K, then
 gemm.combine).
 
@@ -108,6 +110,18 @@ CASES = {
     "narrow, transposed B": (
         ([2048, 516], [12, 516]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
         lambda p: p, ["gemm.narrow", "gemm.combine"]),
+    "narrow rows, sixteen columns": (
+        ([4096, 2048], [2048, 16]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.narrow_rows"]),
+    "narrow rows, ragged rows and columns, K tail, relu": (
+        ([4090, 2100], [2100, 13]), lambda a, b: porch.relu(porch.matmul(a, b) - 2.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p - 2.0, 0.0), ["gemm.narrow_rows"]),
+    "narrow rows, batched": (
+        ([2, 2048, 2048], [2, 2048, 16]), lambda a, b: porch.batched_matmul(a, b) + 1.0, lambda a, b: a @ b,
+        lambda p: p + 1.0, ["gemm.narrow_rows"]),
+    "narrow rows, transposed B": (
+        ([4096, 3000], [9, 3000]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+        lambda p: p, ["gemm.narrow_rows"]),
     "six columns, batched, ragged row groups": (
         ([2, 1101, 512], [2, 512, 6]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.cols"]),
@@ -173,6 +187,7 @@ def test_split_k_chunks(shape, chunks):
 # the epilogue (the combine where there is one) loads it at the output's
 # coordinates.
 BIAS_SHAPES = {
+    (4096, 2048, 16): ["gemm.narrow_rows"],
     (8, 2048, 1024): ["gemm.wide", "gemm.combine"],
     (4, 2048, 1024): ["gemm.rows", "gemm.combine"],
     (40, 1030, 200): ["gemm.mfma", "gemm.combine"],
@@ -213,7 +228,8 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "seven columns over many rows, A transposed",
                                   "narrow, ragged rows and columns, K tail, relu",
                                   "narrow, one chunk, epilogue in the kernel", "narrow, batched, ragged row tiles",
-                                  "narrow, transposed B", "wide, ragged rows and columns, K tail, relu",
+                                  "narrow, transposed B", "narrow rows, ragged rows and columns, K tail, relu",
+                                  "wide, ragged rows and columns, K tail, relu",
                                   "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
@@ -269,7 +285,7 @@ def test_epilogue_reading_an_input_bit_exact(gpu, shape):
 
 
 @pytest.mark.parametrize("shape, chunks", [
-    ((4096, 4096, 16), 8),   # 128 row tiles of 32: 1024 waves, 8 chunks of 512
+    ((4096, 1024, 16), 8),   # 128 row tiles of 32: 1024 waves, 8 chunks of 128
     ((1100, 1036, 20), 9),   # 35 row tiles: 30 chunks for the waves, 12 for partials at most 1/4
                              # of A, of 87 -> 128 values of K (a multiple of 64): 9 chunks
     ((2048, 256, 32), 2),    # partials at most 1/4 of A: 256 / (4 x 32) chunks
@@ -286,10 +302,31 @@ def test_narrow_chunks(shape, chunks):
     assert plan["temps"] == ([chunks * m * n] if chunks > 1 else [])
 
 
+@pytest.mark.parametrize("shape, batch", [((4096, 4096, 16), 1), ((4090, 2100, 13), 1), ((2048, 2048, 16), 2)])
+def test_narrow_rows_plan(shape, batch):
+    # one workgroup of 8 waves per 16 rows (over all batch entries), no
+    # partial products
+    m, k, n = shape
+    a, b = placeholder([batch, m, k] if batch > 1 else [m, k]), placeholder([batch, k, n] if batch > 1 else [k, n])
+    plan = porch.plan(porch.batched_matmul(a, b) if batch > 1 else porch.matmul(a, b))
+    assert [x["kind"] for x in plan["kernels"]] == ["gemm.narrow_rows"]
+    assert plan["kernels"][0]["grid"][0] == batch * -(-m // 16)
+    assert plan["kernels"][0]["block"] == 512
+    assert plan["temps"] == []
+
+
 def test_narrow_bounds():
     # below 7 columns gemm.cols, above 32 or below 128 rows the MFMA tiles
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 6]))) == ["gemm.cols"]
-    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 7])))[0] == "gemm.narrow"
+    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 7])))[0] == "gemm.narrow_rows"
+    # gemm.narrow_rows: up to 16 columns, at least one workgroup of 16 rows
+    # per compute unit, K of 2048 or more
+    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 16])))[0] == "gemm.narrow_rows"
+    assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 17])))[0] == "gemm.narrow"
+    assert _kinds(porch.matmul(placeholder([4080, 4096]), placeholder([4096, 16])))[0] == "gemm.narrow"
+    assert _kinds(porch.matmul(placeholder([4081, 4096]), placeholder([4096, 16])))[0] == "gemm.narrow_rows"
+    assert _kinds(porch.matmul(placeholder([4096, 2044]), placeholder([2044, 16])))[0] == "gemm.narrow"
+    assert _kinds(porch.matmul(placeholder([4096, 2048]), placeholder([2048, 16])))[0] == "gemm.narrow_rows"
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 32])))[0] == "gemm.narrow"
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 33])))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([128, 4096]), placeholder([4096, 16])))[0] == "gemm.narrow"
@@ -369,7 +406,28 @@ def test_wide_infinities_in_the_k_tail(gpu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind, m, k, n", [("gemm.narrow", 1100, 1036, 20), ("gemm.wide", 20, 203, 300)])
+def test_narrow_rows_infinities_at_the_waves_ends(gpu):
+    """Infinities in B's rows at the ends of the waves' ranges of K (K = 2100:
+    264 values a wave, the last wave 252, its second round empty; lanes
+    past a wave's end read column 0 and zero both operands): inf or NaN
+    exactly where the oracle has them."""
+    m, k, n = 4090, 2100, 13
+    a, b = _ints([m, k], 33), _ints([k, n], 34)
+    b[k - 1, :] = np.inf
+    b[263, 3] = -np.inf     # the first wave's last value
+    b[264, 4] = np.inf      # the second wave's first
+    b[k - 252, 7] = np.inf  # the last wave's first
+    expr = porch.matmul(gpu.tensor([m, k], a), gpu.tensor([k, n], b))
+    assert _kinds(expr) == ["gemm.narrow_rows"]
+    out = gpu.materialize(expr).cpu().reshape(m, n)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
+    assert np.isinf(ref).any() and np.isnan(ref).any()
+    assert np.array_equal(out, ref, equal_nan=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind, m, k, n", [("gemm.narrow", 1100, 1036, 20), ("gemm.narrow_rows", 4090, 2100, 13),
+                                           ("gemm.wide", 20, 203, 300)])
 def test_clamped_edge_rows_and_columns(gpu, kind, m, k, n):
     """Rows past m and columns past n of the last tiles are read at the last
     row (column) and feed only outputs that are not stored: a NaN in A's
