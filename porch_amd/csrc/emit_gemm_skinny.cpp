@@ -62,9 +62,10 @@ namespace porch::cg {
         // 128-bit load of B, take over from there)
         constexpr int64_t wide_min_rows = 8;
         constexpr int64_t wide_max_rows = 64;
-        // steps of 4 values of K whose loads are issued together (16
-        // measured no faster, 2 to 7 % slower from 24 rows)
-        constexpr int wide_depth = 8;
+        // steps of 4 values of K whose loads are issued together, in each of
+        // two register sets (one set of 8: 23.0 against 20.1 us on [32,
+        // 4096] @ [4096, 4096])
+        constexpr int wide_depth = 4;
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
 
@@ -223,13 +224,17 @@ namespace porch::cg {
 
         // The K loop of gemm.narrow and gemm.wide over [k0, k1): batches of
         // D steps of `step_k` values, each batch's loads issued together
-        // ahead of its MFMAs; then single steps (`singles`) and a partial
-        // last step (`tail`).  sched_barrier keeps the loads ahead: left to
-        // itself the scheduler sinks each load to its MFMA and waits there.
-        // (Software-pipelining the batches over two register sets, the next
-        // batch's loads issued before this batch's MFMAs, was no faster.)
+        // ahead of its MFMAs, in two register sets: the next batch's loads
+        // are issued before this batch's MFMAs (the last prefetch of a
+        // chunk reloads its own batch: in bounds, no branch around the
+        // loads); then single steps (`singles`) and a partial last step
+        // (`tail`).  sched_barrier keeps the loads ahead: left to itself the
+        // scheduler sinks each load to its MFMA and waits there.  (Measured
+        // on [32, 4096] @ [4096, 4096]: 20.1 us for batches of 4 steps in
+        // two sets, against 23.0 us for batches of 8 in one.)
         std::string batched_k_loop(int D, int64_t step_k, bool singles, bool tail, const set_text& declare,
                                    const load_text& loads, const set_text& mfmas) {
+            const std::string in1 = "    ";
             const std::string in2 = "        ";
             auto batch = [&](int d, bool t) {
                 return declare("R", d, in2) + loads("R", d, t, "kk", in2) + in2 + "__builtin_amdgcn_sched_barrier(0);\n" +
@@ -238,7 +243,22 @@ namespace porch::cg {
             const std::string S = std::to_string(step_k * D);
             const std::string one = std::to_string(step_k);
             std::string s = "    idx_t kk = k0;\n";
-            s += "    for (; kk + " + S + " <= k1; kk += " + S + ") {\n" + batch(D, false) + "    }\n";
+            s += "    const idx_t nb = (k1 - k0) / " + S + ";\n";
+            s += declare("P", D, in1) + declare("Q", D, in1);
+            s += "    if (nb > 0) {\n" + loads("P", D, false, "kk", in2) + "    }\n";
+            s += "    for (idx_t b = 0; b < nb; b += 2) {\n";
+            s += "        {\n            const idx_t kn = b + 1 < nb ? kk + " + S + " : kk;\n" +
+                 loads("Q", D, false, "kn", "            ") + "        }\n";
+            s += in2 + "__builtin_amdgcn_sched_barrier(0);\n" + mfmas("P", D, in2) + in2 +
+                 "__builtin_amdgcn_sched_barrier(0);\n";
+            s += "        kk += " + S + ";\n";
+            s += "        if (b + 1 >= nb) break;\n";
+            s += "        {\n            const idx_t kn = b + 2 < nb ? kk + " + S + " : kk;\n" +
+                 loads("P", D, false, "kn", "            ") + "        }\n";
+            s += in2 + "__builtin_amdgcn_sched_barrier(0);\n" + mfmas("Q", D, in2) + in2 +
+                 "__builtin_amdgcn_sched_barrier(0);\n";
+            s += "        kk += " + S + ";\n";
+            s += "    }\n";
             if (singles) s += "    for (; kk + " + one + " <= k1; kk += " + one + ") {\n" + batch(1, false) + "    }\n";
             if (tail) s += "    if (kk < k1) {\n" + batch(1, true) + "    }\n";
             return s;
