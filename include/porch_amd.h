@@ -319,6 +319,15 @@ void porch_event_release(porch_event* event);
  * next kernel finds neither L2 nor the Infinity Cache warm. */
 porch_status porch_flush_caches(size_t bytes);
 
+/* Returns the device memory the allocator keeps cached for reuse (blocks
+ * of released buffers, at most 32 GiB over all streams) to the
+ * stream-ordered pool, each on the stream that last used it; `released`
+ * (may be NULL) receives the bytes.  Live buffers are not touched.
+ * No reference counterpart: for callers under memory pressure (the
+ * reference keeps no cache: each buffer is freed when its last handle
+ * goes, src/cuda_jit.cpp:552-566). */
+porch_status porch_release_cached_memory(size_t* released);
+
 /* ------------------------------------------------------------------ */
 /* Seeded synthetic inputs (host side, splitmix64)                      */
 /* ------------------------------------------------------------------ */

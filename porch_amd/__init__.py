@@ -866,6 +866,13 @@ def jit_stats() -> dict:
     return {name: getattr(s, name) for name, _ in JitStats._fields_}
 
 
+def release_cached_memory() -> int:
+    """Returns the allocator's cached device blocks to the pool; the bytes."""
+    released = ctypes.c_size_t()
+    check(lib.porch_release_cached_memory(ctypes.byref(released)))
+    return released.value
+
+
 def reset_jit_cache() -> None:
     check(lib.porch_reset_jit_cache())
 

@@ -147,6 +147,7 @@ _SIGNATURES = {
     "porch_event_elapsed_ms": (ctypes.c_int32, [_P, _P, ctypes.POINTER(ctypes.c_float)]),
     "porch_event_release": (None, [_P]),
     "porch_flush_caches": (ctypes.c_int32, [ctypes.c_size_t]),
+    "porch_release_cached_memory": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_size_t)]),
     "porch_synth_uniform": (None, [_P, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_double,
                                    ctypes.c_double]),
     "porch_synth_normal": (None, [_P, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_double,

@@ -528,6 +528,13 @@ void porch_event_release(porch_event* event) {
     delete event;
 }
 
+porch_status porch_release_cached_memory(size_t* released) {
+    return guarded([&] {
+        const size_t bytes = hip_jit::is_available() ? rt::release_cached_blocks() : 0;
+        if (released != nullptr) *released = bytes;
+    });
+}
+
 porch_status porch_flush_caches(size_t bytes) {
     return guarded([&] { rt::flush_caches(bytes); });
 }

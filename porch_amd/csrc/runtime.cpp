@@ -519,6 +519,14 @@ namespace porch::rt {
         c.free.erase(list);
     }
 
+    size_t release_cached_blocks() {
+        block_cache& c = blocks();
+        std::scoped_lock lock{c.mutex};
+        const size_t before = c.cached;
+        drain(c);
+        return before - c.cached;
+    }
+
     size_t cached_block_bytes() {
         std::scoped_lock lock{blocks().mutex};
         return blocks().cached;

@@ -65,6 +65,9 @@ namespace porch::rt {
     void release_block(void* ptr, size_t capacity, const stream& s);
     void release_stream_blocks(const stream& s);
     size_t cached_block_bytes();
+    // Returns every cached block to the stream-ordered pool (hipFreeAsync
+    // on its stream); the bytes released.
+    size_t release_cached_blocks();
 
     // Makes `consumer` wait for all work queued so far on `producer`.
     void order_after(const stream& consumer, const stream& producer);

@@ -210,16 +210,24 @@ def test_matches_materialize_on_two_calls(gpu, name):
 
 def test_counts_see_allocations(gpu):
     """The counters the test above relies on move when the runtime
-    allocates: porch_materialize of a fresh large result allocates its
-    output, and a plan compiled for the first time loads a module."""
-    porch.synchronize()
-    before = allocation_calls()
+    allocates: with the allocator's cache emptied (which frees its blocks),
+    porch_materialize of a large result allocates its output, and a plan
+    compiled for the first time loads a module."""
     x = porch.tensor([3, 1 << 22], rand([3, 1 << 22], 51))
+    porch.synchronize()
+    cached = porch.release_cached_memory()
+    before = allocation_calls()
     r = porch.materialize(x * 3.0 + 7.25)
     r.synchronize()
     after = allocation_calls()
     assert after["device_allocs"] > before["device_allocs"], (before, after)
     assert after["module_loads"] > before["module_loads"], (before, after)
+    # releasing the result caches its block; emptying the cache frees it
+    del r
+    porch.synchronize()
+    assert porch.release_cached_memory() >= 3 * 4 * (1 << 22)
+    assert allocation_calls()["device_frees"] > after["device_frees"]
+    assert cached >= 0
 
 
 def test_uses_the_fixed_array_for_temporaries(gpu):
