@@ -5,7 +5,8 @@
 // of 128 x 128 spend most of their work on padding when one side is a few
 // rows or columns.  Two forms instead:
 //
-//   gemm.rows     few rows (m <= 16, n >= 256): one wave per 256 columns
+//   gemm.rows     few rows (m <= 16, n >= 256) where gemm.wide cannot read
+//                 B's rows as float4s: one wave per 256 columns
 //                 of B and a chunk of K, each lane holding m x 4
 //                 accumulators for its four columns, A's values read as
 //                 wave-uniform scalars; the chunks' partial products go to a
@@ -24,10 +25,12 @@
 //                 lane from the L2; partial products of the chunks summed by
 //                 gemm.combine.
 //   gemm.wide     the same blocks the other way round, few rows (up to 64)
-//                 over many columns: one wave per 64 columns and a chunk of
-//                 K, lane l reading B's row k = l / 16 at columns 4 (l % 16)
-//                 .. + 3 with one 128-bit load, so that MFMA e covers the
-//                 16 columns 4 (l % 16) + e; A read per lane from the L2.
+//                 over many columns: a workgroup of four waves per 64
+//                 columns and a chunk of K, the waves taking its groups of
+//                 16 values in turn; lane l reads B's rows at
+//                 columns 4 (l % 16) .. + 3 with 128-bit loads, so that MFMA
+//                 e covers the 16 columns 4 (l % 16) + e, and A's row l % 16
+//                 from the L2; the waves' sums are added through LDS.
 //
 // Sums run in other orders than the reference's sequential K loop, within
 // the matmul's tolerance (an accumulation-bound per element).
@@ -56,16 +59,19 @@ namespace porch::cg {
         // 32 columns: 8.7 us against 12.6 for the split MFMA kernel)
         constexpr int64_t narrow_min_rows = 128;
         constexpr int narrow_depth = 4;           // steps of K whose loads are issued together
-        // gemm.wide from 8 rows (gemm.rows: 19.0 against 22.0 us at 4 rows
-        // of [4096, 4096], 24.0 against 22.4 at 8) to 64 (42.8 against 47.6
-        // us for the split MFMA kernel; the MFMAs, 4 per row block and
-        // 128-bit load of B, take over from there)
-        constexpr int64_t wide_min_rows = 8;
+        // gemm.wide from 1 row (kernel + combine, against gemm.rows: 17.0
+        // against 18.5 us at 1 row of [4096, 4096], 17.2 against 19.6 at 4,
+        // 12.3 against 19.8 at [4, 1024] @ [1024, 16384]) to 64 (27.3 us;
+        // the split MFMA kernel took 47.6, and the MFMAs, 4 per row block
+        // and 128-bit load of B, take over from there); gemm.rows keeps the
+        // products whose B rows are not read as float4s
+        constexpr int64_t wide_min_rows = 1;
         constexpr int64_t wide_max_rows = 64;
-        // steps of 4 values of K whose loads are issued together, in each of
-        // two register sets (one set of 8: 23.0 against 20.1 us on [32,
-        // 4096] @ [4096, 4096])
-        constexpr int wide_depth = 4;
+        // gemm.wide: four waves a workgroup share one 64-column tile and one
+        // chunk of K, taking its groups of 16 values in turn
+        constexpr int64_t wide_waves = 4;
+        constexpr int64_t wide_group = 16;
+        constexpr int wide_depth = 2; // groups in flight per wave
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
 
@@ -186,7 +192,7 @@ namespace porch::cg {
             int64_t rb = 0;     // 16-row MFMA blocks
             int64_t tiles = 0;  // 64-column tiles per batch entry
             int64_t chunks = 0; // K chunks
-            int64_t chunk = 0;  // K per chunk, a multiple of 4 wide_depth
+            int64_t chunk = 0;  // K per chunk, a multiple of 64 (a group per wave)
         };
 
         wide_shape wide_plan(const gemm_request& r) {
@@ -194,12 +200,11 @@ namespace porch::cg {
             if (r.m < wide_min_rows || r.m > wide_max_rows || r.n < 256 || !b_vector(r) || !big_enough(r)) return sh;
             sh.rb = (r.m + 15) / 16;
             sh.tiles = (r.n + 63) / 64;
-            // About four waves per compute unit (two or eight: 6-60 % and
-            // 4-13 % slower on [m, 4096] @ [4096, 4096]), partials (chunks x
-            // m x n) at most 1/4 of B (K x n), at most 32 chunks.
-            const int64_t waves = 4 * std::max(r.compute_units, 8);
-            const int64_t batch_k = 4 * wide_depth;
-            int64_t chunks = (waves + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
+            // About one workgroup (four waves) per compute unit, partials
+            // (chunks x m x n) at most 1/4 of B (K x n), at most 32 chunks.
+            const int64_t cus = std::max(r.compute_units, 8);
+            const int64_t batch_k = wide_waves * wide_group;
+            int64_t chunks = (cus + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / (4 * r.m)));
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / batch_k));
             chunks = std::min<int64_t>(chunks, 32);
@@ -208,9 +213,10 @@ namespace porch::cg {
             sh.chunks = (r.k + chunk - 1) / chunk;
             sh.chunk = chunk;
             // Over 32 rows a wave's 3 or 4 row blocks of MFMAs are long: only
-            // with the full four waves per CU ([48, 2048] @ [2048, 2048] in
-            // 320 waves: 28.9 us against 19.9 for the split MFMA kernel).
-            if (r.m > 32 && r.batch * sh.tiles * sh.chunks < waves) return wide_shape{};
+            // with a workgroup on every CU ([48, 2048] @ [2048, 2048] in
+            // 320 single waves: 28.9 us against 19.9 for the split MFMA
+            // kernel).
+            if (r.m > 32 && r.batch * sh.tiles * sh.chunks < cus) return wide_shape{};
             return sh;
         }
 
@@ -222,7 +228,7 @@ namespace porch::cg {
         using load_text = std::function<std::string(const std::string& set, int D, bool tail, const std::string& kbase,
                                                     const std::string& ind)>;
 
-        // The K loop of gemm.narrow and gemm.wide over [k0, k1): batches of
+        // The K loop of gemm.narrow over [k0, k1): batches of
         // D steps of `step_k` values, each batch's loads issued together
         // ahead of its MFMAs, in two register sets: the next batch's loads
         // are issued before this batch's MFMAs (the last prefetch of a
@@ -230,8 +236,9 @@ namespace porch::cg {
         // loads); then single steps (`singles`) and a partial last step
         // (`tail`).  sched_barrier keeps the loads ahead: left to itself the
         // scheduler sinks each load to its MFMA and waits there.  (Measured
-        // on [32, 4096] @ [4096, 4096]: 20.1 us for batches of 4 steps in
-        // two sets, against 23.0 us for batches of 8 in one.)
+        // with the same loop in an earlier wide-product kernel on [32, 4096]
+        // @ [4096, 4096]: 20.1 us for batches of 4 steps in two sets,
+        // against 23.0 us for batches of 8 in one.)
         std::string batched_k_loop(int D, int64_t step_k, bool singles, bool tail, const set_text& declare,
                                    const load_text& loads, const set_text& mfmas) {
             const std::string in1 = "    ";
@@ -778,38 +785,41 @@ namespace porch::cg {
         const wide_shape sh = wide_plan(r);
         if (sh.rb == 0) throw std::logic_error("emit_gemm_wide: not a wide product");
         const bool final = sh.chunks == 1;
+        const bool avec = a_vector(r);
         const char* T = r.width.type();
         const std::string batch = r.batched ? "qb" : "";
         const std::string M = std::to_string(r.m);
         const std::string N = std::to_string(r.n);
         const std::string K = std::to_string(r.k);
         const std::string RB = std::to_string(sh.rb);
-        const int64_t tiles = r.batch * sh.tiles;
-        const int64_t waves = tiles * sh.chunks;
+        const std::string CH = std::to_string(sh.chunks);
+        const std::string CK = std::to_string(sh.chunk);
 
         kernel_code kc;
         kc.kind = "gemm.wide";
         kc.name = "porch_gemm";
         kc.n_slots = r.n_slots;
-        kc.block = 256;
-        kc.grid_x = static_cast<unsigned>((waves + 3) / 4);
+        kc.block = 64 * wide_waves;
+        kc.grid_x = static_cast<unsigned>(r.batch * sh.tiles * sh.chunks);
 
         std::string& s = kc.source;
         s = kernel_prologue(r.n_slots, T);
         s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" + kernel_params(r.n_slots) + ") {\n";
         s += "    const int lane = threadIdx.x & 63;\n";
+        // the wave's index, known to the compiler as uniform: the loop over
+        // the wave's groups branches on scalars (as a vector value the loop
+        // was masked per lane and every wait drained all loads)
+        s += "    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n";
         s += "    const int li = lane & 15;\n    const int lg = lane >> 4;\n";
-        // waves of one chunk are adjacent: they share its columns of A
-        s += "    const idx_t wid = (idx_t)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
-        s += "    if (wid >= " + std::to_string(waves) + ") return;\n";
-        s += "    const idx_t ks = wid / " + std::to_string(tiles) + ";\n";
-        s += "    const idx_t tile = wid % " + std::to_string(tiles) + ";\n";
+        // the chunks of a tile are adjacent workgroups: the workgroups of one
+        // chunk (which share its columns of A) land on the same XCDs
+        s += "    const idx_t ks = (idx_t)blockIdx.x % " + CH + ";\n";
+        s += "    const idx_t tile = (idx_t)blockIdx.x / " + CH + ";\n";
         s += "    const idx_t qb = tile / " + std::to_string(sh.tiles) + ";\n";
         if (!r.batched) s += "    (void)qb;\n";
         s += "    const idx_t c0 = (tile % " + std::to_string(sh.tiles) + ") * 64;\n";
-        s += "    const idx_t k0 = ks * " + std::to_string(sh.chunk) + ";\n";
-        s += "    const idx_t k1 = k0 + " + std::to_string(sh.chunk) + " < " + K + " ? k0 + " +
-             std::to_string(sh.chunk) + " : (idx_t)" + K + ";\n";
+        s += "    const idx_t k0 = ks * " + CK + ";\n";
+        s += "    const idx_t k1 = k0 + " + CK + " < " + K + " ? k0 + " + CK + " : (idx_t)" + K + ";\n";
         // acc[i][e]: rows 16 i + 4 (l / 16) + v, column c0 + 4 (l % 16) + e
         s += "    porch_v4f acc[" + RB + "][4];\n";
         s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
@@ -822,61 +832,145 @@ namespace porch::cg {
         s += "        qa[i] = q0 < " + M + " ? q0 : (idx_t)" + std::to_string(r.m - 1) + ";\n";
         s += "    }\n";
         s += "    const idx_t qc = c0 + li * 4 < " + N + " ? c0 + li * 4 : (idx_t)" + std::to_string(r.n - 4) + ";\n";
-        // One step: 4 values of K, lane l holding k = kbase + l / 16.  In
-        // the tail, lanes past K read its last value and zero both
-        // operands.
+        // A group: 16 values of K from kq.  MFMA j of the group gives lane l
+        // k = kq + 4 (l / 16) + j: B's row there at columns qc .. qc + 3 (one
+        // 128-bit load a j: 4 rows x 256 B an instruction; MFMA e takes
+        // value e, the 16 columns 4 (l % 16) + e), and A's row qa[i] at the
+        // four k of the lane (one 128-bit load where A's rows run along K).
         const std::string aslot = "a" + std::to_string(r.a.slot);
         const std::string bslot = "a" + std::to_string(r.b.slot);
-        const set_text declare = [&](const std::string& set, int D, const std::string& ind) {
-            const std::string Ds = std::to_string(D);
-            return ind + "porch_v4f bv" + set + "[" + Ds + "];\n" + ind + "float av" + set + "[" + Ds + "][" + RB + "];\n";
+        auto declare = [&](const std::string& set, const std::string& ind) {
+            return ind + "porch_v4f bv" + set + "[4];\n" + ind + "porch_v4f av" + set + "[" + RB + "];\n";
         };
-        const load_text loads = [&](const std::string& set, int D, bool tail, const std::string& kbase,
-                                    const std::string& ind) {
+        auto loads = [&](const std::string& set, const std::string& kq, const std::string& ind) {
             std::string t;
-            const std::string av = "av" + set, bv = "bv" + set;
-            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d) {\n";
-            t += ind + "    const idx_t kq = " + kbase + " + d * 4 + lg;\n";
-            if (tail) {
-                t += ind + "    const bool kin = kq < k1;\n";
-                t += ind + "    const idx_t kr = kin ? kq : k1 - 1;\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < 4; ++j)\n";
+            t += ind + "    bv" + set + "[j] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot +
+                 " + " + operand_index(r.b, "(" + kq + " + lg * 4 + j)", "qc", batch) + "));\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int i = 0; i < " + RB + "; ++i) {\n";
+            if (avec) {
+                t += ind + "    av" + set + "[i] = *reinterpret_cast<const porch_v4f*>(" + aslot + " + " +
+                     operand_index(r.a, "qa[i]", "(" + kq + " + lg * 4)", batch) + ");\n";
             }
-            const std::string kr = tail ? "kr" : "kq";
-            t += ind + "    " + bv + "[d] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
-                 operand_index(r.b, kr, "qc", batch) + "));\n";
-            if (tail) t += ind + "    if (!kin) " + bv + "[d] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
-            t += ind + "    #pragma unroll\n" + ind + "    for (int i = 0; i < " + RB + "; ++i) {\n";
-            t += ind + "        const idx_t q0 = qa[i];\n";
-            t += ind + "        " + av + "[d][i] = " + aslot + "[" + operand_index(r.a, "q0", kr, batch) + "];\n";
-            if (tail) t += ind + "        if (!kin) " + av + "[d][i] = 0.0f;\n";
-            t += ind + "    }\n" + ind + "}\n";
+            else {
+                t += ind + "    #pragma unroll\n" + ind + "    for (int j = 0; j < 4; ++j)\n";
+                t += ind + "        av" + set + "[i][j] = " + aslot + "[" +
+                     operand_index(r.a, "qa[i]", "(" + kq + " + lg * 4 + j)", batch) + "];\n";
+            }
+            t += ind + "}\n";
             return t;
         };
-        const set_text mfmas = [&](const std::string& set, int D, const std::string& ind) {
+        auto mfmas = [&](const std::string& set, const std::string& ind) {
             std::string t;
-            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d)\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < 4; ++j)\n";
             t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
             t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
-            t += ind + "            acc[i][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[d][i], bv" + set +
-                 "[d][e], acc[i][e], 0, 0, 0);\n";
+            t += ind + "            acc[i][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[i][j], bv" + set +
+                 "[j][e], acc[i][e], 0, 0, 0);\n";
             return t;
         };
-        s += batched_k_loop(wide_depth, 4, r.k % (4 * wide_depth) != 0, r.k % 4 != 0, declare, loads, mfmas);
-        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
-        s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e)\n";
-        s += "            #pragma unroll\n            for (int v = 0; v < 4; ++v) {\n";
-        s += "                const idx_t q0 = i * 16 + lg * 4 + v;\n";
-        s += "                const idx_t q1 = c0 + li * 4 + e;\n";
-        s += "                if (q0 < " + M + " && q1 < " + N + ") {\n";
-        const std::string o = std::string(r.batched ? "(qb * " + M + " + q0)" : "q0") + " * " + N + " + q1";
-        if (final) {
-            s += "                    const float acc_v = acc[i][e][v];\n";
-            s += epilogue_store(r, "acc_v", o, "                    ");
+        // The chunk's full groups go to the waves in turn (wave w: groups w,
+        // w + 4, ...), so the four waves read 64 adjacent rows at a time.
+        // Each wave keeps two groups' loads in flight: the next group's
+        // loads are issued before this group's MFMAs.  The loop takes the
+        // groups in pairs with no exit in between (with a break after the
+        // first half the compiler sank the second set's loads below the
+        // first set's MFMAs); the last prefetch of a wave with an even
+        // count reloads its own last group: in bounds, no branch around the
+        // loads.
+        // Measured on [32, 4096] @ [4096, 4096], 4 chunks of 1024: 14.4 us,
+        // against 22.7 us for one wave per tile and chunk (16 chunks) with
+        // A read a value a lane; eight or sixteen waves a workgroup 17.5 and
+        // 21.7 us, three groups in flight 15.6 us.
+        const std::string G16 = std::to_string(wide_group);
+        // Where every chunk is whole, every wave has the same compile-time
+        // count of groups and the loop is written out (no loop-carried copy
+        // of the accumulators, which the compiler's register assignment
+        // for the rolled loop adds at each turn), wide_depth groups in
+        // flight.
+        const int64_t per_wave = r.k % sh.chunk == 0 ? sh.chunk / (wide_waves * wide_group) : 0;
+        if (per_wave > 0 && per_wave <= 32) {
+            auto set_of = [](int64_t t) { return "S" + std::to_string(t % wide_depth); };
+            auto load_group = [&](int64_t t) {
+                return "    {\n        const idx_t kq = k0 + " + G16 + " * w + " +
+                       std::to_string(t * wide_waves * wide_group) + ";\n" + loads(set_of(t), "kq", "        ") + "    }\n";
+            };
+            for (int d = 0; d < wide_depth; ++d) s += declare(set_of(d), "    ");
+            for (int64_t t = 0; t + 1 < wide_depth && t < per_wave; ++t) s += load_group(t);
+            for (int64_t t = 0; t < per_wave; ++t) {
+                if (t + wide_depth - 1 < per_wave) s += load_group(t + wide_depth - 1);
+                s += "    __builtin_amdgcn_sched_barrier(0);\n" + mfmas(set_of(t), "    ") +
+                     "    __builtin_amdgcn_sched_barrier(0);\n";
+            }
         }
         else {
-            s += "                    out[ks * " + std::to_string(r.batch * r.m * r.n) + " + " + o + "] = acc[i][e][v];\n";
+            s += declare("P", "    ") + declare("Q", "    ");
+            s += "    const idx_t full = (k1 - k0) / " + G16 + ";\n";
+            s += "    const idx_t nf = full > w ? (full - w + 3) / 4 : 0;\n";
+            s += "    if (nf > 0) {\n        const idx_t kq = k0 + " + G16 + " * w;\n" + loads("P", "kq", "        ") + "    }\n";
+            s += "    idx_t t = 0;\n";
+            s += "    for (; t + 2 <= nf; t += 2) {\n";
+            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 1));\n" +
+                 loads("Q", "kq", "            ") + "        }\n";
+            s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("P", "        ") +
+                 "        __builtin_amdgcn_sched_barrier(0);\n";
+            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 2 < nf ? t + 2 : t + 1));\n" +
+                 loads("P", "kq", "            ") + "        }\n";
+            s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("Q", "        ") +
+                 "        __builtin_amdgcn_sched_barrier(0);\n";
+            s += "    }\n";
+            s += "    if (t < nf) {\n" + mfmas("P", "        ") + "    }\n";
         }
-        s += "                }\n            }\n}\n";
+        // The partial last group (a chunk not a multiple of 16 values), in
+        // the wave whose turn it is: lanes past the chunk read its last
+        // value and zero both operands.
+        if (sh.chunk % wide_group != 0 || r.k % wide_group != 0) {
+            s += "    if (full * " + G16 + " < k1 - k0 && full % 4 == w) {\n";
+            s += "        const idx_t kq = k0 + full * " + G16 + ";\n";
+            s += declare("R", "        ");
+            s += "        #pragma unroll\n        for (int j = 0; j < 4; ++j) {\n";
+            s += "            const idx_t kb = kq + lg * 4 + j;\n";
+            s += "            const bool kin = kb < k1;\n";
+            s += "            const idx_t kr = kin ? kb : k1 - 1;\n";
+            s += "            bvR[j] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                 operand_index(r.b, "kr", "qc", batch) + "));\n";
+            s += "            if (!kin) bvR[j] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+            s += "            #pragma unroll\n            for (int i = 0; i < " + RB + "; ++i) {\n";
+            s += "                const float x = " + aslot + "[" + operand_index(r.a, "qa[i]", "kr", batch) + "];\n";
+            s += "                avR[i][j] = kin ? x : 0.0f;\n";
+            s += "            }\n        }\n";
+            s += mfmas("R", "        ");
+            s += "    }\n";
+        }
+        // The waves' sums, added in wave order through LDS; each thread
+        // then holds four adjacent columns of one row.
+        s += "    __shared__ porch_v4f red[4][" + std::to_string(4 * sh.rb) + "][64];\n";
+        s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
+        s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) red[w][i * 4 + e][lane] = acc[i][e];\n";
+        s += "    __syncthreads();\n";
+        s += "    for (int t = threadIdx.x; t < " + std::to_string(256 * sh.rb) + "; t += 256) {\n";
+        s += "        const int i = t >> 8, v = (t >> 6) & 3, l = t & 63;\n";
+        s += "        const idx_t q0 = i * 16 + (l >> 4) * 4 + v;\n";
+        s += "        const idx_t qc4 = c0 + (l & 15) * 4;\n";
+        s += "        if (q0 < " + M + " && qc4 < " + N + ") {\n";
+        s += "            porch_v4f sum;\n";
+        s += "            #pragma unroll\n            for (int e = 0; e < 4; ++e) {\n";
+        s += "                float x = red[0][i * 4 + e][l][v];\n";
+        s += "                #pragma unroll\n                for (int u = 1; u < 4; ++u) x += red[u][i * 4 + e][l][v];\n";
+        s += "                sum[e] = x;\n            }\n";
+        const std::string row = r.batched ? "(qb * " + M + " + q0)" : "q0";
+        if (final) {
+            s += "            #pragma unroll\n            for (int e = 0; e < 4; ++e) {\n";
+            s += "                const idx_t q1 = qc4 + e;\n";
+            s += "                const float acc_v = sum[e];\n";
+            s += epilogue_store(r, "acc_v", row + " * " + N + " + q1", "                ");
+            s += "            }\n";
+        }
+        else {
+            s += "            *reinterpret_cast<porch_v4f*>(out + ks * " + std::to_string(r.batch * r.m * r.n) + " + " + row +
+                 " * " + N + " + qc4) = sum;\n";
+        }
+        s += "        }\n    }\n}\n";
         return kc;
     }
 

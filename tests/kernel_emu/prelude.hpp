@@ -175,6 +175,8 @@ namespace emu {
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
 #define __builtin_amdgcn_sched_barrier(a) ((void)0)
 #define __builtin_amdgcn_wave_barrier() emu::wave_sync()
+// the kernels read only wave-uniform values through it
+#define __builtin_amdgcn_readfirstlane(x) (x)
 #define __builtin_amdgcn_s_sleep(n) std::this_thread::yield()
 #define __HIP_MEMORY_SCOPE_AGENT 0
 #define __hip_atomic_load(p, order, scope) __atomic_load_n((p), (order))

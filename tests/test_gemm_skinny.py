@@ -46,12 +46,15 @@ def _reals(shape, seed):
 CASES = {
     "vector times matrix": (
         ([1, 4096], [4096, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
-        ["gemm.rows", "gemm.combine"]),
+        ["gemm.wide", "gemm.combine"]),
     "eight rows, relu epilogue": (
         ([8, 2048], [2048, 1024]), lambda a, b: porch.relu(porch.matmul(a, b) - 1.0), lambda a, b: a @ b,
         lambda p: np.maximum(p - 1.0, 0.0), ["gemm.wide", "gemm.combine"]),
     "seven rows, relu epilogue": (
         ([7, 2048], [2048, 1024]), lambda a, b: porch.relu(porch.matmul(a, b) - 1.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p - 1.0, 0.0), ["gemm.wide", "gemm.combine"]),
+    "seven rows, columns not a multiple of four, relu epilogue": (
+        ([7, 2048], [2048, 1022]), lambda a, b: porch.relu(porch.matmul(a, b) - 1.0), lambda a, b: a @ b,
         lambda p: np.maximum(p - 1.0, 0.0), ["gemm.rows", "gemm.combine"]),
     "wide, thirty-two rows": (
         ([32, 1024], [1024, 4096]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
@@ -62,6 +65,12 @@ CASES = {
     "wide, one chunk, epilogue in the kernel": (
         ([32, 100], [100, 256]), lambda a, b: porch.matmul(a, b) * 0.5 - 1.0, lambda a, b: a @ b,
         lambda p: p * 0.5 - 1.0, ["gemm.wide"]),
+    "wide, two groups a wave, written out": (
+        ([32, 512], [512, 1024]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.wide", "gemm.combine"]),
+    "wide, four groups a wave, written out, relu": (
+        ([32, 2048], [2048, 2048]), lambda a, b: porch.relu(porch.matmul(a, b) - 2.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p - 2.0, 0.0), ["gemm.wide", "gemm.combine"]),
     "wide, batched": (
         ([2, 24, 516], [2, 516, 512]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.wide", "gemm.combine"]),
@@ -75,11 +84,17 @@ CASES = {
         ([2, 1024], [3000, 1024]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
         lambda p: p, ["gemm.rows", "gemm.combine"]),
     "rows, batched": (
-        ([4, 3, 512], [4, 512, 1024]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ([4, 3, 512], [4, 512, 1022]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.rows", "gemm.combine"]),
+    "wide, three rows, batched": (
+        ([4, 3, 512], [4, 512, 1024]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.wide", "gemm.combine"]),
     "rows, one chunk": (
-        ([2, 64], [64, 4096]), lambda a, b: porch.matmul(a, b) * 0.5, lambda a, b: a @ b, lambda p: p * 0.5,
+        ([2, 64], [64, 4094]), lambda a, b: porch.matmul(a, b) * 0.5, lambda a, b: a @ b, lambda p: p * 0.5,
         ["gemm.rows"]),
+    "wide, two rows, one chunk": (
+        ([2, 64], [64, 4096]), lambda a, b: porch.matmul(a, b) * 0.5, lambda a, b: a @ b, lambda p: p * 0.5,
+        ["gemm.wide"]),
     "matrix times vector": (
         ([4096, 4096], [4096, 1]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.cols"]),
@@ -189,7 +204,8 @@ def test_split_k_chunks(shape, chunks):
 BIAS_SHAPES = {
     (4096, 2048, 16): ["gemm.narrow_rows"],
     (8, 2048, 1024): ["gemm.wide", "gemm.combine"],
-    (4, 2048, 1024): ["gemm.rows", "gemm.combine"],
+    (4, 2048, 1024): ["gemm.wide", "gemm.combine"],
+    (4, 2048, 1022): ["gemm.rows", "gemm.combine"],
     (40, 1030, 200): ["gemm.mfma", "gemm.combine"],
     (3000, 300, 2): ["gemm.cols"],
 }
@@ -230,7 +246,8 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "narrow, one chunk, epilogue in the kernel", "narrow, batched, ragged row tiles",
                                   "narrow, transposed B", "narrow rows, ragged rows and columns, K tail, relu",
                                   "wide, ragged rows and columns, K tail, relu",
-                                  "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A"])
+                                  "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A",
+                                  "wide, two groups a wave, written out"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
     xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
@@ -355,9 +372,9 @@ def test_narrow_infinities_in_the_k_tail(gpu):
 
 
 @pytest.mark.parametrize("shape, chunks", [
-    ((32, 4096, 4096), 16),  # 64 column tiles: 16 chunks for four waves a CU
+    ((32, 4096, 4096), 4),   # 64 column tiles: 4 chunks for a workgroup a CU
     ((20, 203, 300), 2),     # partials at most 1/4 of B: 203 / (4 x 20) chunks
-    ((8, 8192, 256), 32),    # 4 column tiles: 256 chunks for the waves, at most 32
+    ((8, 8192, 256), 32),    # 4 column tiles: 64 chunks for the CUs, at most 32
     ((32, 100, 256), 1),     # too short a K to split: the epilogue in the kernel
 ])
 def test_wide_chunks(shape, chunks):
@@ -365,21 +382,25 @@ def test_wide_chunks(shape, chunks):
     plan = porch.plan(porch.matmul(placeholder([m, k]), placeholder([k, n])))
     kinds = [x["kind"] for x in plan["kernels"]]
     assert kinds == (["gemm.wide", "gemm.combine"] if chunks > 1 else ["gemm.wide"])
-    waves = -(-n // 64) * chunks
-    assert plan["kernels"][0]["grid"][0] == -(-waves // 4)
+    # one workgroup of four waves per 64-column tile and chunk
+    assert plan["kernels"][0]["grid"][0] == -(-n // 64) * chunks
+    assert plan["kernels"][0]["block"] == 256
     assert plan["temps"] == ([chunks * m * n] if chunks > 1 else [])
 
 
 def test_wide_bounds():
-    # from 8 to 32 rows over 256 columns or more (64 with enough waves), B's
-    # rows read as float4s
-    assert _kinds(porch.matmul(placeholder([7, 4096]), placeholder([4096, 4096])))[0] == "gemm.rows"
+    # from 1 to 32 rows over 256 columns or more (64 with enough
+    # workgroups), B's rows read as float4s
+    assert _kinds(porch.matmul(placeholder([1, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([7, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([7, 4096]), placeholder([4096, 4094])))[0] == "gemm.rows"
     assert _kinds(porch.matmul(placeholder([8, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
     assert _kinds(porch.matmul(placeholder([64, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
     assert _kinds(porch.matmul(placeholder([65, 4096]), placeholder([4096, 4096])))[0] == "gemm.mfma"
-    # over 32 rows only with four waves per CU (64 tiles x 16 chunks here, 32 x 10 below)
+    # over 32 rows only with a workgroup for every CU (64 tiles x 4 chunks,
+    # 32 x 8, then 16 x 2 below)
     assert _kinds(porch.matmul(placeholder([48, 4096]), placeholder([4096, 4096])))[0] == "gemm.wide"
-    assert _kinds(porch.matmul(placeholder([48, 2048]), placeholder([2048, 2048])))[0] == "gemm.mfma"
+    assert _kinds(porch.matmul(placeholder([48, 2048]), placeholder([2048, 2048])))[0] == "gemm.wide"
     assert _kinds(porch.matmul(placeholder([64, 512]), placeholder([512, 1024])))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([32, 4096]), placeholder([4096, 252])))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([16, 4096]), placeholder([4096, 254])))[0] == "gemm.mfma"
