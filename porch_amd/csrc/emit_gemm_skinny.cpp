@@ -132,22 +132,30 @@ namespace porch::cg {
             int64_t chunk = 0;  // K per chunk, a multiple of 16
         };
 
-        // gemm.narrow_rows: 7 to 16 columns, one workgroup of 8 waves per
-        // 16 rows of A over all of K (no partial products, no combine).
-        // Each wave takes K / 8 values in rounds of 256: the 16 rows'
-        // values are read as one 1 KB run per row (a float4 a lane),
-        // written to the wave's own area of LDS and read back in the MFMA
-        // layout; the next round's rows are loaded during this round.  At
-        // least one workgroup per compute unit, and K long enough for a
-        // full round per wave (measured on [4096, 4096] @ [4096, 16]:
-        // 16.0 us, against 16.7 + 4.5 us for gemm.narrow and its combine).
-        constexpr int64_t rows_waves = 8;
+        // gemm.narrow_rows: 7 to 16 columns, one workgroup of 8 (or 4)
+        // waves per 16 rows of A over all of K (no partial products, no
+        // combine).  Each wave takes K / 8 values in rounds of 256 (64
+        // lanes x a float4): the 16 rows' values are read as one 1 KB run
+        // per row, written to the wave's own area of LDS and read back in
+        // the MFMA layout; the next round's rows are loaded during this
+        // round.  At least one workgroup per compute unit, and K long
+        // enough for a full round per wave (measured on [4096, 4096] @
+        // [4096, 16]: 16.0 us, against 16.7 + 4.5 us for gemm.narrow and its
+        // combine).  The rounds are written out: past two rounds a wave of
+        // eight no longer fits the register budget of two waves per SIMD
+        // (spills: 42.6 us at [4096, 8192] @ [8192, 16]), so longer K takes
+        // four waves a workgroup (28.3 us there; at K = 4096 four waves are
+        // 3-7 % slower than eight), up to 16 rounds a wave.
         constexpr int64_t rows_round = 256;
         constexpr int64_t rows_stride = rows_round + 4; // LDS row, floats
+        constexpr int64_t rows_max_rounds = 16;
+
+        int64_t rows_waves(const gemm_request& r) { return r.k <= 8 * 2 * rows_round ? 8 : 4; }
 
         bool narrow_rows(const gemm_request& r) {
             return r.n >= narrow_min_cols && r.n <= 16 && a_vector(r) && big_enough(r) &&
-                   r.batch * ((r.m + 15) / 16) >= std::max(r.compute_units, 8) && r.k >= rows_waves * rows_round;
+                   r.batch * ((r.m + 15) / 16) >= std::max(r.compute_units, 8) && r.k >= 8 * rows_round &&
+                   r.k <= 4 * rows_max_rounds * rows_round;
         }
 
         narrow_shape narrow_plan(const gemm_request& r) {
@@ -502,7 +510,8 @@ namespace porch::cg {
             const int64_t row_tiles = (r.m + 15) / 16;
             // K per wave: a multiple of 4, so a float4 never straddles a
             // wave's end
-            const int64_t kw = (r.k + 4 * rows_waves - 1) / (4 * rows_waves) * 4;
+            const int64_t waves = rows_waves(r);
+            const int64_t kw = (r.k + 4 * waves - 1) / (4 * waves) * 4;
             const int64_t rounds = (kw + rows_round - 1) / rows_round;
             const std::string KW = std::to_string(kw);
             const std::string RS = std::to_string(rows_stride);
@@ -511,7 +520,7 @@ namespace porch::cg {
             kc.kind = "gemm.narrow_rows";
             kc.name = "porch_gemm";
             kc.n_slots = r.n_slots;
-            kc.block = static_cast<unsigned>(64 * rows_waves);
+            kc.block = static_cast<unsigned>(64 * waves);
             kc.grid_x = static_cast<unsigned>(r.batch * row_tiles);
 
             const std::string aslot = "a" + std::to_string(r.a.slot);
@@ -521,7 +530,7 @@ namespace porch::cg {
             s += "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(kc.block) + ") porch_gemm(" +
                  kernel_params(r.n_slots) + ") {\n";
             // each wave's own area: 16 rows of a round, rows padded by 16 bytes
-            s += "    __shared__ __attribute__((aligned(16))) float stage[" + std::to_string(rows_waves) + "][16 * " + RS +
+            s += "    __shared__ __attribute__((aligned(16))) float stage[" + std::to_string(waves) + "][16 * " + RS +
                  "];\n";
             s += "    const int lane = threadIdx.x & 63;\n";
             s += "    const int li = lane & 15;\n    const int lg = lane >> 4;\n";
@@ -638,7 +647,7 @@ namespace porch::cg {
             s += "    red[w * 64 + lane] = acc;\n";
             s += "    __syncthreads();\n";
             s += "    if (w != 0) return;\n";
-            s += "    #pragma unroll\n    for (int q = 1; q < " + std::to_string(rows_waves) + "; ++q) acc += red[q * 64 + lane];\n";
+            s += "    #pragma unroll\n    for (int q = 1; q < " + std::to_string(waves) + "; ++q) acc += red[q * 64 + lane];\n";
             // accumulator value v of lane l: row 4 (l / 16) + v, column l % 16
             s += "    #pragma unroll\n    for (int v = 0; v < 4; ++v) {\n";
             s += "        const idx_t q0 = r0 + lg * 4 + v;\n";

@@ -134,6 +134,12 @@ CASES = {
     "narrow rows, batched": (
         ([2, 2048, 2048], [2, 2048, 16]), lambda a, b: porch.batched_matmul(a, b) + 1.0, lambda a, b: a @ b,
         lambda p: p + 1.0, ["gemm.narrow_rows"]),
+    "narrow rows, four waves, K tail": (
+        ([4096, 4104], [4104, 9]), lambda a, b: porch.matmul(a, b) * 0.5, lambda a, b: a @ b, lambda p: p * 0.5,
+        ["gemm.narrow_rows"]),
+    "narrow rows, four waves, eight rounds, relu": (
+        ([4096, 8196], [8196, 11]), lambda a, b: porch.relu(porch.matmul(a, b) + 1.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p + 1.0, 0.0), ["gemm.narrow_rows"]),
     "narrow rows, transposed B": (
         ([4096, 3000], [9, 3000]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
         lambda p: p, ["gemm.narrow_rows"]),
@@ -245,6 +251,7 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "narrow, ragged rows and columns, K tail, relu",
                                   "narrow, one chunk, epilogue in the kernel", "narrow, batched, ragged row tiles",
                                   "narrow, transposed B", "narrow rows, ragged rows and columns, K tail, relu",
+                                  "narrow rows, four waves, K tail",
                                   "wide, ragged rows and columns, K tail, relu",
                                   "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A",
                                   "wide, two groups a wave, written out"])
@@ -319,16 +326,18 @@ def test_narrow_chunks(shape, chunks):
     assert plan["temps"] == ([chunks * m * n] if chunks > 1 else [])
 
 
-@pytest.mark.parametrize("shape, batch", [((4096, 4096, 16), 1), ((4090, 2100, 13), 1), ((2048, 2048, 16), 2)])
+@pytest.mark.parametrize("shape, batch", [((4096, 4096, 16), 1), ((4090, 2100, 13), 1), ((2048, 2048, 16), 2),
+                                          ((4096, 8192, 16), 1), ((4096, 16384, 7), 1)])
 def test_narrow_rows_plan(shape, batch):
-    # one workgroup of 8 waves per 16 rows (over all batch entries), no
-    # partial products
+    # one workgroup per 16 rows (over all batch entries), no partial
+    # products: 8 waves while each takes at most two rounds of 256 values
+    # of K, else 4
     m, k, n = shape
     a, b = placeholder([batch, m, k] if batch > 1 else [m, k]), placeholder([batch, k, n] if batch > 1 else [k, n])
     plan = porch.plan(porch.batched_matmul(a, b) if batch > 1 else porch.matmul(a, b))
     assert [x["kind"] for x in plan["kernels"]] == ["gemm.narrow_rows"]
     assert plan["kernels"][0]["grid"][0] == batch * -(-m // 16)
-    assert plan["kernels"][0]["block"] == 512
+    assert plan["kernels"][0]["block"] == (512 if k <= 4096 else 256)
     assert plan["temps"] == []
 
 
@@ -344,6 +353,9 @@ def test_narrow_bounds():
     assert _kinds(porch.matmul(placeholder([4081, 4096]), placeholder([4096, 16])))[0] == "gemm.narrow_rows"
     assert _kinds(porch.matmul(placeholder([4096, 2044]), placeholder([2044, 16])))[0] == "gemm.narrow"
     assert _kinds(porch.matmul(placeholder([4096, 2048]), placeholder([2048, 16])))[0] == "gemm.narrow_rows"
+    # at most 16 rounds of 256 values a wave (four waves): K up to 16384
+    assert _kinds(porch.matmul(placeholder([4096, 16384]), placeholder([16384, 16])))[0] == "gemm.narrow_rows"
+    assert _kinds(porch.matmul(placeholder([4096, 16388]), placeholder([16388, 16])))[0] == "gemm.narrow"
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 32])))[0] == "gemm.narrow"
     assert _kinds(porch.matmul(placeholder([4096, 4096]), placeholder([4096, 33])))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([128, 4096]), placeholder([4096, 16])))[0] == "gemm.narrow"
