@@ -18,11 +18,13 @@
 //                 each load of B), lanes along K reading A with 128-bit
 //                 loads, n accumulators per row and lane and a butterfly
 //                 per output.
-//   gemm.narrow   7 to 32 columns over 128 rows or more: one wave per 32 rows and
-//                 a chunk of K, v_mfma_f32_16x16x4f32 blocks fed straight
-//                 from 128-bit loads of A (lane l reads row l % 16, k in
-//                 4 (l / 16) .. +3, one MFMA per k of the four), B read per
-//                 lane from the L2; partial products of the chunks summed by
+//   gemm.narrow   7 to 32 columns over 128 rows or more: a workgroup of
+//                 four waves per 32 rows and a chunk of K, the waves taking
+//                 its groups of 16 values in turn; v_mfma_f32_16x16x4f32
+//                 blocks fed straight from 128-bit loads of A (lane l reads
+//                 row l % 16, k in 4 (l / 16) .. +3, one MFMA per k of the
+//                 four), B read per lane from the L2; the waves' sums added
+//                 through LDS, the chunks' partial products summed by
 //                 gemm.combine.
 //   gemm.wide     the same blocks the other way round, few rows (up to 64)
 //                 over many columns: a workgroup of four waves per 64
@@ -58,7 +60,6 @@ namespace porch::cg {
         // rows of A over all batch entries (at 128 rows of 4096 x 4096 with
         // 32 columns: 8.7 us against 12.6 for the split MFMA kernel)
         constexpr int64_t narrow_min_rows = 128;
-        constexpr int narrow_depth = 4;           // steps of K whose loads are issued together
         // gemm.wide from 1 row (kernel + combine, against gemm.rows: 17.0
         // against 18.5 us at 1 row of [4096, 4096], 17.2 against 19.6 at 4,
         // 12.3 against 19.8 at [4, 1024] @ [1024, 16384]) to 64 (27.3 us;
@@ -67,11 +68,11 @@ namespace porch::cg {
         // products whose B rows are not read as float4s
         constexpr int64_t wide_min_rows = 1;
         constexpr int64_t wide_max_rows = 64;
-        // gemm.wide: four waves a workgroup share one 64-column tile and one
-        // chunk of K, taking its groups of 16 values in turn
-        constexpr int64_t wide_waves = 4;
-        constexpr int64_t wide_group = 16;
-        constexpr int wide_depth = 2; // groups in flight per wave
+        // gemm.wide and gemm.narrow: four waves a workgroup share one tile
+        // and one chunk of K, taking its groups of 16 values in turn
+        constexpr int64_t group_waves = 4;
+        constexpr int64_t group_size = 16;
+        constexpr int group_depth = 2; // groups in flight per wave
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
 
@@ -174,18 +175,14 @@ namespace porch::cg {
             sh.rb = 2;
             sh.nb = (r.n + 15) / 16;
             sh.tiles = (r.m + 16 * sh.rb - 1) / (16 * sh.rb);
-            // About four waves per compute unit (measured on [4096, 4096]
-            // @ [4096, n], n = 4 .. 32: 20.0-24.1 us with the combine, 19.6-
-            // 27.4 at eight, 21.7-38.1 at sixteen); the partial products
-            // (chunks x m x n) at most 1/4 of A (m x K) and at most 32
-            // chunks (on 128 to 1024 rows: 1/16 of A left too few waves,
-            // [256, 4096] @ [4096, 32] 17.9 us against 8.7, and 64 chunks
-            // made the combine dear, 4.9 us at [512, 4096] @ [4096, 16]);
-            // chunks a multiple of the loop's 64 values of K (10 chunks of
-            // 416 at n = 24: 33.7 us, against 19.6 with 8 of 512).
-            const int64_t waves = 4 * std::max(r.compute_units, 8);
-            const int64_t batch_k = 16 * narrow_depth;
-            int64_t chunks = (waves + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
+            // One workgroup (four waves) per 32-row tile and chunk of K, about
+            // one workgroup per compute unit; the partial products (chunks x
+            // m x n) at most 1/4 of A (m x K) and at most 32 chunks (64
+            // chunks made the combine dear, 4.9 us at [512, 4096] @ [4096,
+            // 16]); chunks a multiple of the waves' 64 values of K.
+            const int64_t cus = std::max(r.compute_units, 8);
+            const int64_t batch_k = group_waves * group_size;
+            int64_t chunks = (cus + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / (4 * r.n)));
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / batch_k));
             chunks = std::min<int64_t>(chunks, 32);
@@ -211,7 +208,7 @@ namespace porch::cg {
             // About one workgroup (four waves) per compute unit, partials
             // (chunks x m x n) at most 1/4 of B (K x n), at most 32 chunks.
             const int64_t cus = std::max(r.compute_units, 8);
-            const int64_t batch_k = wide_waves * wide_group;
+            const int64_t batch_k = group_waves * group_size;
             int64_t chunks = (cus + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / (4 * r.m)));
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / batch_k));
@@ -228,57 +225,69 @@ namespace porch::cg {
             return sh;
         }
 
-        // Emitted code, at indent `ind`, for operand register set `set`
-        // (names suffixed with it) holding D steps.
-        using set_text = std::function<std::string(const std::string& set, int D, const std::string& ind)>;
-        // ... loading D steps from K offset `kbase` (`tail`: the last,
-        // partial step, lanes past K zeroing both operands).
-        using load_text = std::function<std::string(const std::string& set, int D, bool tail, const std::string& kbase,
-                                                    const std::string& ind)>;
+        // Emitted code, at indent `ind`, for operand register set `set` of
+        // one group ...
+        using group_text = std::function<std::string(const std::string& set, const std::string& ind)>;
+        // ... loading the group of 16 values of K from `kq` into it.
+        using group_load_text =
+            std::function<std::string(const std::string& set, const std::string& kq, const std::string& ind)>;
 
-        // The K loop of gemm.narrow over [k0, k1): batches of
-        // D steps of `step_k` values, each batch's loads issued together
-        // ahead of its MFMAs, in two register sets: the next batch's loads
-        // are issued before this batch's MFMAs (the last prefetch of a
-        // chunk reloads its own batch: in bounds, no branch around the
-        // loads); then single steps (`singles`) and a partial last step
-        // (`tail`).  sched_barrier keeps the loads ahead: left to itself the
-        // scheduler sinks each load to its MFMA and waits there.  (Measured
-        // with the same loop in an earlier wide-product kernel on [32, 4096]
-        // @ [4096, 4096]: 20.1 us for batches of 4 steps in two sets,
-        // against 23.0 us for batches of 8 in one.)
-        std::string batched_k_loop(int D, int64_t step_k, bool singles, bool tail, const set_text& declare,
-                                   const load_text& loads, const set_text& mfmas) {
-            const std::string in1 = "    ";
-            const std::string in2 = "        ";
-            auto batch = [&](int d, bool t) {
-                return declare("R", d, in2) + loads("R", d, t, "kk", in2) + in2 + "__builtin_amdgcn_sched_barrier(0);\n" +
-                       mfmas("R", d, in2);
-            };
-            const std::string S = std::to_string(step_k * D);
-            const std::string one = std::to_string(step_k);
-            std::string s = "    idx_t kk = k0;\n";
-            s += "    const idx_t nb = (k1 - k0) / " + S + ";\n";
-            s += declare("P", D, in1) + declare("Q", D, in1);
-            s += "    if (nb > 0) {\n" + loads("P", D, false, "kk", in2) + "    }\n";
-            s += "    for (idx_t b = 0; b < nb; b += 2) {\n";
-            s += "        {\n            const idx_t kn = b + 1 < nb ? kk + " + S + " : kk;\n" +
-                 loads("Q", D, false, "kn", "            ") + "        }\n";
-            s += in2 + "__builtin_amdgcn_sched_barrier(0);\n" + mfmas("P", D, in2) + in2 +
-                 "__builtin_amdgcn_sched_barrier(0);\n";
-            s += "        kk += " + S + ";\n";
-            s += "        if (b + 1 >= nb) break;\n";
-            s += "        {\n            const idx_t kn = b + 2 < nb ? kk + " + S + " : kk;\n" +
-                 loads("P", D, false, "kn", "            ") + "        }\n";
-            s += in2 + "__builtin_amdgcn_sched_barrier(0);\n" + mfmas("Q", D, in2) + in2 +
-                 "__builtin_amdgcn_sched_barrier(0);\n";
-            s += "        kk += " + S + ";\n";
+        // The K loop of gemm.wide and gemm.narrow over a workgroup's chunk
+        // [k0, k1) (names k0, k1 and the uniform wave index w in scope): the
+        // chunk's full groups go to the waves in turn (wave w: groups w,
+        // w + 4, ...), so the four waves read 64 adjacent values of K at a
+        // time.  Each wave keeps two groups' loads in flight: the next
+        // group's loads are issued before this group's MFMAs.  Where every
+        // chunk is whole (`per_wave` groups for every wave, > 0) the loop is
+        // written out: rolled, the compiler's register assignment copied the
+        // accumulators at every turn.  Otherwise the loop takes the groups in
+        // pairs with no exit in between (with a break after the first half
+        // the compiler sank the second set's loads below the first set's
+        // MFMAs), the last prefetch of a wave with an even count reloading
+        // its own last group (in bounds, no branch around the loads), and
+        // declares `full`, the chunk's count of full groups, for a partial
+        // last group that the caller handles.  (Measured for gemm.wide on
+        // [32, 4096] @ [4096, 4096], 4 chunks of 1024: 14.4 us, against 22.7
+        // us for one wave per tile and chunk with 16 chunks; eight or sixteen
+        // waves a workgroup 17.5 and 21.7 us, three groups in flight 15.6.)
+        std::string group_loop(int64_t per_wave, const group_text& declare, const group_load_text& loads,
+                               const group_text& mfmas) {
+            const std::string G16 = std::to_string(group_size);
+            std::string s;
+            if (per_wave > 0 && per_wave <= 32) {
+                auto set_of = [](int64_t t) { return "S" + std::to_string(t % group_depth); };
+                auto load_group = [&](int64_t t) {
+                    return "    {\n        const idx_t kq = k0 + " + G16 + " * w + " +
+                           std::to_string(t * group_waves * group_size) + ";\n" + loads(set_of(t), "kq", "        ") +
+                           "    }\n";
+                };
+                for (int d = 0; d < group_depth; ++d) s += declare(set_of(d), "    ");
+                for (int64_t t = 0; t + 1 < group_depth && t < per_wave; ++t) s += load_group(t);
+                for (int64_t t = 0; t < per_wave; ++t) {
+                    if (t + group_depth - 1 < per_wave) s += load_group(t + group_depth - 1);
+                    s += "    __builtin_amdgcn_sched_barrier(0);\n" + mfmas(set_of(t), "    ") +
+                         "    __builtin_amdgcn_sched_barrier(0);\n";
+                }
+                return s;
+            }
+            s += declare("P", "    ") + declare("Q", "    ");
+            s += "    const idx_t full = (k1 - k0) / " + G16 + ";\n";
+            s += "    const idx_t nf = full > w ? (full - w + 3) / 4 : 0;\n";
+            s += "    if (nf > 0) {\n        const idx_t kq = k0 + " + G16 + " * w;\n" + loads("P", "kq", "        ") + "    }\n";
+            s += "    idx_t t = 0;\n";
+            s += "    for (; t + 2 <= nf; t += 2) {\n";
+            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 1));\n" +
+                 loads("Q", "kq", "            ") + "        }\n";
+            s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("P", "        ") +
+                 "        __builtin_amdgcn_sched_barrier(0);\n";
+            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 2 < nf ? t + 2 : t + 1));\n" +
+                 loads("P", "kq", "            ") + "        }\n";
+            s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("Q", "        ") +
+                 "        __builtin_amdgcn_sched_barrier(0);\n";
             s += "    }\n";
-            if (singles) s += "    for (; kk + " + one + " <= k1; kk += " + one + ") {\n" + batch(1, false) + "    }\n";
-            if (tail) s += "    if (kk < k1) {\n" + batch(1, true) + "    }\n";
+            s += "    if (t < nf) {\n" + mfmas("P", "        ") + "    }\n";
             return s;
         }
-
     } // namespace
 
     bool gemm_few_rows(const gemm_request& r) { return rows_plan(r).blocks > 0; }
@@ -674,32 +683,32 @@ namespace porch::cg {
         const std::string K = std::to_string(r.k);
         const std::string RB = std::to_string(sh.rb);
         const std::string NB = std::to_string(sh.nb);
-        const int64_t tiles = r.batch * sh.tiles;
-        const int64_t waves = tiles * sh.chunks;
+        const std::string CH = std::to_string(sh.chunks);
+        const std::string CK = std::to_string(sh.chunk);
+        const std::string G16 = std::to_string(group_size);
 
         kernel_code kc;
         kc.kind = "gemm.narrow";
         kc.name = "porch_gemm";
         kc.n_slots = r.n_slots;
-        kc.block = 256;
-        kc.grid_x = static_cast<unsigned>((waves + 3) / 4);
+        kc.block = 64 * group_waves;
+        kc.grid_x = static_cast<unsigned>(r.batch * sh.tiles * sh.chunks);
 
         std::string& s = kc.source;
         s = kernel_prologue(r.n_slots, T);
         s += "extern \"C\" __global__ void __launch_bounds__(256) porch_gemm(" + kernel_params(r.n_slots) + ") {\n";
         s += "    const int lane = threadIdx.x & 63;\n";
+        s += "    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n";
         s += "    const int li = lane & 15;\n    const int lg = lane >> 4;\n";
-        // waves of one chunk are adjacent: they share its rows of B
-        s += "    const idx_t wid = (idx_t)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
-        s += "    if (wid >= " + std::to_string(waves) + ") return;\n";
-        s += "    const idx_t ks = wid / " + std::to_string(tiles) + ";\n";
-        s += "    const idx_t tile = wid % " + std::to_string(tiles) + ";\n";
+        // the chunks of a tile are adjacent workgroups: the workgroups of one
+        // chunk (which share its rows of B) land on the same XCDs
+        s += "    const idx_t ks = (idx_t)blockIdx.x % " + CH + ";\n";
+        s += "    const idx_t tile = (idx_t)blockIdx.x / " + CH + ";\n";
         s += "    const idx_t qb = tile / " + std::to_string(sh.tiles) + ";\n";
         if (!r.batched) s += "    (void)qb;\n";
         s += "    const idx_t r0 = (tile % " + std::to_string(sh.tiles) + ") * " + std::to_string(16 * sh.rb) + ";\n";
-        s += "    const idx_t k0 = ks * " + std::to_string(sh.chunk) + ";\n";
-        s += "    const idx_t k1 = k0 + " + std::to_string(sh.chunk) + " < " + K + " ? k0 + " +
-             std::to_string(sh.chunk) + " : (idx_t)" + K + ";\n";
+        s += "    const idx_t k0 = ks * " + CK + ";\n";
+        s += "    const idx_t k1 = k0 + " + CK + " < " + K + " ? k0 + " + CK + " : (idx_t)" + K + ";\n";
         s += "    porch_v4f acc[" + RB + "][" + NB + "];\n";
         s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
         s += "        #pragma unroll\n        for (int j = 0; j < " + NB + "; ++j) acc[i][j] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
@@ -717,72 +726,87 @@ namespace porch::cg {
         s += "        const idx_t q1 = j * 16 + li;\n";
         s += "        qc[j] = q1 < " + N + " ? q1 : (idx_t)" + std::to_string(r.n - 1) + ";\n";
         s += "    }\n";
-        // One step of 16 values of K: lane l holds k = kq + e, kq = kbase +
-        // 4 (l / 16), of its A row and B column; MFMA e takes value e of
-        // every lane.  In the tail, k past K is read at its last 4 values
-        // and both operands are zeroed (zeroing one would turn an infinity
-        // in the other into NaN).
+        // A group: 16 values of K from kq.  Lane l holds k = kq + 4 (l / 16)
+        // + e of its A row (one 128-bit non-temporal load a row block: 16
+        // rows x 64 B an instruction) and of its B column (scalar loads from
+        // the L2); MFMA e takes value e of every lane.
         const std::string aslot = "a" + std::to_string(r.a.slot);
         const std::string bslot = "a" + std::to_string(r.b.slot);
-        const set_text declare = [&](const std::string& set, int D, const std::string& ind) {
-            const std::string Ds = std::to_string(D);
-            return ind + "porch_v4f av" + set + "[" + Ds + "][" + RB + "];\n" + ind + "float bv" + set + "[" + Ds + "][" +
-                   NB + "][4];\n";
+        auto declare = [&](const std::string& set, const std::string& ind) {
+            return ind + "porch_v4f av" + set + "[" + RB + "];\n" + ind + "float bv" + set + "[" + NB + "][4];\n";
         };
-        const load_text loads = [&](const std::string& set, int D, bool tail, const std::string& kbase,
-                                    const std::string& ind) {
+        auto loads = [&](const std::string& set, const std::string& kq, const std::string& ind) {
             std::string t;
-            const std::string av = "av" + set, bv = "bv" + set;
-            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d) {\n";
-            t += ind + "    const idx_t kq = " + kbase + " + d * 16 + lg * 4;\n";
-            if (tail) {
-                t += ind + "    const bool kin = kq < k1;\n";
-                t += ind + "    const idx_t kr = kin ? kq : k1 - 4;\n";
-            }
-            const std::string kr = tail ? "kr" : "kq";
-            t += ind + "    #pragma unroll\n" + ind + "    for (int i = 0; i < " + RB + "; ++i) {\n";
-            t += ind + "        const idx_t q0 = qa[i];\n";
-            t += ind + "        " + av + "[d][i] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + aslot +
-                 " + " + operand_index(r.a, "q0", kr, batch) + "));\n";
-            if (tail) t += ind + "        if (!kin) " + av + "[d][i] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
-            t += ind + "    }\n";
-            t += ind + "    #pragma unroll\n" + ind + "    for (int j = 0; j < " + NB + "; ++j) {\n";
-            t += ind + "        const idx_t q1 = qc[j];\n";
-            t += ind + "        #pragma unroll\n" + ind + "        for (int e = 0; e < 4; ++e) {\n";
-            t += ind + "            " + bv + "[d][j][e] = " + bslot + "[" + operand_index(r.b, kr + " + e", "q1", batch) +
-                 "];\n";
-            if (tail) t += ind + "            if (!kin) " + bv + "[d][j][e] = 0.0f;\n";
-            t += ind + "        }\n" + ind + "    }\n" + ind + "}\n";
-            return t;
-        };
-        const set_text mfmas = [&](const std::string& set, int D, const std::string& ind) {
-            std::string t;
-            t += ind + "#pragma unroll\n" + ind + "for (int d = 0; d < " + std::to_string(D) + "; ++d)\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int i = 0; i < " + RB + "; ++i)\n";
+            t += ind + "    av" + set + "[i] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + aslot +
+                 " + " + operand_index(r.a, "qa[i]", "(" + kq + " + lg * 4)", batch) + "));\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < " + NB + "; ++j)\n";
             t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
-            t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
-            t += ind + "            #pragma unroll\n" + ind + "            for (int j = 0; j < " + NB + "; ++j)\n";
-            t += ind + "                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[d][i][e], bv" + set +
-                 "[d][j][e], acc[i][j], 0, 0, 0);\n";
+            t += ind + "        bv" + set + "[j][e] = " + bslot + "[" +
+                 operand_index(r.b, "(" + kq + " + lg * 4 + e)", "qc[j]", batch) + "];\n";
             return t;
         };
-        s += batched_k_loop(narrow_depth, 16, sh.chunk % (16 * narrow_depth) != 0 || r.k % (16 * narrow_depth) != 0,
-                            r.k % 16 != 0, declare, loads, mfmas);
-        // accumulator value v of lane l: row 4 (l / 16) + v, column l % 16
+        auto mfmas = [&](const std::string& set, const std::string& ind) {
+            std::string t;
+            t += ind + "#pragma unroll\n" + ind + "for (int e = 0; e < 4; ++e)\n";
+            t += ind + "    #pragma unroll\n" + ind + "    for (int i = 0; i < " + RB + "; ++i)\n";
+            t += ind + "        #pragma unroll\n" + ind + "        for (int j = 0; j < " + NB + "; ++j)\n";
+            t += ind + "            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[i][e], bv" + set +
+                 "[j][e], acc[i][j], 0, 0, 0);\n";
+            return t;
+        };
+        s += group_loop(r.k % sh.chunk == 0 ? sh.chunk / (group_waves * group_size) : 0, declare, loads, mfmas);
+        // The partial last group (a chunk not a multiple of 16 values), in
+        // the wave whose turn it is.  K and the chunks are multiples of 4,
+        // so a lane's four values lie all inside or all past the chunk:
+        // past it they are read at its last four values and both operands
+        // are zeroed (zeroing one would turn an infinity in the other into
+        // NaN).
+        if (sh.chunk % group_size != 0 || r.k % group_size != 0) {
+            s += "    if (full * " + G16 + " < k1 - k0 && full % 4 == w) {\n";
+            s += "        const idx_t kb = k0 + full * " + G16 + " + lg * 4;\n";
+            s += "        const bool kin = kb < k1;\n";
+            s += "        const idx_t kr = kin ? kb : k1 - 4;\n";
+            s += declare("R", "        ");
+            s += "        #pragma unroll\n        for (int i = 0; i < " + RB + "; ++i) {\n";
+            s += "            avR[i] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + aslot + " + " +
+                 operand_index(r.a, "qa[i]", "kr", batch) + "));\n";
+            s += "            if (!kin) avR[i] = porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+            s += "        }\n";
+            s += "        #pragma unroll\n        for (int j = 0; j < " + NB + "; ++j)\n";
+            s += "            #pragma unroll\n            for (int e = 0; e < 4; ++e) {\n";
+            s += "                const float x = " + bslot + "[" + operand_index(r.b, "(kr + e)", "qc[j]", batch) + "];\n";
+            s += "                bvR[j][e] = kin ? x : 0.0f;\n";
+            s += "            }\n";
+            s += mfmas("R", "        ");
+            s += "    }\n";
+        }
+        // The waves' sums, added in wave order through LDS.  Accumulator
+        // value v of lane l: row 16 i + 4 (l / 16) + v, column 16 j + l % 16.
+        const int64_t blocks = sh.rb * sh.nb;
+        s += "    __shared__ porch_v4f red[4][" + std::to_string(blocks) + "][64];\n";
         s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
-        s += "        #pragma unroll\n        for (int j = 0; j < " + NB + "; ++j)\n";
-        s += "            #pragma unroll\n            for (int v = 0; v < 4; ++v) {\n";
-        s += "                const idx_t q0 = r0 + i * 16 + lg * 4 + v;\n";
-        s += "                const idx_t q1 = j * 16 + li;\n";
-        s += "                if (q0 < " + M + " && q1 < " + N + ") {\n";
+        s += "        #pragma unroll\n        for (int j = 0; j < " + NB + "; ++j) red[w][i * " + NB +
+             " + j][lane] = acc[i][j];\n";
+        s += "    __syncthreads();\n";
+        s += "    for (int t = threadIdx.x; t < " + std::to_string(64 * blocks) + "; t += 256) {\n";
+        s += "        const int b = t >> 6, l = t & 63;\n";
+        s += "        const int i = b / " + NB + ", j = b % " + NB + ";\n";
+        s += "        porch_v4f sum = red[0][b][l];\n";
+        s += "        #pragma unroll\n        for (int u = 1; u < 4; ++u) sum += red[u][b][l];\n";
+        s += "        const idx_t q1 = j * 16 + (l & 15);\n";
+        s += "        #pragma unroll\n        for (int v = 0; v < 4; ++v) {\n";
+        s += "            const idx_t q0 = r0 + i * 16 + (l >> 4) * 4 + v;\n";
+        s += "            if (q0 < " + M + " && q1 < " + N + ") {\n";
         const std::string o = std::string(r.batched ? "(qb * " + M + " + q0)" : "q0") + " * " + N + " + q1";
         if (final) {
-            s += "                    const float acc_v = acc[i][j][v];\n";
-            s += epilogue_store(r, "acc_v", o, "                    ");
+            s += "                const float acc_v = sum[v];\n";
+            s += epilogue_store(r, "acc_v", o, "                ");
         }
         else {
-            s += "                    out[ks * " + std::to_string(r.batch * r.m * r.n) + " + " + o + "] = acc[i][j][v];\n";
+            s += "                out[ks * " + std::to_string(r.batch * r.m * r.n) + " + " + o + "] = sum[v];\n";
         }
-        s += "                }\n            }\n}\n";
+        s += "            }\n        }\n    }\n}\n";
         return kc;
     }
 
@@ -808,7 +832,7 @@ namespace porch::cg {
         kc.kind = "gemm.wide";
         kc.name = "porch_gemm";
         kc.n_slots = r.n_slots;
-        kc.block = 64 * wide_waves;
+        kc.block = 64 * group_waves;
         kc.grid_x = static_cast<unsigned>(r.batch * sh.tiles * sh.chunks);
 
         std::string& s = kc.source;
@@ -878,62 +902,12 @@ namespace porch::cg {
                  "[j][e], acc[i][e], 0, 0, 0);\n";
             return t;
         };
-        // The chunk's full groups go to the waves in turn (wave w: groups w,
-        // w + 4, ...), so the four waves read 64 adjacent rows at a time.
-        // Each wave keeps two groups' loads in flight: the next group's
-        // loads are issued before this group's MFMAs.  The loop takes the
-        // groups in pairs with no exit in between (with a break after the
-        // first half the compiler sank the second set's loads below the
-        // first set's MFMAs); the last prefetch of a wave with an even
-        // count reloads its own last group: in bounds, no branch around the
-        // loads.
-        // Measured on [32, 4096] @ [4096, 4096], 4 chunks of 1024: 14.4 us,
-        // against 22.7 us for one wave per tile and chunk (16 chunks) with
-        // A read a value a lane; eight or sixteen waves a workgroup 17.5 and
-        // 21.7 us, three groups in flight 15.6 us.
-        const std::string G16 = std::to_string(wide_group);
-        // Where every chunk is whole, every wave has the same compile-time
-        // count of groups and the loop is written out (no loop-carried copy
-        // of the accumulators, which the compiler's register assignment
-        // for the rolled loop adds at each turn), wide_depth groups in
-        // flight.
-        const int64_t per_wave = r.k % sh.chunk == 0 ? sh.chunk / (wide_waves * wide_group) : 0;
-        if (per_wave > 0 && per_wave <= 32) {
-            auto set_of = [](int64_t t) { return "S" + std::to_string(t % wide_depth); };
-            auto load_group = [&](int64_t t) {
-                return "    {\n        const idx_t kq = k0 + " + G16 + " * w + " +
-                       std::to_string(t * wide_waves * wide_group) + ";\n" + loads(set_of(t), "kq", "        ") + "    }\n";
-            };
-            for (int d = 0; d < wide_depth; ++d) s += declare(set_of(d), "    ");
-            for (int64_t t = 0; t + 1 < wide_depth && t < per_wave; ++t) s += load_group(t);
-            for (int64_t t = 0; t < per_wave; ++t) {
-                if (t + wide_depth - 1 < per_wave) s += load_group(t + wide_depth - 1);
-                s += "    __builtin_amdgcn_sched_barrier(0);\n" + mfmas(set_of(t), "    ") +
-                     "    __builtin_amdgcn_sched_barrier(0);\n";
-            }
-        }
-        else {
-            s += declare("P", "    ") + declare("Q", "    ");
-            s += "    const idx_t full = (k1 - k0) / " + G16 + ";\n";
-            s += "    const idx_t nf = full > w ? (full - w + 3) / 4 : 0;\n";
-            s += "    if (nf > 0) {\n        const idx_t kq = k0 + " + G16 + " * w;\n" + loads("P", "kq", "        ") + "    }\n";
-            s += "    idx_t t = 0;\n";
-            s += "    for (; t + 2 <= nf; t += 2) {\n";
-            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 1));\n" +
-                 loads("Q", "kq", "            ") + "        }\n";
-            s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("P", "        ") +
-                 "        __builtin_amdgcn_sched_barrier(0);\n";
-            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 2 < nf ? t + 2 : t + 1));\n" +
-                 loads("P", "kq", "            ") + "        }\n";
-            s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("Q", "        ") +
-                 "        __builtin_amdgcn_sched_barrier(0);\n";
-            s += "    }\n";
-            s += "    if (t < nf) {\n" + mfmas("P", "        ") + "    }\n";
-        }
+        s += group_loop(r.k % sh.chunk == 0 ? sh.chunk / (group_waves * group_size) : 0, declare, loads, mfmas);
+        const std::string G16 = std::to_string(group_size);
         // The partial last group (a chunk not a multiple of 16 values), in
         // the wave whose turn it is: lanes past the chunk read its last
         // value and zero both operands.
-        if (sh.chunk % wide_group != 0 || r.k % wide_group != 0) {
+        if (sh.chunk % group_size != 0 || r.k % group_size != 0) {
             s += "    if (full * " + G16 + " < k1 - k0 && full % 4 == w) {\n";
             s += "        const idx_t kq = k0 + full * " + G16 + ";\n";
             s += declare("R", "        ");

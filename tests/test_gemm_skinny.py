@@ -125,6 +125,9 @@ CASES = {
     "narrow, transposed B": (
         ([2048, 516], [12, 516]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
         lambda p: p, ["gemm.narrow", "gemm.combine"]),
+    "narrow, two groups a wave, written out": (
+        ([1024, 1024], [1024, 24]), lambda a, b: porch.matmul(a, b) - 1.0, lambda a, b: a @ b, lambda p: p - 1.0,
+        ["gemm.narrow", "gemm.combine"]),
     "narrow rows, sixteen columns": (
         ([4096, 2048], [2048, 16]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.narrow_rows"]),
@@ -251,7 +254,7 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "narrow, ragged rows and columns, K tail, relu",
                                   "narrow, one chunk, epilogue in the kernel", "narrow, batched, ragged row tiles",
                                   "narrow, transposed B", "narrow rows, ragged rows and columns, K tail, relu",
-                                  "narrow rows, four waves, K tail",
+                                  "narrow rows, four waves, K tail", "narrow, two groups a wave, written out",
                                   "wide, ragged rows and columns, K tail, relu",
                                   "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A",
                                   "wide, two groups a wave, written out"])
@@ -309,11 +312,12 @@ def test_epilogue_reading_an_input_bit_exact(gpu, shape):
 
 
 @pytest.mark.parametrize("shape, chunks", [
-    ((4096, 1024, 16), 8),   # 128 row tiles of 32: 1024 waves, 8 chunks of 128
-    ((1100, 1036, 20), 9),   # 35 row tiles: 30 chunks for the waves, 12 for partials at most 1/4
-                             # of A, of 87 -> 128 values of K (a multiple of 64): 9 chunks
+    ((4096, 1024, 16), 2),   # 128 row tiles of 32: 2 chunks of 512 for a workgroup a CU
+    ((1100, 1036, 20), 6),   # 35 row tiles: 8 chunks for the CUs (12 for partials at most 1/4
+                             # of A), of 130 -> 192 values of K (a multiple of 64): 6 chunks
     ((2048, 256, 32), 2),    # partials at most 1/4 of A: 256 / (4 x 32) chunks
-    ((512, 4096, 16), 32),   # 16 row tiles: 64 chunks for the waves, at most 32
+    ((512, 4096, 16), 16),   # 16 row tiles: 16 chunks of 256 for the CUs
+    ((256, 8192, 8), 32),    # 8 row tiles: 32 chunks for the CUs, at most 32
     ((2048, 120, 32), 1),    # too short a K to split: the epilogue in the kernel
 ])
 def test_narrow_chunks(shape, chunks):
@@ -321,8 +325,9 @@ def test_narrow_chunks(shape, chunks):
     plan = porch.plan(porch.matmul(placeholder([m, k]), placeholder([k, n])))
     kinds = [x["kind"] for x in plan["kernels"]]
     assert kinds == (["gemm.narrow", "gemm.combine"] if chunks > 1 else ["gemm.narrow"])
-    waves = -(-m // 32) * chunks
-    assert plan["kernels"][0]["grid"][0] == -(-waves // 4)
+    # one workgroup of four waves per 32-row tile and chunk
+    assert plan["kernels"][0]["grid"][0] == -(-m // 32) * chunks
+    assert plan["kernels"][0]["block"] == 256
     assert plan["temps"] == ([chunks * m * n] if chunks > 1 else [])
 
 
