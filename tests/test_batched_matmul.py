@@ -16,7 +16,7 @@ import pytest
 
 import porch_amd as porch
 from oracle import host
-from tests.helpers import placeholder
+from tests.helpers import CONFIG_SIZES, config_graph, config_inputs, placeholder
 
 
 def ints(shape, rng, lo=-3, hi=4):
@@ -324,3 +324,29 @@ def test_empty_extents(gpu, shape_a, shape_b):
     expected_shape = (shape_a[0], shape_a[1], shape_b[2])
     assert tuple(out.shape()) == expected_shape
     assert np.array_equal(out.cpu().reshape(expected_shape), np.ones(expected_shape, np.float32))
+
+
+@pytest.mark.gpu
+def test_attention_scores_every_output(gpu):
+    """The benchmark's attention product, batched_matmul(q, k) * 0.125 over
+    16 heads of [4096, 64] @ [64, 4096], on its seeded inputs: all 268 M
+    outputs against a float64 product of the same float32 operands, within
+    the accumulation bound (K - 1) 2^-24 sum |q||k| (scaled like the
+    product; the scale by a power of two is exact), head by head."""
+    size = CONFIG_SIZES["attention_scores"]
+    nb, m, k, n = size["batch"], size["m"], size["k"], size["n"]
+    q, kt = config_inputs("attention_scores")
+    expr = config_graph("attention_scores", [gpu.tensor([nb, m, k], q), gpu.tensor([nb, k, n], kt)])
+    assert [x["kind"] for x in gpu.plan(expr)["kernels"]] == ["gemm.mfma"]
+    out = gpu.materialize(expr).cpu().reshape(nb, m, n)
+    q64 = np.asarray(q, np.float32).reshape(nb, m, k).astype(np.float64)
+    k64 = np.asarray(kt, np.float32).reshape(nb, k, n).astype(np.float64)
+    worst = 0.0
+    for h in range(nb):
+        exact = (q64[h] @ k64[h]) * 0.125
+        bound = (k - 1) * 2.0 ** -24 * 0.125 * (np.abs(q64[h]) @ np.abs(k64[h]))
+        frac = np.abs(out[h].astype(np.float64) - exact) / bound
+        worst = max(worst, float(frac.max()))
+        assert np.all(frac <= 1.0), (h, float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
+    print("attention scores: max |err| / bound", worst)
+

@@ -22,7 +22,7 @@ import pytest
 
 import porch_amd as porch
 from oracle import host
-from tests.helpers import placeholder
+from tests.helpers import CONFIG_SIZES, config_graph, config_inputs, placeholder
 from tests.kernel_emu import emulate as emu
 
 needs_clang = pytest.mark.skipif(not emu.available(), reason="host clang++ from ROCm is required")
@@ -480,3 +480,26 @@ def test_clamped_edge_rows_and_columns(gpu, kind, m, k, n):
     ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
     assert np.isnan(ref[m - 1]).all() and not np.isnan(ref[: m - 1, : n - 1]).any()
     assert np.array_equal(out, ref, equal_nan=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name, kinds", [("narrow_product", ["gemm.narrow_rows"]),
+                                         ("wide_product", ["gemm.wide", "gemm.combine"])])
+def test_benchmark_products_every_output(gpu, name, kinds):
+    """The benchmark's two products with one short side, at their size, on
+    its seeded inputs: every output against a float64 product of the same
+    float32 operands, within the accumulation bound (K - 1) 2^-24 sum |a||b|
+    (the reference computes every output through its K loop,
+    src/tensor.cpp:684-721)."""
+    size = CONFIG_SIZES[name]
+    m, k, n = size["m"], size["k"], size["n"]
+    a, b = config_inputs(name)
+    expr = config_graph(name, [gpu.tensor([m, k], a), gpu.tensor([k, n], b)])
+    assert _kinds(expr) == kinds
+    out = gpu.materialize(expr).cpu().reshape(m, n).astype(np.float64)
+    a64 = np.asarray(a, np.float32).reshape(m, k).astype(np.float64)
+    b64 = np.asarray(b, np.float32).reshape(k, n).astype(np.float64)
+    bound = (k - 1) * 2.0 ** -24 * (np.abs(a64) @ np.abs(b64))
+    frac = np.abs(out - a64 @ b64) / bound
+    assert np.all(frac <= 1.0), (float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
+
