@@ -16,7 +16,7 @@ import pytest
 
 import porch_amd as porch
 from oracle import host
-from tests.helpers import CONFIG_SIZES, config_graph, config_inputs, placeholder
+from tests.helpers import CONFIG_SIZES, check_matmul_epilogue_every_output, config_graph, config_inputs, placeholder
 
 
 def ints(shape, rng, lo=-3, hi=4):
@@ -349,4 +349,22 @@ def test_attention_scores_every_output(gpu):
         worst = max(worst, float(frac.max()))
         assert np.all(frac <= 1.0), (h, float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
     print("attention scores: max |err| / bound", worst)
+
+
+@pytest.mark.gpu
+def test_batched_matmul_benchmark_size_every_output(gpu):
+    """The benchmark's batched product, relu(batched_matmul(A, B) + bias) -
+    0.5 over 32 entries of [1024, 1024] @ [1024, 1024] on its seeded inputs:
+    every output of every entry against a float64 product (the product
+    within the accumulation bound, the result within 1e-4 relative)."""
+    size = CONFIG_SIZES["batched_matmul"]
+    nb, m, k, n = size["batch"], size["m"], size["k"], size["n"]
+    a, b, bias = config_inputs("batched_matmul")
+    expr = config_graph("batched_matmul", [gpu.tensor([nb, m, k], a), gpu.tensor([nb, k, n], b),
+                                           gpu.tensor([1, 1, n], bias)])
+    out = gpu.materialize(expr).cpu().reshape(nb, m, n)
+    a3 = np.asarray(a, np.float32).reshape(nb, m, k)
+    b3 = np.asarray(b, np.float32).reshape(nb, k, n)
+    for e in range(nb):
+        check_matmul_epilogue_every_output(out[e], a3[e], b3[e], bias, m, k, n)
 

@@ -203,3 +203,16 @@ def test_permute_of_an_empty_tensor(gpu):
     t = gpu.tensor([3, 0, 2], np.zeros(0, np.float32))
     out = gpu.materialize(gpu.permute(t, [2, 0, 1]) * 2.0)
     assert tuple(out.shape()) == (2, 3, 0) and out.cpu().size == 0
+
+
+@pytest.mark.gpu
+def test_heads_permute_benchmark_size_bit_exact(gpu):
+    """The benchmark's heads permute, permute(x, [0, 2, 1, 3]) over x
+    [32, 1024, 16, 128] on its seeded input: every element moved exactly."""
+    from porch_amd.workloads import config_graph, config_inputs, config_shapes
+    (shape,) = config_shapes("heads_permute")
+    (x,) = config_inputs("heads_permute")
+    expr = config_graph("heads_permute", [gpu.tensor(shape, x)])
+    out = gpu.materialize(expr).cpu().reshape(shape[0], shape[2], shape[1], shape[3])
+    assert np.array_equal(out, np.transpose(np.asarray(x, np.float32).reshape(shape), (0, 2, 1, 3)))
+
