@@ -3,7 +3,7 @@
 // The one-output-per-lane K loop (gemm.scalar) gives a vector-matrix
 // product [1, 4096] @ [4096, 4096] 16 workgroups and 182 us; the MFMA tiles
 // of 128 x 128 spend most of their work on padding when one side is a few
-// rows or columns.  Two forms instead:
+// rows or columns.  Instead:
 //
 //   gemm.rows     few rows (m <= 16, n >= 256) where gemm.wide cannot read
 //                 B's rows as float4s: one wave per 256 columns
@@ -301,7 +301,6 @@ namespace porch::cg {
         const rows_shape sh = rows_plan(r);
         if (sh.blocks == 0) throw std::logic_error("emit_gemm_few_rows: not a few-row product");
         const bool final = sh.chunks == 1;
-        const bool vec = b_vector(r);
         const char* T = r.width.type();
         const std::string batch = r.batched ? "qb" : "";
         const std::string M = std::to_string(r.m);
@@ -328,29 +327,21 @@ namespace porch::cg {
         s += "    float acc[" + M + "][4];\n";
         s += "    #pragma unroll\n    for (int i = 0; i < " + M + "; ++i)\n";
         s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) acc[i][e] = 0.0f;\n";
-        // column of value e of this lane
-        const std::string col0 = vec ? "blk * 256 + lane * 4" : "blk * 256 + lane";
-        const std::string col_step = vec ? "1" : "64";
-        s += "    const idx_t c0 = " + col0 + ";\n";
-        // B rows in flight per lane: 8 for up to 8 rows of A (measured
-        // [1 and 4, 4096] @ [4096, 4096]: 15.5 -> 13.2 and 18.2 -> 15.5 us
-        // against 4; 16 gave no more, and at 16 rows 8 gave no gain).
+        // value e of this lane is column c0 + 64 e: B's rows are not read as
+        // float4s here (gemm.wide takes the products where they can be)
+        const std::string col_step = "64";
+        s += "    const idx_t c0 = blk * 256 + lane;\n";
+        // B rows in flight per lane: 8 for up to 8 rows of A (measured when
+        // this kernel also read float4s of B, [1 and 4, 4096] @ [4096, 4096]:
+        // 15.5 -> 13.2 and 18.2 -> 15.5 us against 4; 16 gave no more, and at
+        // 16 rows 8 gave no gain).
         s += std::string("    #pragma unroll ") + (r.m <= 8 ? "8" : "4") + "\n    for (idx_t kk = k0; kk < k1; ++kk) {\n";
         s += "        float bv[4];\n";
-        if (vec) {
-            s += "        if (c0 < " + N + ") {\n";
-            s += "            const porch_v4f w = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(a" +
-                 std::to_string(r.b.slot) + " + " + operand_index(r.b, "kk", "c0", batch) + "));\n";
-            s += "            bv[0] = w.x; bv[1] = w.y; bv[2] = w.z; bv[3] = w.w;\n";
-            s += "        }\n        else {\n            bv[0] = bv[1] = bv[2] = bv[3] = 0.0f;\n        }\n";
-        }
-        else {
-            s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) {\n";
-            s += "            const idx_t c = c0 + e * " + col_step + ";\n";
-            s += "            bv[e] = c < " + N + " ? a" + std::to_string(r.b.slot) + "[" +
-                 operand_index(r.b, "kk", "c", batch) + "] : 0.0f;\n";
-            s += "        }\n";
-        }
+        s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) {\n";
+        s += "            const idx_t c = c0 + e * " + col_step + ";\n";
+        s += "            bv[e] = c < " + N + " ? a" + std::to_string(r.b.slot) + "[" +
+             operand_index(r.b, "kk", "c", batch) + "] : 0.0f;\n";
+        s += "        }\n";
         s += "        #pragma unroll\n        for (int i = 0; i < " + M + "; ++i) {\n";
         s += "            const float av = a" + std::to_string(r.a.slot) + "[" + operand_index(r.a, "i", "kk", batch) +
              "];\n";
