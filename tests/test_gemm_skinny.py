@@ -71,6 +71,12 @@ CASES = {
     "wide, four groups a wave, written out, relu": (
         ([32, 2048], [2048, 2048]), lambda a, b: porch.relu(porch.matmul(a, b) - 2.0), lambda a, b: a @ b,
         lambda p: np.maximum(p - 2.0, 0.0), ["gemm.wide", "gemm.combine"]),
+    "wide, forty-eight rows": (
+        ([48, 4096], [4096, 2048]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
+        ["gemm.wide", "gemm.combine"]),
+    "wide, sixty-four rows, relu": (
+        ([64, 4096], [4096, 4096]), lambda a, b: porch.relu(porch.matmul(a, b) + 0.5), lambda a, b: a @ b,
+        lambda p: np.maximum(p + 0.5, 0.0), ["gemm.wide", "gemm.combine"]),
     "wide, batched": (
         ([2, 24, 516], [2, 516, 512]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.wide", "gemm.combine"]),
