@@ -204,17 +204,26 @@ namespace porch::cg {
     bool gemm_few_cols(const gemm_request& request);
     kernel_code emit_gemm_few_cols(const gemm_request& request);
     // 7 to 32 columns over 128 rows or more (A rows contiguous along K):
-    // one wave per 32 rows and a chunk of K on 16x16x4 MFMA blocks, the
-    // chunks' partial products summed by emit_gemm_combine.
+    // a workgroup of four waves per 32 rows and a chunk of K on 16x16x4
+    // MFMA blocks (or, for up to 16 columns over enough rows, one workgroup
+    // per 16 rows over all of K), the chunks' partial products summed by
+    // emit_gemm_combine.
     bool gemm_narrow(const gemm_request& request);
     int64_t gemm_narrow_chunks(const gemm_request& request);
     kernel_code emit_gemm_narrow(const gemm_request& request);
-    // 8 to 32 rows over 256 columns or more (B rows contiguous along N; up
-    // to 64 where the chunks fill four waves per compute unit):
-    // one wave per 64 columns and a chunk of K on 16x16x4 MFMA blocks, the
+    // 1 to 32 rows over 256 columns or more (B rows contiguous along N; up
+    // to 64 where the workgroups fill every compute unit): a workgroup of
+    // four waves per 64 columns and a chunk of K on 16x16x4 MFMA blocks, the
     // chunks' partial products summed by emit_gemm_combine.
     bool gemm_wide(const gemm_request& request);
     int64_t gemm_wide_chunks(const gemm_request& request);
     kernel_code emit_gemm_wide(const gemm_request& request);
+
+    // A short K (8 to 64, a multiple of 8) over at least two bands of 128
+    // rows per compute unit and 256 columns or more, A's rows contiguous
+    // along K and B's along N (emit_gemm_band.cpp): one workgroup per band,
+    // its A held in registers, walking the band's column tiles.
+    bool gemm_band(const gemm_request& request);
+    kernel_code emit_gemm_band(const gemm_request& request);
 
 } // namespace porch::cg

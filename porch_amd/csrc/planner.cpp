@@ -325,6 +325,10 @@ namespace porch::plan {
                     add_step(cg::emit_gemm_few_cols(r), dest);
                     return true;
                 }
+                if (cg::gemm_band(r)) {
+                    add_step(cg::emit_gemm_band(r), dest);
+                    return true;
+                }
                 r.k_chunks = cg::gemm_k_chunks(r);
                 if (r.k_chunks > 1) {
                     // Too few tiles for the machine: chunks of K in

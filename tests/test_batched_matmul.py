@@ -337,7 +337,7 @@ def test_attention_scores_every_output(gpu):
     nb, m, k, n = size["batch"], size["m"], size["k"], size["n"]
     q, kt = config_inputs("attention_scores")
     expr = config_graph("attention_scores", [gpu.tensor([nb, m, k], q), gpu.tensor([nb, k, n], kt)])
-    assert [x["kind"] for x in gpu.plan(expr)["kernels"]] == ["gemm.mfma"]
+    assert [x["kind"] for x in gpu.plan(expr)["kernels"]] == ["gemm.band"]
     out = gpu.materialize(expr).cpu().reshape(nb, m, n)
     q64 = np.asarray(q, np.float32).reshape(nb, m, k).astype(np.float64)
     k64 = np.asarray(kt, np.float32).reshape(nb, k, n).astype(np.float64)

@@ -1,0 +1,137 @@
+"""Products with a short K over many bands of rows (kernel kind gemm.band):
+one workgroup per batch entry and 128-row band, A held in registers, the
+band's column tiles walked with B through LDS, results stored as float4
+rows through LDS.  The plan's choice, exactness on integer data (in CPU
+emulation and on the GPU, against the oracle) and real data within the
+matmul's accumulation bound (K - 1) 2^-24 sum |a||b| against float64."""
+
+import numpy as np
+import pytest
+
+import porch_amd as porch
+from oracle import host
+from tests.helpers import placeholder
+from tests.kernel_emu import emulate as emu
+
+needs_clang = pytest.mark.skipif(not emu.available(), reason="host clang++ from ROCm is required")
+
+
+def _kinds(expr):
+    return [k["kind"] for k in porch.plan(expr)["kernels"]]
+
+
+def _ints(shape, seed):
+    return np.random.default_rng(seed).integers(-3, 4, size=shape).astype(np.float32)
+
+
+def _reals(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+def _product(a, b, batched):
+    return porch.batched_matmul(a, b) if batched else porch.matmul(a, b)
+
+
+# name: (A shape, B shape, graph over (product, bias tensor or None), epilogue on the float64 product
+# and bias, bias shape or None)
+CASES = {
+    "attention-shaped, scaled": (
+        [16, 4096, 64], [16, 64, 4096], lambda p, c: p * 0.125, lambda p, c: p * 0.125, None),
+    "bias and relu, K of 16": (
+        [4, 16384, 16], [4, 16, 256], lambda p, c: porch.relu(p + porch.broadcast_to(c, [4, 16384, 256])),
+        lambda p, c: np.maximum(p + c, 0.0), [1, 1, 256]),
+    "ragged last band and tile, K of 8": (
+        [2, 32700, 8], [2, 8, 300], lambda p, c: p - porch.broadcast_to(c, [2, 32700, 300]),
+        lambda p, c: p - c, [1, 1, 300]),
+    "unbatched": (
+        [65536, 64], [64, 512], lambda p, c: p, lambda p, c: p, None),
+}
+
+
+def _graph(name, make):
+    sa, sb, graph, _, sbias = CASES[name]
+    tensors = [make(sa, 1), make(sb, 2)] + ([make(sbias, 3)] if sbias else [])
+    bias = tensors[2] if sbias else None
+    return graph(_product(tensors[0], tensors[1], len(sa) == 3), bias), tensors
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_band_products_take_the_band_kernel(name):
+    expr, _ = _graph(name, lambda s, seed: placeholder(s))
+    plan = porch.plan(expr, compile=True)
+    assert [k["kind"] for k in plan["kernels"]] == ["gemm.band"]
+    sa = CASES[name][0]
+    rows = sa[-2]
+    batch = sa[0] if len(sa) == 3 else 1
+    assert plan["kernels"][0]["grid"][0] == batch * -(-rows // 128)
+    assert plan["temps"] == []
+
+
+def test_band_bounds():
+    # K from 8 to 64 in steps of 8, 256 columns or more, at least two bands
+    # of 128 rows per compute unit (512 on 256 CUs)
+    def kind(sa, sb):
+        return _kinds(porch.batched_matmul(placeholder(sa), placeholder(sb)))[0]
+    assert kind([16, 4096, 64], [16, 64, 4096]) == "gemm.band"
+    assert kind([16, 4096, 72], [16, 72, 4096]) == "gemm.mfma"
+    assert kind([16, 4096, 60], [16, 60, 4096]) == "gemm.mfma"
+    assert kind([16, 4096, 8], [16, 8, 4096]) == "gemm.band"
+    assert kind([16, 4096, 64], [16, 64, 256]) == "gemm.band"
+    assert kind([16, 4096, 64], [16, 64, 252]) == "gemm.mfma"
+    assert kind([16, 4096, 64], [16, 64, 128]) == "gemm.mfma"
+    assert kind([1, 65408, 64], [1, 64, 256]) == "gemm.mfma"   # 511 bands
+    assert kind([1, 65409, 64], [1, 64, 256]) == "gemm.band"   # 512, the last of one row
+    # B transposed: its rows along N are not contiguous
+    assert _kinds(porch.batched_matmul(placeholder([16, 4096, 64]),
+                                       porch.permute(placeholder([16, 4096, 64]), [0, 2, 1])))[0] == "gemm.mfma"
+
+
+@needs_clang
+@pytest.mark.parametrize("name", ["bias and relu, K of 16", "ragged last band and tile, K of 8"])
+def test_emulated_band_products_are_exact(name):
+    xs = {}
+
+    def make(shape, seed):
+        xs[seed] = _ints(shape, seed)
+        return placeholder(shape, xs[seed])
+
+    expr, _ = _graph(name, make)
+    assert _kinds(expr) == ["gemm.band"]
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=900))
+    got = emu.evaluate(expr, [xs[s] for s in sorted(xs)], timeout=900)
+    want = np.asarray(host.evaluate(expr), np.float32)
+    assert np.array_equal(got.reshape(want.shape), want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_band_products_bit_exact_on_integers(gpu, name):
+    expr, _ = _graph(name, lambda s, seed: gpu.tensor(s, _ints(s, seed).reshape(-1)))
+    assert [k["kind"] for k in gpu.plan(expr)["kernels"]] == ["gemm.band"]
+    out = gpu.materialize(expr).cpu()
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_band_products_within_the_accumulation_bound(gpu, name):
+    sa, sb, _, epi, sbias = CASES[name]
+    vals = {1: _reals(sa, 11), 2: _reals(sb, 12)}
+    if sbias:
+        vals[3] = _reals(sbias, 13)
+    expr, _ = _graph(name, lambda s, seed: gpu.tensor(s, vals[seed].reshape(-1)))
+    out = gpu.materialize(expr).cpu().reshape(expr.shape()).astype(np.float64)
+    a64, b64 = vals[1].astype(np.float64), vals[2].astype(np.float64)
+    k = sa[-1]
+    exact = np.matmul(a64, b64)
+    bound = (k - 1) * 2.0 ** -24 * np.matmul(np.abs(a64), np.abs(b64))
+    bias64 = vals[3].astype(np.float64) if sbias else None
+    want = epi(exact, bias64)
+    # the product's bound carried through the epilogue (a scale by 1/8 is
+    # exact, relu does not widen an error), plus half an ulp of the result
+    # for the one rounded add or subtract after the product
+    scale = 0.125 if name.startswith("attention") else 1.0
+    slack = scale * bound + np.abs(want) * 2.0 ** -24
+    frac = np.abs(out - want) / np.maximum(slack, 1e-300)
+    assert np.all(frac <= 1.0), (float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
