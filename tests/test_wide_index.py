@@ -46,6 +46,14 @@ def test_large_product_operand_uses_64_bit_indices():
         assert "typedef long long idx_t;" in source, kind
 
 
+def test_large_band_product_uses_64_bit_indices():
+    # [33, 8192, 8] @ [33, 8, 8192]: 33 x 8192^2 = 2^31 + 2^26 outputs
+    expr = porch.batched_matmul(placeholder([33, 8192, 8]), placeholder([33, 8, 8192]))
+    (kind, source), = wide_kernels(expr)
+    assert kind == "gemm.band"
+    assert "typedef long long idx_t;" in source
+
+
 def device_data(gpu, rows, cols):
     """x[i, j] = (i % 7) + (j % 5), made on the device from two small
     vectors (a broadcast sum, materialised)."""
@@ -109,3 +117,25 @@ def test_wide_matmul_operand(gpu):
     rows = [0, 1, 2, 12345, 32767, 32768, 40000, C - 1]
     a_rows = np.concatenate([expected_rows(r, r + 1, R) for r in rows]).astype(np.float64)
     assert np.array_equal(out[rows], (a_rows @ b_host.reshape(R, 64).astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.gpu
+def test_wide_band_product(gpu):
+    # 33 entries of [8192, 8] @ [8, 8192]: entry 32 starts at output 2^31;
+    # small integers sum exactly in any order
+    nb, n, k = 33, 8192, 8
+    bi, ii, kk = np.meshgrid(np.arange(nb), np.arange(n), np.arange(k), indexing="ij")
+    a_host = ((bi + ii + kk) % 5).astype(np.float32)
+    bb, kb, jb = np.meshgrid(np.arange(nb), np.arange(k), np.arange(n), indexing="ij")
+    b_host = ((3 * bb + kb + jb) % 7).astype(np.float32)
+    a = gpu.tensor([nb, n, k], a_host.reshape(-1))
+    b = gpu.tensor([nb, k, n], b_host.reshape(-1))
+    expr = gpu.batched_matmul(a, b) - 1.0
+    assert [x["kind"] for x in gpu.plan(expr)["kernels"]] == ["gemm.band"]
+    print("wide: band product", flush=True)
+    out = gpu.materialize(expr).cpu().reshape(nb, n, n)
+    for e in (0, 31, 32):
+        for r in (0, 1, 4097, n - 1):
+            want = a_host[e, r].astype(np.float64) @ b_host[e].astype(np.float64) - 1.0
+            assert np.array_equal(out[e, r], want.astype(np.float32)), (e, r)
+
