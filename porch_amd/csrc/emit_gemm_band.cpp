@@ -148,6 +148,12 @@ namespace porch::cg {
         s += "        #pragma unroll\n        for (int i = 0; i < 2; ++i)\n";
         s += "            #pragma unroll\n            for (int j = 0; j < 2; ++j)\n";
         s += "                #pragma unroll\n                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;\n";
+        // the next tile into the other buffer (its last readers finished
+        // before the previous barrier) and the one after into registers,
+        // issued ahead of this tile's MFMAs
+        s += "        if (t + 1 < " + std::to_string(tiles) + ") {\n" + write_b("buf ^ 1") + "        }\n";
+        s += "        if (t + 2 < " + std::to_string(tiles) + ") {\n" + load_b("t + 2") + "        }\n";
+        s += "        __builtin_amdgcn_sched_barrier(0);\n";
         s += "        #pragma unroll\n        for (int st = 0; st < " + HK + "; ++st) {\n";
         s += "            const float b0 = Bs[buf][" + HK + " * h + st][64 * wn + li];\n";
         s += "            const float b1 = Bs[buf][" + HK + " * h + st][64 * wn + 32 + li];\n";
@@ -158,10 +164,6 @@ namespace porch::cg {
         s += "            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(x1, b0, acc[1][0], 0, 0, 0);\n";
         s += "            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(x1, b1, acc[1][1], 0, 0, 0);\n";
         s += "        }\n";
-        // the next tile into the other buffer (its last readers finished
-        // before the previous barrier), the one after into registers
-        s += "        if (t + 1 < " + std::to_string(tiles) + ") {\n" + write_b("buf ^ 1") + "        }\n";
-        s += "        if (t + 2 < " + std::to_string(tiles) + ") {\n" + load_b("t + 2") + "        }\n";
         // The results, 8 rows at a time: register v of block (bi, bj) is row
         // 8 (v / 4) + 4 h + v % 4 of the block, column li; pass g takes
         // block row bi = g / 4 and registers 4 (g % 4) .. + 3.  The epilogue
