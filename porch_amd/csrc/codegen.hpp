@@ -219,10 +219,10 @@ namespace porch::cg {
     int64_t gemm_wide_chunks(const gemm_request& request);
     kernel_code emit_gemm_wide(const gemm_request& request);
 
-    // A short K (8 to 64, a multiple of 8) over at least two bands of 128
-    // rows per compute unit and 256 columns or more, A's rows contiguous
-    // along K and B's along N (emit_gemm_band.cpp): one workgroup per band,
-    // its A held in registers, walking the band's column tiles.
+    // A short K (8 to 64, a multiple of 8) over 256 columns or more, A's
+    // rows contiguous along K and B's along N, with two workgroups per
+    // compute unit (emit_gemm_band.cpp): one workgroup per band of 128 rows
+    // and run of at least two column tiles, its A held in registers.
     bool gemm_band(const gemm_request& request);
     kernel_code emit_gemm_band(const gemm_request& request);
 

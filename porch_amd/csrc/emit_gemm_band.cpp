@@ -5,7 +5,9 @@
 // decides the rate.
 //
 //   gemm.band   one workgroup (four waves, two per compute unit) per batch
-//               entry and band of 128 rows, walking the band's column tiles.
+//               entry and band of 128 rows, walking the band's column tiles
+//               (or a run of them, where there are fewer bands than two per
+//               compute unit).
 //               Each wave keeps its 64 rows x K of A in registers as
 //               v_mfma_f32_32x32x2f32 operands for the whole band, with K
 //               permuted so that lane half h takes k = hK/2 + s at step s
@@ -25,7 +27,10 @@
 // texture-address FIFOs were full for about as many cycles as the shader
 // engines were busy; this kernel's never are.  B's tiles are read with
 // plain loads: every band of a batch entry reads them (with non-temporal
-// loads the kernel was no faster than the persistent one, 376.7 us).
+// loads the kernel was no faster than the persistent one, 376.7 us).  With
+// the bands split into runs, against the persistent kernel on one box:
+// [2, 8192, 64] @ [2, 64, 8192] 213.0 against 243.9 us, [4096, 64] @ [64,
+// 4096] 28.8 against 31.6, [6016, 8] @ [8, 3968] 17.5 against 23.0.
 //
 // Sums: each output's K products in the MFMA's order, within the matmul's
 // accumulation bound.
@@ -44,7 +49,31 @@ namespace porch::cg {
         constexpr int64_t b_pitch = tile_cols + 4; // LDS row of B, floats
         constexpr int64_t w_pitch = 64 + 4;        // LDS row of a wave's results, floats
 
-        int64_t bands(const gemm_request& r) { return r.batch * ((r.m + band_rows - 1) / band_rows); }
+        struct band_shape {
+            int64_t per_entry = 0; // bands of 128 rows per batch entry
+            int64_t tiles = 0;     // column tiles of 128
+            int64_t chunks = 0;    // runs of column tiles a band is split into
+            int64_t per_chunk = 0; // column tiles a run
+            int64_t groups = 0;    // workgroups
+        };
+
+        // Two workgroups for every compute unit: the bands, each split into
+        // runs of its column tiles where there are fewer bands than that,
+        // every run at least two tiles (a workgroup loads its rows of A once
+        // for all of its tiles).
+        band_shape band_plan(const gemm_request& r) {
+            band_shape sh;
+            sh.per_entry = (r.m + band_rows - 1) / band_rows;
+            sh.tiles = (r.n + tile_cols - 1) / tile_cols;
+            const int64_t want = 2 * static_cast<int64_t>(std::max(r.compute_units, 8));
+            const int64_t bands = r.batch * sh.per_entry;
+            int64_t chunks = std::max<int64_t>(1, (want + bands - 1) / bands);
+            chunks = std::min(chunks, std::max<int64_t>(1, sh.tiles / 2));
+            sh.per_chunk = (sh.tiles + chunks - 1) / chunks;
+            sh.chunks = (sh.tiles + sh.per_chunk - 1) / sh.per_chunk;
+            sh.groups = bands * sh.chunks;
+            return sh;
+        }
 
     } // namespace
 
@@ -53,18 +82,18 @@ namespace porch::cg {
                             r.a.stride_batch % 4 == 0;
         const bool b_rows = r.b.stride_col == 1 && r.n % 4 == 0 && r.b.offset % 4 == 0 && r.b.stride_row % 4 == 0 &&
                             r.b.stride_batch % 4 == 0;
-        // two column tiles a band at least (the band's A is loaded once for
-        // all of them), and two workgroups for every compute unit
-        return r.k_chunks == 1 && r.k >= 8 && r.k <= max_k && r.k % 8 == 0 && a_runs && b_rows &&
-               r.n >= 2 * tile_cols && bands(r) >= 2 * static_cast<int64_t>(std::max(r.compute_units, 8));
+        if (r.k_chunks != 1 || r.k < 8 || r.k > max_k || r.k % 8 != 0 || !a_runs || !b_rows || r.n < 2 * tile_cols)
+            return false;
+        return band_plan(r).groups >= 2 * static_cast<int64_t>(std::max(r.compute_units, 8));
     }
 
     kernel_code emit_gemm_band(const gemm_request& r) {
         if (!gemm_band(r)) throw std::logic_error("emit_gemm_band: not a short-K band product");
         const char* T = r.width.type();
-        const int64_t per_entry = (r.m + band_rows - 1) / band_rows;
-        const int64_t total = r.batch * per_entry;
-        const int64_t tiles = (r.n + tile_cols - 1) / tile_cols;
+        const band_shape sh = band_plan(r);
+        const int64_t per_entry = sh.per_entry;
+        const int64_t total = sh.groups;
+        const int64_t tiles = sh.tiles;
         const int64_t hk = r.k / 2;                      // MFMA steps (and values a lane holds a row)
         const int64_t b_loads = r.k * tile_cols / 4 / 256; // float4s of B a thread per tile
         const std::string M = std::to_string(r.m);
@@ -97,14 +126,21 @@ namespace porch::cg {
         s += "    const int wm = wave >> 1, wn = wave & 1;\n";
         s += "    const int h = lane >> 5, li = lane & 31;\n";
         // Workgroups are dispatched round-robin over the 8 XCDs: adjacent
-        // bands (which read the same B) go to one XCD where the grid allows.
+        // bands of one run of tiles (which read the same B) go to one XCD
+        // where the grid allows.  Workgroup (batch entry, run, band), the
+        // band fastest.
         if (total % 8 == 0)
             s += "    const idx_t lin = (idx_t)(blockIdx.x % 8) * " + std::to_string(total / 8) + " + blockIdx.x / 8;\n";
         else
             s += "    const idx_t lin = blockIdx.x;\n";
-        s += "    const idx_t qb = lin / " + std::to_string(per_entry) + ";\n";
-        if (!r.batched) s += "    (void)qb;\n";
         s += "    const idx_t m0 = (lin % " + std::to_string(per_entry) + ") * " + std::to_string(band_rows) + ";\n";
+        s += "    const idx_t run = (lin / " + std::to_string(per_entry) + ") % " + std::to_string(sh.chunks) + ";\n";
+        s += "    const idx_t qb = lin / " + std::to_string(per_entry * sh.chunks) + ";\n";
+        if (!r.batched) s += "    (void)qb;\n";
+        // this workgroup's column tiles: t0 .. t0 + count - 1
+        s += "    const int t0 = (int)run * " + std::to_string(sh.per_chunk) + ";\n";
+        s += "    const int count = " + std::to_string(tiles) + " - t0 < " + std::to_string(sh.per_chunk) + " ? " +
+             std::to_string(tiles) + " - t0 : " + std::to_string(sh.per_chunk) + ";\n";
         // A as MFMA operands: af[bi][j] holds row 64 wm + 32 bi + li of the
         // band at k = h K/2 + 4 j .. + 3 (rows past m read at m - 1: they
         // feed only outputs that are not stored)
@@ -139,10 +175,12 @@ namespace porch::cg {
             t += "    }\n";
             return t;
         };
-        s += load_b("0") + write_b("0");
+        // (a run's second tile is loaded ahead even where the run has one:
+        // the columns are clamped into B and the values never used)
+        s += load_b("t0") + write_b("0");
         s += "    __syncthreads();\n";
-        s += load_b("1");
-        s += "    for (int t = 0; t < " + std::to_string(tiles) + "; ++t) {\n";
+        s += load_b("t0 + 1");
+        s += "    for (int t = 0; t < count; ++t) {\n";
         s += "        const int buf = t & 1;\n";
         s += "        floatx16 acc[2][2];\n";
         s += "        #pragma unroll\n        for (int i = 0; i < 2; ++i)\n";
@@ -151,8 +189,8 @@ namespace porch::cg {
         // the next tile into the other buffer (its last readers finished
         // before the previous barrier) and the one after into registers,
         // issued ahead of this tile's MFMAs
-        s += "        if (t + 1 < " + std::to_string(tiles) + ") {\n" + write_b("buf ^ 1") + "        }\n";
-        s += "        if (t + 2 < " + std::to_string(tiles) + ") {\n" + load_b("t + 2") + "        }\n";
+        s += "        if (t + 1 < count) {\n" + write_b("buf ^ 1") + "        }\n";
+        s += "        if (t + 2 < count) {\n" + load_b("t0 + t + 2") + "        }\n";
         s += "        __builtin_amdgcn_sched_barrier(0);\n";
         s += "        #pragma unroll\n        for (int st = 0; st < " + HK + "; ++st) {\n";
         s += "            const float b0 = Bs[buf][" + HK + " * h + st][64 * wn + li];\n";
@@ -174,7 +212,7 @@ namespace porch::cg {
         s += "            #pragma unroll\n            for (int bj = 0; bj < 2; ++bj)\n";
         s += "                #pragma unroll\n                for (int q = 0; q < 4; ++q) {\n";
         s += "                    const idx_t q0 = m0 + 64 * wm + 32 * bi + 8 * (g & 3) + 4 * h + q;\n";
-        s += "                    const idx_t q1 = (idx_t)t * " + std::to_string(tile_cols) + " + 64 * wn + 32 * bj + li;\n";
+        s += "                    const idx_t q1 = (idx_t)(t0 + t) * " + std::to_string(tile_cols) + " + 64 * wn + 32 * bj + li;\n";
         s += "                    const idx_t e0 = q0 < " + M + " ? q0 : (idx_t)" + std::to_string(r.m - 1) + ";\n";
         s += "                    const idx_t e1 = q1 < " + N + " ? q1 : (idx_t)" + std::to_string(r.n - 1) + ";\n";
         s += "                    (void)e0; (void)e1;\n";
@@ -200,7 +238,7 @@ namespace porch::cg {
         s += "                const int f = lane + 64 * u;\n";
         s += "                const int rr = f >> 4, c4 = f & 15;\n";
         s += "                const idx_t q0 = m0 + 64 * wm + 32 * bi + 8 * (g & 3) + rr;\n";
-        s += "                const idx_t q1 = (idx_t)t * " + std::to_string(tile_cols) + " + 64 * wn + 4 * c4;\n";
+        s += "                const idx_t q1 = (idx_t)(t0 + t) * " + std::to_string(tile_cols) + " + 64 * wn + 4 * c4;\n";
         s += "                const porch_v4f x = *reinterpret_cast<const porch_v4f*>(&Ws[wave][rr][4 * c4]);\n";
         const std::string row = r.batched ? "(qb * " + M + " + q0)" : "q0";
         s += "                if (q0 < " + M + " && q1 < " + N + ")\n";

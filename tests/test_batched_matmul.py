@@ -139,8 +139,11 @@ def test_large_products_use_mfma_over_every_entry():
 
 def test_many_tiles_use_persistent_workgroups():
     # more (entry, tile) pairs than two per compute unit: each workgroup
-    # walks tiles, prefetching its next tile during the current one's last step
-    for b, m, k, n in [(32, 1024, 32, 1024), (18, 1024, 40, 1024), (8, 2048, 16, 2048), (16, 1024, 64, 1024)]:
+    # walks tiles, prefetching its next tile during the current one's last
+    # step (fewer than 512 runs of two column tiles, which the band kernel
+    # would take)
+    for b, m, k, n in [(15, 1024, 32, 1024), (14, 1024, 40, 1024), (7, 2048, 16, 1024), (13, 1024, 64, 1024),
+                       (32, 1024, 36, 1024)]:
         plan = porch.plan(plain(placeholder, b, m, k, n))
         (kernel,) = plan["kernels"]
         assert kernel["kind"] == "gemm.mfma" and kernel["grid"][0] == 512, (b, m, k, n)
@@ -195,12 +198,13 @@ def test_batched_real_values_within_float64_bound(gpu):
 # shapes with more tiles than resident workgroups and a short K: even K-step
 # counts (loads two slices ahead) and odd ones (the LDS buffer parity
 # carried across tiles), a ragged K, ragged rows, a single step, and the
-# rank-2 product with a transposed operand
+# rank-2 product with a transposed operand (batch counts kept below the
+# two workgroups a compute unit that would take the band kernel)
 PERSISTENT = [
     (lambda make: plain(make, 12, 1024, 64, 1024)),
-    (lambda make: with_epilogue(make, 18, 1024, 40, 1024)),
+    (lambda make: with_epilogue(make, 14, 1024, 40, 1024)),
     (lambda make: plain(make, 20, 1020, 36, 1024)),
-    (lambda make: shared_weight(make, 24, 1024, 32, 768)),
+    (lambda make: shared_weight(make, 20, 1024, 32, 768)),
     (lambda make: with_epilogue(make, 40, 512, 16, 516)),
     (lambda make: porch.matmul(make([5116, 20]), porch.transpose(make([5120, 20]))) * 2.0),
 ]

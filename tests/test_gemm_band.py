@@ -1,6 +1,6 @@
 """Products with a short K over many bands of rows (kernel kind gemm.band):
-one workgroup per batch entry and 128-row band, A held in registers, the
-band's column tiles walked with B through LDS, results stored as float4
+one workgroup per batch entry, 128-row band and run of column tiles, A held
+in registers, the tiles walked with B through LDS, results stored as float4
 rows through LDS.  The plan's choice, exactness on integer data (in CPU
 emulation and on the GPU, against the oracle) and real data within the
 matmul's accumulation bound (K - 1) 2^-24 sum |a||b| against float64."""
@@ -45,7 +45,23 @@ CASES = {
         lambda p, c: p - c, [1, 1, 300]),
     "unbatched": (
         [65536, 64], [64, 512], lambda p, c: p, lambda p, c: p, None),
+    "runs of column tiles": (
+        [4096, 64], [64, 4096], lambda p, c: p * 2.0, lambda p, c: p * 2.0, None),
+    "runs, the last of one tile, K of 8, bias": (
+        [6016, 8], [8, 3968], lambda p, c: p + porch.broadcast_to(c, [6016, 3968]),
+        lambda p, c: p + c, [1, 3968]),
 }
+
+
+def _groups(sa, sb, cus=256):
+    """Workgroups of the band kernel: bands of 128 rows, each split into
+    runs of at least two column tiles until there are two a CU."""
+    batch = sa[0] if len(sa) == 3 else 1
+    bands = batch * -(-sa[-2] // 128)
+    tiles = -(-sb[-1] // 128)
+    chunks = min(max(1, -(-2 * cus // bands)), max(1, tiles // 2))
+    per = -(-tiles // chunks)
+    return bands * -(-tiles // per)
 
 
 def _graph(name, make):
@@ -60,10 +76,8 @@ def test_band_products_take_the_band_kernel(name):
     expr, _ = _graph(name, lambda s, seed: placeholder(s))
     plan = porch.plan(expr, compile=True)
     assert [k["kind"] for k in plan["kernels"]] == ["gemm.band"]
-    sa = CASES[name][0]
-    rows = sa[-2]
-    batch = sa[0] if len(sa) == 3 else 1
-    assert plan["kernels"][0]["grid"][0] == batch * -(-rows // 128)
+    sa, sb = CASES[name][0], CASES[name][1]
+    assert plan["kernels"][0]["grid"][0] == _groups(sa, sb)
     assert plan["temps"] == []
 
 
@@ -79,15 +93,19 @@ def test_band_bounds():
     assert kind([16, 4096, 64], [16, 64, 256]) == "gemm.band"
     assert kind([16, 4096, 64], [16, 64, 252]) == "gemm.mfma"
     assert kind([16, 4096, 64], [16, 64, 128]) == "gemm.mfma"
-    assert kind([1, 65408, 64], [1, 64, 256]) == "gemm.mfma"   # 511 bands
+    assert kind([1, 65408, 64], [1, 64, 256]) == "gemm.mfma"   # 511 bands of two tiles
     assert kind([1, 65409, 64], [1, 64, 256]) == "gemm.band"   # 512, the last of one row
+    # fewer bands: runs of at least two column tiles, up to two workgroups a CU
+    assert kind([2, 8192, 64], [2, 64, 8192]) == "gemm.band"   # 128 bands x 4 runs
+    assert kind([8, 1024, 64], [8, 64, 1024]) == "gemm.mfma"   # 64 bands x 4 runs of 2
     # B transposed: its rows along N are not contiguous
     assert _kinds(porch.batched_matmul(placeholder([16, 4096, 64]),
                                        porch.permute(placeholder([16, 4096, 64]), [0, 2, 1])))[0] == "gemm.mfma"
 
 
 @needs_clang
-@pytest.mark.parametrize("name", ["bias and relu, K of 16", "ragged last band and tile, K of 8"])
+@pytest.mark.parametrize("name", ["bias and relu, K of 16", "ragged last band and tile, K of 8",
+                                  "runs, the last of one tile, K of 8, bias"])
 def test_emulated_band_products_are_exact(name):
     xs = {}
 
@@ -131,7 +149,7 @@ def test_band_products_within_the_accumulation_bound(gpu, name):
     # the product's bound carried through the epilogue (a scale by 1/8 is
     # exact, relu does not widen an error), plus half an ulp of the result
     # for the one rounded add or subtract after the product
-    scale = 0.125 if name.startswith("attention") else 1.0
+    scale = 0.125 if name.startswith("attention") else 2.0 if name == "runs of column tiles" else 1.0
     slack = scale * bound + np.abs(want) * 2.0 ** -24
     frac = np.abs(out - want) / np.maximum(slack, 1e-300)
     assert np.all(frac <= 1.0), (float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
