@@ -50,6 +50,14 @@ CASES = {
     "runs, the last of one tile, K of 8, bias": (
         [6016, 8], [8, 3968], lambda p, c: p + porch.broadcast_to(c, [6016, 3968]),
         lambda p, c: p + c, [1, 3968]),
+    # staging passes over 10, 6 and 14 steps; non-temporal stores past K = 32
+    "ragged runs, K of 40": (
+        [8, 1000, 40], [8, 40, 2000], lambda p, c: p * 2.0, lambda p, c: p * 2.0, None),
+    "K of 24": (
+        [4, 4096, 24], [4, 24, 1024], lambda p, c: p, lambda p, c: p, None),
+    "K of 56, bias": (
+        [4, 8192, 56], [4, 56, 512], lambda p, c: p + porch.broadcast_to(c, [4, 8192, 512]),
+        lambda p, c: p + c, [1, 1, 512]),
 }
 
 
@@ -105,7 +113,7 @@ def test_band_bounds():
 
 @needs_clang
 @pytest.mark.parametrize("name", ["bias and relu, K of 16", "ragged last band and tile, K of 8",
-                                  "runs, the last of one tile, K of 8, bias"])
+                                  "runs, the last of one tile, K of 8, bias", "ragged runs, K of 40"])
 def test_emulated_band_products_are_exact(name):
     xs = {}
 
@@ -149,7 +157,7 @@ def test_band_products_within_the_accumulation_bound(gpu, name):
     # the product's bound carried through the epilogue (a scale by 1/8 is
     # exact, relu does not widen an error), plus half an ulp of the result
     # for the one rounded add or subtract after the product
-    scale = 0.125 if name.startswith("attention") else 2.0 if name == "runs of column tiles" else 1.0
+    scale = 0.125 if name.startswith("attention") else 2.0 if name in ("runs of column tiles", "ragged runs, K of 40") else 1.0
     slack = scale * bound + np.abs(want) * 2.0 ** -24
     frac = np.abs(out - want) / np.maximum(slack, 1e-300)
     assert np.all(frac <= 1.0), (float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
