@@ -161,3 +161,72 @@ def test_band_products_within_the_accumulation_bound(gpu, name):
     slack = scale * bound + np.abs(want) * 2.0 ** -24
     frac = np.abs(out - want) / np.maximum(slack, 1e-300)
     assert np.all(frac <= 1.0), (float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
+
+
+def _random_band_graph(make, form, b, m, k, n, epi):
+    """Graph `form` of a short-K product: 0 batched, 1 unbatched, 2 one
+    weight shared by every entry (B a broadcast view), with epilogue `epi`
+    (0 none, 1 a scale, 2 relu of a bias add, less a half, 3 a bias
+    subtracted)."""
+    if form == 1:
+        p = porch.matmul(make([m, k]), make([k, n]))
+        out_shape, bias_shape = [m, n], [1, n]
+    elif form == 2:
+        p = porch.batched_matmul(make([b, m, k]), porch.broadcast_to(make([k, n]), [b, k, n]))
+        out_shape, bias_shape = [b, m, n], [1, 1, n]
+    else:
+        p = porch.batched_matmul(make([b, m, k]), make([b, k, n]))
+        out_shape, bias_shape = [b, m, n], [1, 1, n]
+    if epi == 1:
+        return p * 0.25
+    if epi == 2:
+        return porch.relu(p + porch.broadcast_to(make(bias_shape), out_shape)) - 0.5
+    if epi == 3:
+        return p - porch.broadcast_to(make(bias_shape), out_shape)
+    return p
+
+
+def random_band_product(rng):
+    """Shape and form of a product the band kernel takes, drawn until the
+    plan says so: K of 8 to 64 in steps of 8, 256 to 3196 columns (a
+    multiple of 4, the last tile often ragged), ragged row counts, batched,
+    unbatched or with a shared weight, and a random epilogue; at most 40 M
+    outputs."""
+    while True:
+        k = 8 * int(rng.integers(1, 9))
+        n = 4 * int(rng.integers(64, 800))
+        form = int(rng.integers(0, 3))
+        b = 1 if form == 1 else int(rng.integers(1, 9))
+        m = int(rng.integers(100, 20000))
+        epi = int(rng.integers(0, 4))
+        if b * m * n > 40_000_000:
+            continue
+        expr = _random_band_graph(lambda s: placeholder(s), form, b, m, k, n, epi)
+        if _kinds(expr) == ["gemm.band"]:
+            return form, b, m, k, n, epi
+
+
+def test_random_band_products_plan_as_band():
+    rng = np.random.default_rng(21)
+    shapes = [random_band_product(rng) for _ in range(12)]
+    assert len({s[3] for s in shapes}) >= 4            # several K
+    assert any(s[2] % 128 for s in shapes) and any(s[4] % 128 for s in shapes)  # ragged edges
+
+
+@pytest.mark.gpu
+def test_random_band_products_bit_exact(gpu):
+    rng = np.random.default_rng(21)
+    data = np.random.default_rng(22)
+    for trial in range(12):
+        form, b, m, k, n, epi = random_band_product(rng)
+
+        def make(shape):
+            return gpu.tensor(list(shape), _ints(shape, int(data.integers(0, 1 << 30))).reshape(-1))
+
+        expr = _random_band_graph(make, form, b, m, k, n, epi)
+        plan = gpu.plan(expr)
+        print("band fuzz", trial, (form, b, m, k, n, epi), plan["kernels"][0]["grid"][0], flush=True)
+        assert [x["kind"] for x in plan["kernels"]] == ["gemm.band"]
+        out = gpu.materialize(expr).cpu()
+        ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, form, b, m, k, n, epi)
