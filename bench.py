@@ -464,6 +464,50 @@ extern "C" __global__ void __launch_bounds__(256) porch_control_stream(
     for (int r = 0; r < 4; ++r)
         __builtin_nontemporal_store(__builtin_nontemporal_load(x + g + r * count), y + g + r * count);
 }
+// The wide product's B [4096, 4096] (a0) read alone, 256 workgroups (count =
+// 65536 lanes), nothing stored unless a lane's sum is 1234.5 (never, for the
+// workload's inputs): "strips" reads it as the wide product's split kernel
+// does (workgroup = 64 columns by a quarter of K; wave w, group g: rows
+// k0 + 16 w + 64 g + 4 (lane / 16) + j, 256 B of each), two groups of four
+// float4 a lane in flight; "blocks" reads workgroup b's contiguous 256 KB,
+// sixteen float4 a lane in flight.
+extern "C" __global__ void __launch_bounds__(256) porch_control_strips(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, li = lane & 15, lg = lane >> 4;
+    const int c0 = (blockIdx.x / 4) * 64, k0 = (blockIdx.x % 4) * 1024;
+    porch_v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    porch_v4f b[2][4];
+    for (int g = 0; g < 2; ++g)
+        for (int j = 0; j < 4; ++j)
+            b[g][j] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(
+                a0 + (unsigned long long)(k0 + 16 * w + 64 * g + 4 * lg + j) * 4096 + c0 + 4 * li));
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+        for (int j = 0; j < 4; ++j) acc += b[g & 1][j];
+        if (g + 2 < 16)
+            for (int j = 0; j < 4; ++j)
+                b[g & 1][j] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(
+                    a0 + (unsigned long long)(k0 + 16 * w + 64 * (g + 2) + 4 * lg + j) * 4096 + c0 + 4 * li));
+    }
+    const float s = (acc.x + acc.y) + (acc.z + acc.w);
+    if (s == 1234.5f) out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+extern "C" __global__ void __launch_bounds__(256) porch_control_blocks(
+    const float* __restrict__ a0, const float* __restrict__ a1, float* __restrict__ out,
+    unsigned long long count) {
+    const porch_v4f* x = reinterpret_cast<const porch_v4f*>(a0) + blockIdx.x * 16384ull;
+    porch_v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = threadIdx.x; i < 16384; i += 4096) {
+        porch_v4f v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = __builtin_nontemporal_load(x + i + 256 * u);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc += v[u];
+    }
+    const float s = (acc.x + acc.y) + (acc.z + acc.w);
+    if (s == 1234.5f) out[blockIdx.x * 256 + threadIdx.x] = s;
+}
 """
 
 
@@ -471,7 +515,8 @@ def controls(launches: int) -> int:
     """Each control kernel, then the elementwise workload's own kernel,
     `launches` times each over rotated (cache-cold) buffers; then the view
     chain's bytes moved in coalesced order and that workload itself; then
-    a plain copy of the vocabulary softmax's bytes and that workload,
+    a plain copy of the vocabulary softmax's bytes and that workload; then
+    two read-only passes over the wide product's B and that workload,
     `launches` times each; timed by the profiler this runs under
     (rocprofv3 --kernel-trace --stats)."""
     import porch_amd as porch
@@ -560,6 +605,28 @@ def controls(launches: int) -> int:
         porch.materialize(config_graph("vocab_softmax", [x]))
     porch.synchronize()
     log(f"controls: vocab_softmax workload x {launches}")
+    del x, y
+
+    # The wide product beside kernels that only read its B, over rotated B
+    # copies: its split kernel reads B at the wide product's geometry.
+    a_shape, b_shape = config_shapes("wide_product")
+    a_values, b_values = config_inputs("wide_product")
+    copies = ROTATION["wide_product"]
+    a = porch.tensor(a_shape, a_values)
+    bs = [porch.tensor(b_shape, b_values) for _ in range(copies)]
+    sink = porch.zeros([65536]).realize()
+    for kernel in (b"porch_control_strips", b"porch_control_blocks"):
+        for i in range(launches):
+            h = bs[i % copies].device_data().handle
+            ins = (ctypes.c_void_p * 2)(h, h)
+            _lib.check(_lib.lib.porch_launch_fused_elementwise(
+                data, size, kernel, ins, 2, sink.device_data().handle, 65536))
+        porch.synchronize()
+        log(f"controls: {kernel.decode()} x {launches}")
+    for i in range(launches):
+        porch.materialize(config_graph("wide_product", [a, bs[i % copies]]))
+    porch.synchronize()
+    log(f"controls: wide_product workload x {launches}")
     _lib.lib.porch_code_object_release(code)
     return 0
 
