@@ -26,6 +26,10 @@
 //                 four), B read per lane from the L2; the waves' sums added
 //                 through LDS, the chunks' partial products summed by
 //                 gemm.combine.
+//   gemm.narrow_rows  7 to 16 columns over 4096 rows or more: a workgroup
+//                 per 16 rows over all of K, the rows' values staged
+//                 through LDS into the MFMA layout, no partial products
+//                 (its constants below say more).
 //   gemm.wide     the same blocks the other way round, few rows (up to 64)
 //                 over many columns: a workgroup of four waves per 64
 //                 columns and a chunk of K, the waves taking its groups of
