@@ -29,8 +29,9 @@ for a copy kernel of known size; both come from the counter summaries under
 profiles/ (null when a workload has none).
 
     python bench.py [--steps K] [--warmup W] [--configs view_chain,...] [--no-cpu]
-    python bench.py --controls LAUNCHES   (control kernels beside the elementwise and
-                                          vocabulary-softmax workloads, under rocprofv3)
+    python bench.py --controls LAUNCHES   (control kernels beside the elementwise, view
+                                          chain, vocabulary-softmax and wide-product
+                                          workloads, under rocprofv3)
 """
 
 from __future__ import annotations
@@ -642,7 +643,7 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--jit-probe", default=None, help=argparse.SUPPRESS)
     parser.add_argument("--controls", type=int, default=0, metavar="LAUNCHES",
-                        help="launch the elementwise control kernels (for rocprofv3) and exit")
+                        help="launch the control kernels beside their workloads (for rocprofv3) and exit")
     args = parser.parse_args()
     if args.jit_probe:
         return jit_probe(args.jit_probe)
