@@ -220,7 +220,8 @@ namespace porch::cg {
     kernel_code emit_gemm_wide(const gemm_request& request);
 
     // A short K (8 to 64, a multiple of 8) over 256 columns or more, A's
-    // rows contiguous along K and B's along N, with two workgroups per
+    // rows contiguous along K and B's rows along N or its columns along K
+    // (B stored transposed), with two workgroups per
     // compute unit (emit_gemm_band.cpp): one workgroup per band of 128 rows
     // and run of at least two column tiles, its A held in registers.
     bool gemm_band(const gemm_request& request);

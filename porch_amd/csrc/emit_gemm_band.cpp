@@ -13,7 +13,10 @@
 //               permuted so that lane half h takes k = hK/2 + s at step s
 //               (a lane's K/2 values are one run, read as float4s); only
 //               the K x 128 tile of B goes through LDS, double-buffered,
-//               the next tile's loads one tile ahead in registers.  A
+//               the next tile's loads one tile ahead in registers (B's
+//               rows read along N, or, where B is stored transposed as in
+//               q @ k^T with k [n, K], its columns read along K and
+//               written to LDS transposed).  A
 //               wave's 64 x 64 of a tile is two halves of 64 x 32: the
 //               MFMAs of one half run while the other half's results (of
 //               this tile or the previous one), with the epilogue applied,
@@ -41,6 +44,9 @@
 // 4096, 32] @ [16, 32, 4096] 261.9 against 266.5; at K of 8 and 16 within
 // 1-2 %.  In the benchmark, alternating runs on one box: attention 309.4
 // against 324.3-325.2 us (70.6 % against 67.3 % of the fp32 MFMA peak).
+// With k^T a view (B's columns along K), the attention product under the
+// tracer on one (slow) box: 383.0 us, against 371.2 for k^T stored and
+// 436.1 for the persistent kernel that took the view before.
 //
 // Sums: each output's K products in the MFMA's order, within the matmul's
 // accumulation bound.
@@ -57,6 +63,10 @@ namespace porch::cg {
         constexpr int64_t tile_cols = 128;
         constexpr int64_t max_k = 64;
         constexpr int64_t b_pitch = tile_cols + 4; // LDS row of B, floats
+        // LDS row of B read from columns along K: 129 = 1 mod 64, so the
+        // scalar writes of a wave (16 k-quads x 4 columns) and the MFMA-side
+        // reads (32 columns of two rows K/2 apart) meet 64 different banks
+        constexpr int64_t b_pitch_cols = tile_cols + 1;
         constexpr int64_t w_pitch = 32 + 4;        // LDS row of a wave's staged results, floats
 
         struct band_shape {
@@ -85,14 +95,24 @@ namespace porch::cg {
             return sh;
         }
 
+        // B's rows contiguous along N (read as float4 rows of a tile)
+        bool b_rows(const gemm_request& r) {
+            return r.b.stride_col == 1 && r.b.offset % 4 == 0 && r.b.stride_row % 4 == 0 && r.b.stride_batch % 4 == 0;
+        }
+
+        // B's columns contiguous along K, as in q @ k^T with k stored [n, K]
+        // (read as float4 runs of a column, written to LDS transposed)
+        bool b_cols(const gemm_request& r) {
+            return r.b.stride_row == 1 && r.b.offset % 4 == 0 && r.b.stride_col % 4 == 0 && r.b.stride_batch % 4 == 0;
+        }
+
     } // namespace
 
     bool gemm_band(const gemm_request& r) {
         const bool a_runs = r.a.stride_col == 1 && r.a.offset % 4 == 0 && r.a.stride_row % 4 == 0 &&
                             r.a.stride_batch % 4 == 0;
-        const bool b_rows = r.b.stride_col == 1 && r.n % 4 == 0 && r.b.offset % 4 == 0 && r.b.stride_row % 4 == 0 &&
-                            r.b.stride_batch % 4 == 0;
-        if (r.k_chunks != 1 || r.k < 8 || r.k > max_k || r.k % 8 != 0 || !a_runs || !b_rows || r.n < 2 * tile_cols)
+        if (r.k_chunks != 1 || r.k < 8 || r.k > max_k || r.k % 8 != 0 || !a_runs || r.n % 4 != 0 ||
+            !(b_rows(r) || b_cols(r)) || r.n < 2 * tile_cols)
             return false;
         return band_plan(r).groups >= 2 * static_cast<int64_t>(std::max(r.compute_units, 8));
     }
@@ -117,7 +137,8 @@ namespace porch::cg {
         const std::string HK = std::to_string(hk);
         const std::string BL = std::to_string(b_loads);
         const std::string TC = std::to_string(tile_cols);
-        const std::string BP = std::to_string(b_pitch);
+        const bool transposed = !b_rows(r); // B's columns contiguous along K
+        const std::string BP = std::to_string(transposed ? b_pitch_cols : b_pitch);
         const std::string WP = std::to_string(w_pitch);
         const std::string batch = r.batched ? "qb" : "";
         const std::string last = "t0 + count - 1";
@@ -171,19 +192,30 @@ namespace porch::cg {
         s += "            af[bi][j] = *reinterpret_cast<const porch_v4f*>(" + aslot + " + " +
              operand_index(r.a, "qa", HK + " * h + 4 * j", batch) + ");\n";
         s += "    }\n";
-        // B's tile nt: thread tid takes float4 f = tid + 256 u, row f / 32,
-        // columns 4 (f % 32) .. + 3 (columns past n read at n - 4)
+        // B's tile nt, rows along N: thread tid takes float4 f = tid + 256 u,
+        // row f / 32, columns 4 (f % 32) .. + 3 (columns past n read at
+        // n - 4).  Columns along K: float4 f holds k = 4 (f % (K / 4)) .. + 3
+        // of column f / (K / 4) (columns past n read at n - 1), written to
+        // LDS as four rows of one column.
+        const std::string KQ = std::to_string(r.k / 4);
         s += "    porch_v4f rb[" + BL + "];\n";
         auto load_b = [&](const std::string& nt) {
             std::string t;
             t += "    {\n        const int nt = " + nt + ";\n";
             t += "        #pragma unroll\n        for (int u = 0; u < " + BL + "; ++u) {\n";
             t += "            const int f = tid + 256 * u;\n";
-            t += "            const idx_t c = (idx_t)nt * " + TC + " + 4 * (f & 31);\n";
-            t += "            const idx_t cc = c < " + N + " ? c : (idx_t)" + std::to_string(r.n - 4) + ";\n";
-            // plain loads: every band of a batch entry reads the same tiles
-            t += "            rb[u] = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
-                 operand_index(r.b, "(f >> 5)", "cc", batch) + ");\n";
+            if (transposed) {
+                t += "            const idx_t c = (idx_t)nt * " + TC + " + f / " + KQ + ";\n";
+                t += "            const idx_t cc = c < " + N + " ? c : (idx_t)" + std::to_string(r.n - 1) + ";\n";
+                t += "            rb[u] = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                     operand_index(r.b, "4 * (f % " + KQ + ")", "cc", batch) + ");\n";
+            } else {
+                t += "            const idx_t c = (idx_t)nt * " + TC + " + 4 * (f & 31);\n";
+                t += "            const idx_t cc = c < " + N + " ? c : (idx_t)" + std::to_string(r.n - 4) + ";\n";
+                // plain loads: every band of a batch entry reads the same tiles
+                t += "            rb[u] = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                     operand_index(r.b, "(f >> 5)", "cc", batch) + ");\n";
+            }
             t += "        }\n    }\n";
             return t;
         };
@@ -191,7 +223,12 @@ namespace porch::cg {
             std::string t;
             t += "    #pragma unroll\n    for (int u = 0; u < " + BL + "; ++u) {\n";
             t += "        const int f = tid + 256 * u;\n";
-            t += "        *reinterpret_cast<porch_v4f*>(&Bs[" + buf + "][f >> 5][4 * (f & 31)]) = rb[u];\n";
+            if (transposed) {
+                t += "        #pragma unroll\n        for (int e = 0; e < 4; ++e)\n";
+                t += "            Bs[" + buf + "][4 * (f % " + KQ + ") + e][f / " + KQ + "] = rb[u][e];\n";
+            } else {
+                t += "        *reinterpret_cast<porch_v4f*>(&Bs[" + buf + "][f >> 5][4 * (f & 31)]) = rb[u];\n";
+            }
             t += "    }\n";
             return t;
         };

@@ -106,9 +106,12 @@ def test_band_bounds():
     # fewer bands: runs of at least two column tiles, up to two workgroups a CU
     assert kind([2, 8192, 64], [2, 64, 8192]) == "gemm.band"   # 128 bands x 4 runs
     assert kind([8, 1024, 64], [8, 64, 1024]) == "gemm.mfma"   # 64 bands x 4 runs of 2
-    # B transposed: its rows along N are not contiguous
+    # B stored transposed (k^T as a view of k [n, K]): read along K
     assert _kinds(porch.batched_matmul(placeholder([16, 4096, 64]),
-                                       porch.permute(placeholder([16, 4096, 64]), [0, 2, 1])))[0] == "gemm.mfma"
+                                       porch.permute(placeholder([16, 4096, 64]), [0, 2, 1])))[0] == "gemm.band"
+    # neither B's rows nor its columns contiguous: a strided view of both
+    assert _kinds(porch.batched_matmul(placeholder([16, 4096, 64]),
+                                       placeholder([16, 128, 8192])[:, ::2, ::2]))[0] == "gemm.mfma"
 
 
 @needs_clang
@@ -230,3 +233,86 @@ def test_random_band_products_bit_exact(gpu):
         out = gpu.materialize(expr).cpu()
         ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (trial, form, b, m, k, n, epi)
+
+
+# B stored transposed: (A shape, shape of the tensor whose transpose is B,
+# graph over (product, bias or None), epilogue on the float64 product and
+# bias, bias shape or None)
+TRANSPOSED = {
+    "attention-shaped, k^T a view": (
+        [4, 4096, 64], [4, 2048, 64], lambda p, c: p * 0.125, lambda p, c: p * 0.125, None),
+    "unbatched, ragged tile, K of 32, bias": (
+        [16384, 32], [1000, 32], lambda p, c: p + porch.broadcast_to(c, [16384, 1000]),
+        lambda p, c: p + c, [1, 1000]),
+    "ragged band, K of 8": (
+        [2, 32700, 8], [2, 300, 8], lambda p, c: p, lambda p, c: p, None),
+}
+
+
+def _transposed_graph(name, make):
+    sa, sk, graph, _, sbias = TRANSPOSED[name]
+    tensors = [make(sa, 1), make(sk, 2)] + ([make(sbias, 3)] if sbias else [])
+    if len(sa) == 3:
+        p = porch.batched_matmul(tensors[0], porch.permute(tensors[1], [0, 2, 1]))
+    else:
+        p = porch.matmul(tensors[0], porch.transpose(tensors[1]))
+    return graph(p, tensors[2] if sbias else None)
+
+
+@pytest.mark.parametrize("name", sorted(TRANSPOSED))
+def test_transposed_b_takes_the_band_kernel(name):
+    expr = _transposed_graph(name, lambda s, seed: placeholder(s))
+    plan = porch.plan(expr, compile=True)
+    assert [k["kind"] for k in plan["kernels"]] == ["gemm.band"]
+    sa, sk = TRANSPOSED[name][0], TRANSPOSED[name][1]
+    sb = sk[:-2] + [sk[-1], sk[-2]]
+    assert plan["kernels"][0]["grid"][0] == _groups(sa, sb)
+    # B's columns are read in place (no copy of the transpose)
+    assert plan["temps"] == []
+
+
+@needs_clang
+@pytest.mark.parametrize("name", ["ragged band, K of 8"])
+def test_emulated_transposed_b_is_exact(name):
+    xs = {}
+
+    def make(shape, seed):
+        xs[seed] = _ints(shape, seed)
+        return placeholder(shape, xs[seed])
+
+    expr = _transposed_graph(name, make)
+    assert _kinds(expr) == ["gemm.band"]
+    assert all(r["ok"] for r in emu.emulate(expr, timeout=900))
+    got = emu.evaluate(expr, [xs[s] for s in sorted(xs)], timeout=900)
+    want = np.asarray(host.evaluate(expr), np.float32)
+    assert np.array_equal(got.reshape(want.shape), want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(TRANSPOSED))
+def test_transposed_b_bit_exact_on_integers(gpu, name):
+    expr = _transposed_graph(name, lambda s, seed: gpu.tensor(s, _ints(s, seed).reshape(-1)))
+    assert [k["kind"] for k in gpu.plan(expr)["kernels"]] == ["gemm.band"]
+    out = gpu.materialize(expr).cpu()
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(-1)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(TRANSPOSED))
+def test_transposed_b_within_the_accumulation_bound(gpu, name):
+    sa, sk, _, epi, sbias = TRANSPOSED[name]
+    vals = {1: _reals(sa, 31), 2: _reals(sk, 32)}
+    if sbias:
+        vals[3] = _reals(sbias, 33)
+    expr = _transposed_graph(name, lambda s, seed: gpu.tensor(s, vals[seed].reshape(-1)))
+    out = gpu.materialize(expr).cpu().reshape(expr.shape()).astype(np.float64)
+    a64 = vals[1].astype(np.float64)
+    b64 = np.swapaxes(vals[2].astype(np.float64), -1, -2)
+    k = sa[-1]
+    bound = (k - 1) * 2.0 ** -24 * np.matmul(np.abs(a64), np.abs(b64))
+    want = epi(np.matmul(a64, b64), vals[3].astype(np.float64) if sbias else None)
+    scale = 0.125 if name.startswith("attention") else 1.0
+    slack = scale * bound + np.abs(want) * 2.0 ** -24
+    frac = np.abs(out - want) / np.maximum(slack, 1e-300)
+    assert np.all(frac <= 1.0), (float(frac.max()), np.unravel_index(frac.argmax(), frac.shape))
