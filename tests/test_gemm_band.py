@@ -168,11 +168,18 @@ def test_band_products_within_the_accumulation_bound(gpu, name):
 
 def _random_band_graph(make, form, b, m, k, n, epi):
     """Graph `form` of a short-K product: 0 batched, 1 unbatched, 2 one
-    weight shared by every entry (B a broadcast view), with epilogue `epi`
-    (0 none, 1 a scale, 2 relu of a bias add, less a half, 3 a bias
-    subtracted)."""
+    weight shared by every entry (B a broadcast view), 3 batched and 4
+    unbatched with B stored transposed (a permuted or transposed view),
+    with epilogue `epi` (0 none, 1 a scale, 2 relu of a bias add, less a
+    half, 3 a bias subtracted)."""
     if form == 1:
         p = porch.matmul(make([m, k]), make([k, n]))
+        out_shape, bias_shape = [m, n], [1, n]
+    elif form == 3:
+        p = porch.batched_matmul(make([b, m, k]), porch.permute(make([b, n, k]), [0, 2, 1]))
+        out_shape, bias_shape = [b, m, n], [1, 1, n]
+    elif form == 4:
+        p = porch.matmul(make([m, k]), porch.transpose(make([n, k])))
         out_shape, bias_shape = [m, n], [1, n]
     elif form == 2:
         p = porch.batched_matmul(make([b, m, k]), porch.broadcast_to(make([k, n]), [b, k, n]))
@@ -193,13 +200,13 @@ def random_band_product(rng):
     """Shape and form of a product the band kernel takes, drawn until the
     plan says so: K of 8 to 64 in steps of 8, 256 to 3196 columns (a
     multiple of 4, the last tile often ragged), ragged row counts, batched,
-    unbatched or with a shared weight, and a random epilogue; at most 40 M
-    outputs."""
+    unbatched, with a shared weight or with B stored transposed, and a
+    random epilogue; at most 40 M outputs."""
     while True:
         k = 8 * int(rng.integers(1, 9))
         n = 4 * int(rng.integers(64, 800))
-        form = int(rng.integers(0, 3))
-        b = 1 if form == 1 else int(rng.integers(1, 9))
+        form = int(rng.integers(0, 5))
+        b = 1 if form in (1, 4) else int(rng.integers(1, 9))
         m = int(rng.integers(100, 20000))
         epi = int(rng.integers(0, 4))
         if b * m * n > 40_000_000:
@@ -214,6 +221,8 @@ def test_random_band_products_plan_as_band():
     shapes = [random_band_product(rng) for _ in range(12)]
     assert len({s[3] for s in shapes}) >= 4            # several K
     assert any(s[2] % 128 for s in shapes) and any(s[4] % 128 for s in shapes)  # ragged edges
+    forms = {s[0] for s in shapes}
+    assert len(forms) >= 4 and forms & {3, 4}            # B stored transposed among them
 
 
 @pytest.mark.gpu
