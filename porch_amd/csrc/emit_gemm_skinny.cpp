@@ -36,7 +36,15 @@
 //                 16 values in turn; lane l reads B's rows at
 //                 columns 4 (l % 16) .. + 3 with 128-bit loads, so that MFMA
 //                 e covers the 16 columns 4 (l % 16) + e, and A's row l % 16
-//                 from the L2; the waves' sums are added through LDS.
+//                 from the L2; the waves' sums are added through LDS.  Where
+//                 B is stored transposed (x @ W^T with a weight W [n, K]),
+//                 lane l reads column 16 e + l % 16 at its four k with one
+//                 128-bit load, so that MFMA e covers 16 adjacent columns
+//                 (x [32, 4096] @ W^T: 21.1 + 4.0 us, against 42.5 + 4.8
+//                 for the split MFMA kernel that took it before; x @ W
+//                 with W stored [K, n]: 15.0 + 4.0).  gemm.narrow_rows reads
+//                 such a B's four values of a group as one 128-bit load too
+//                 ([4096, 4096] @ w^T, w [16, 4096]: 19.3 against 38.6 us).
 //
 // Sums run in other orders than the reference's sequential K loop, within
 // the matmul's tolerance (an accumulation-bound per element).
@@ -79,6 +87,13 @@ namespace porch::cg {
         constexpr int group_depth = 2; // groups in flight per wave
 
         bool big_enough(const gemm_request& r) { return r.batch * r.m * r.n * r.k >= (int64_t{1} << 18); }
+
+        // B's columns contiguous along K in aligned quads (B stored
+        // transposed, as in x @ w^T with a weight w [n, K])
+        bool b_column_runs(const gemm_request& r) {
+            return r.b.stride_row == 1 && r.b.stride_col % 4 == 0 && r.b.offset % 4 == 0 &&
+                   r.b.stride_batch % 4 == 0 && r.k % 4 == 0;
+        }
 
         bool b_vector(const gemm_request& r) {
             return r.b.stride_col == 1 && r.n % 4 == 0 && r.b.offset % 4 == 0 && r.b.stride_row % 4 == 0 &&
@@ -206,7 +221,10 @@ namespace porch::cg {
 
         wide_shape wide_plan(const gemm_request& r) {
             wide_shape sh;
-            if (r.m < wide_min_rows || r.m > wide_max_rows || r.n < 256 || !b_vector(r) || !big_enough(r)) return sh;
+            // B's rows read along N, or its columns along K where B is
+            // stored transposed (then in whole groups of 16 values of K)
+            const bool b_ok = b_vector(r) || (b_column_runs(r) && r.k % group_size == 0);
+            if (r.m < wide_min_rows || r.m > wide_max_rows || r.n < 256 || !b_ok || !big_enough(r)) return sh;
             sh.rb = (r.m + 15) / 16;
             sh.tiles = (r.n + 63) / 64;
             // About one workgroup (four waves) per compute unit, partials
@@ -590,6 +608,22 @@ namespace porch::cg {
                 s += "        const bool full = kbeg + " + std::to_string((n + 1) * rows_round) + " <= kend;\n";
                 auto b_loads = [&](bool clamp) {
                     std::string t;
+                    if (b_column_runs(r)) {
+                        // B stored transposed (w^T of a weight w [n, K]):
+                        // the lane's four values of group q are one float4
+                        // of column li (a quad past the wave's range reads
+                        // k = 0 and is masked in the MFMAs)
+                        t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q) {\n";
+                        t += "                const idx_t k = kbeg + " + std::to_string(n * rows_round) +
+                             " + q * 16 + lg * 4;\n";
+                        t += std::string("                const idx_t kr = ") +
+                             (clamp ? "k < kend ? k : (idx_t)0" : "k") + ";\n";
+                        t += "                const porch_v4f bq = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                             operand_index(r.b, "kr", "qc", batch) + ");\n";
+                        t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) bv[q][e] = bq[e];\n";
+                        t += "            }\n";
+                        return t;
+                    }
                     t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q)\n";
                     t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) {\n";
                     t += "                    const idx_t k = kbeg + " + std::to_string(n * rows_round) +
@@ -814,6 +848,9 @@ namespace porch::cg {
         if (sh.rb == 0) throw std::logic_error("emit_gemm_wide: not a wide product");
         const bool final = sh.chunks == 1;
         const bool avec = a_vector(r);
+        // B stored transposed: its columns read along K, lane l taking the
+        // columns c0 + 16 e + l % 16
+        const bool bt = !b_vector(r);
         const char* T = r.width.type();
         const std::string batch = r.batched ? "qb" : "";
         const std::string M = std::to_string(r.m);
@@ -859,7 +896,15 @@ namespace porch::cg {
         s += "        const idx_t q0 = i * 16 + li;\n";
         s += "        qa[i] = q0 < " + M + " ? q0 : (idx_t)" + std::to_string(r.m - 1) + ";\n";
         s += "    }\n";
-        s += "    const idx_t qc = c0 + li * 4 < " + N + " ? c0 + li * 4 : (idx_t)" + std::to_string(r.n - 4) + ";\n";
+        if (bt) {
+            s += "    idx_t qc[4];\n";
+            s += "    #pragma unroll\n    for (int e = 0; e < 4; ++e) {\n";
+            s += "        const idx_t c = c0 + 16 * e + li;\n";
+            s += "        qc[e] = c < " + N + " ? c : (idx_t)" + std::to_string(r.n - 1) + ";\n";
+            s += "    }\n";
+        } else {
+            s += "    const idx_t qc = c0 + li * 4 < " + N + " ? c0 + li * 4 : (idx_t)" + std::to_string(r.n - 4) + ";\n";
+        }
         // A group: 16 values of K from kq.  MFMA j of the group gives lane l
         // k = kq + 4 (l / 16) + j: B's row there at columns qc .. qc + 3 (one
         // 128-bit load a j: 4 rows x 256 B an instruction; MFMA e takes
@@ -872,9 +917,17 @@ namespace porch::cg {
         };
         auto loads = [&](const std::string& set, const std::string& kq, const std::string& ind) {
             std::string t;
-            t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < 4; ++j)\n";
-            t += ind + "    bv" + set + "[j] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot +
-                 " + " + operand_index(r.b, "(" + kq + " + lg * 4 + j)", "qc", batch) + "));\n";
+            if (bt) {
+                // column qc[e] at the lane's four k: one 128-bit load each
+                // (16 columns x 64 B an instruction)
+                t += ind + "#pragma unroll\n" + ind + "for (int e = 0; e < 4; ++e)\n";
+                t += ind + "    bv" + set + "[e] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot +
+                     " + " + operand_index(r.b, "(" + kq + " + lg * 4)", "qc[e]", batch) + "));\n";
+            } else {
+                t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < 4; ++j)\n";
+                t += ind + "    bv" + set + "[j] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot +
+                     " + " + operand_index(r.b, "(" + kq + " + lg * 4 + j)", "qc", batch) + "));\n";
+            }
             t += ind + "#pragma unroll\n" + ind + "for (int i = 0; i < " + RB + "; ++i) {\n";
             if (avec) {
                 t += ind + "    av" + set + "[i] = *reinterpret_cast<const porch_v4f*>(" + aslot + " + " +
@@ -894,7 +947,7 @@ namespace porch::cg {
             t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
             t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
             t += ind + "            acc[i][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[i][j], bv" + set +
-                 "[j][e], acc[i][e], 0, 0, 0);\n";
+                 (bt ? "[e][j]" : "[j][e]") + ", acc[i][e], 0, 0, 0);\n";
             return t;
         };
         s += group_loop(r.k % sh.chunk == 0 ? sh.chunk / (group_waves * group_size) : 0, declare, loads, mfmas);
@@ -903,6 +956,8 @@ namespace porch::cg {
         // the wave whose turn it is: lanes past the chunk read its last
         // value and zero both operands.
         if (sh.chunk % group_size != 0 || r.k % group_size != 0) {
+            if (bt) throw std::logic_error("emit_gemm_wide: B read along K needs whole groups");
+            if (bt) throw std::logic_error("emit_gemm_wide: B read along K needs whole groups");
             s += "    if (full * " + G16 + " < k1 - k0 && full % 4 == w) {\n";
             s += "        const idx_t kq = k0 + full * " + G16 + ";\n";
             s += declare("R", "        ");
@@ -921,7 +976,8 @@ namespace porch::cg {
             s += "    }\n";
         }
         // The waves' sums, added in wave order through LDS; each thread
-        // then holds four adjacent columns of one row.
+        // then holds four adjacent columns of one row (B read along K: the
+        // columns c0 + 16 e + l % 16).
         s += "    __shared__ porch_v4f red[4][" + std::to_string(4 * sh.rb) + "][64];\n";
         s += "    #pragma unroll\n    for (int i = 0; i < " + RB + "; ++i)\n";
         s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e) red[w][i * 4 + e][lane] = acc[i][e];\n";
@@ -929,7 +985,7 @@ namespace porch::cg {
         s += "    for (int t = threadIdx.x; t < " + std::to_string(256 * sh.rb) + "; t += 256) {\n";
         s += "        const int i = t >> 8, v = (t >> 6) & 3, l = t & 63;\n";
         s += "        const idx_t q0 = i * 16 + (l >> 4) * 4 + v;\n";
-        s += "        const idx_t qc4 = c0 + (l & 15) * 4;\n";
+        s += std::string("        const idx_t qc4 = c0 + (l & 15) * ") + (bt ? "1" : "4") + ";\n";
         s += "        if (q0 < " + M + " && qc4 < " + N + ") {\n";
         s += "            porch_v4f sum;\n";
         s += "            #pragma unroll\n            for (int e = 0; e < 4; ++e) {\n";
@@ -937,7 +993,20 @@ namespace porch::cg {
         s += "                #pragma unroll\n                for (int u = 1; u < 4; ++u) x += red[u][i * 4 + e][l][v];\n";
         s += "                sum[e] = x;\n            }\n";
         const std::string row = r.batched ? "(qb * " + M + " + q0)" : "q0";
-        if (final) {
+        if (bt) {
+            s += "            #pragma unroll\n            for (int e = 0; e < 4; ++e) {\n";
+            s += "                const idx_t q1 = qc4 + 16 * e;\n";
+            s += "                if (q1 < " + N + ") {\n";
+            if (final) {
+                s += "                    const float acc_v = sum[e];\n";
+                s += epilogue_store(r, "acc_v", row + " * " + N + " + q1", "                    ");
+            } else {
+                s += "                    out[ks * " + std::to_string(r.batch * r.m * r.n) + " + " + row + " * " + N +
+                     " + q1] = sum[e];\n";
+            }
+            s += "                }\n            }\n";
+        }
+        else if (final) {
             s += "            #pragma unroll\n            for (int e = 0; e < 4; ++e) {\n";
             s += "                const idx_t q1 = qc4 + e;\n";
             s += "                const float acc_v = sum[e];\n";

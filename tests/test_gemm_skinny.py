@@ -86,9 +86,24 @@ CASES = {
     "rows, ragged columns": (
         ([3, 777], [777, 1003]), lambda a, b: porch.matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.rows", "gemm.combine"]),
-    "rows, transposed B": (
-        ([2, 1024], [3000, 1024]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+    "rows, transposed B, K not a multiple of 16": (
+        ([2, 1000], [3000, 1000]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
         lambda p: p, ["gemm.rows", "gemm.combine"]),
+    "wide, transposed B, two rows": (
+        ([2, 1024], [3000, 1024]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+        lambda p: p, ["gemm.wide", "gemm.combine"]),
+    "wide, transposed B (x @ W^T)": (
+        ([32, 4096], [4096, 4096]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+        lambda p: p, ["gemm.wide", "gemm.combine"]),
+    "wide, transposed B, ragged columns, relu": (
+        ([20, 512], [1000, 512]), lambda a, b: porch.relu(porch.matmul(a, porch.transpose(b)) + 1.0),
+        lambda a, b: a @ b.T, lambda p: np.maximum(p + 1.0, 0.0), ["gemm.wide", "gemm.combine"]),
+    "wide, transposed B, one chunk, epilogue in the kernel": (
+        ([32, 64], [300, 64]), lambda a, b: porch.matmul(a, porch.transpose(b)) * 0.5 - 1.0,
+        lambda a, b: a @ b.T, lambda p: p * 0.5 - 1.0, ["gemm.wide"]),
+    "wide, transposed B, batched": (
+        ([2, 24, 512], [2, 520, 512]), lambda a, b: porch.batched_matmul(a, porch.permute(b, [0, 2, 1])),
+        lambda a, b: a @ np.swapaxes(b, -1, -2), lambda p: p, ["gemm.wide", "gemm.combine"]),
     "rows, batched": (
         ([4, 3, 512], [4, 512, 1022]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.rows", "gemm.combine"]),
@@ -250,7 +265,7 @@ def test_emulated_split_k_with_a_bias_is_exact():
 
 
 @needs_clang
-@pytest.mark.parametrize("name", ["rows, ragged columns", "rows, transposed B", "rows, batched",
+@pytest.mark.parametrize("name", ["rows, ragged columns", "rows, transposed B, K not a multiple of 16", "rows, batched",
                                   "rows, one chunk", "three columns, odd K, bias", "columns, transposed A",
                                   "split K, ragged K, relu epilogue", "split K, transposed A",
                                   "split K, five rows", "split K, eight columns",
@@ -263,7 +278,9 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "narrow rows, four waves, K tail", "narrow, two groups a wave, written out",
                                   "wide, ragged rows and columns, K tail, relu",
                                   "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A",
-                                  "wide, two groups a wave, written out"])
+                                  "wide, two groups a wave, written out", "wide, transposed B, ragged columns, relu",
+                                  "wide, transposed B, one chunk, epilogue in the kernel",
+                                  "wide, transposed B, batched", "narrow rows, transposed B"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
     xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
@@ -427,8 +444,12 @@ def test_wide_bounds():
     assert _kinds(porch.matmul(placeholder([64, 512]), placeholder([512, 1024])))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([32, 4096]), placeholder([4096, 252])))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([16, 4096]), placeholder([4096, 254])))[0] == "gemm.mfma"
-    # B transposed: its rows along N are not contiguous
-    assert _kinds(porch.matmul(placeholder([32, 4096]), porch.transpose(placeholder([4096, 4096]))))[0] == "gemm.mfma"
+    # B stored transposed (x @ W^T): its columns read along K, in whole
+    # groups of 16 values of K
+    assert _kinds(porch.matmul(placeholder([32, 4096]), porch.transpose(placeholder([4096, 4096]))))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([32, 4080]), porch.transpose(placeholder([4096, 4080]))))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([32, 4092]), porch.transpose(placeholder([4096, 4092]))))[0] == "gemm.mfma"
+    assert _kinds(porch.matmul(placeholder([8, 4092]), porch.transpose(placeholder([4096, 4092]))))[0] == "gemm.rows"
 
 
 @pytest.mark.gpu
