@@ -769,10 +769,19 @@ namespace porch::cg {
             t += ind + "#pragma unroll\n" + ind + "for (int i = 0; i < " + RB + "; ++i)\n";
             t += ind + "    av" + set + "[i] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + aslot +
                  " + " + operand_index(r.a, "qa[i]", "(" + kq + " + lg * 4)", batch) + "));\n";
-            t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < " + NB + "; ++j)\n";
-            t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
-            t += ind + "        bv" + set + "[j][e] = " + bslot + "[" +
-                 operand_index(r.b, "(" + kq + " + lg * 4 + e)", "qc[j]", batch) + "];\n";
+            t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < " + NB + "; ++j) {\n";
+            if (b_column_runs(r)) {
+                // B stored transposed: the lane's four values of column
+                // qc[j] are one 128-bit load
+                t += ind + "    const porch_v4f bq = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                     operand_index(r.b, "(" + kq + " + lg * 4)", "qc[j]", batch) + ");\n";
+                t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e) bv" + set + "[j][e] = bq[e];\n";
+            } else {
+                t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
+                t += ind + "        bv" + set + "[j][e] = " + bslot + "[" +
+                     operand_index(r.b, "(" + kq + " + lg * 4 + e)", "qc[j]", batch) + "];\n";
+            }
+            t += ind + "}\n";
             return t;
         };
         auto mfmas = [&](const std::string& set, const std::string& ind) {
