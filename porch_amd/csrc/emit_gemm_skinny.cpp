@@ -39,8 +39,10 @@
 //                 from the L2; the waves' sums are added through LDS.  Where
 //                 B is stored transposed (x @ W^T with a weight W [n, K]),
 //                 lane l reads column 16 e + l % 16 at its four k with one
-//                 128-bit load, so that MFMA e covers 16 adjacent columns
-//                 (x [32, 4096] @ W^T: 21.1 + 4.0 us, against 42.5 + 4.8
+//                 128-bit load (a wave taking 32 values of K a group, two
+//                 such loads a column), so that MFMA e covers 16 adjacent
+//                 columns
+//                 (x [32, 4096] @ W^T: 20.1 + 4.0 us, against 42.5 + 4.8
 //                 for the split MFMA kernel that took it before; x @ W
 //                 with W stored [K, n]: 15.0 + 4.0).  gemm.narrow_rows reads
 //                 such a B's four values of a group as one 128-bit load too
@@ -219,18 +221,25 @@ namespace porch::cg {
             int64_t chunk = 0;  // K per chunk, a multiple of 64 (a group per wave)
         };
 
+        // Values of K a wave of gemm.wide takes per group: 16, or 32 where
+        // B is stored transposed (a lane then reads 128 B of each of its
+        // columns in two loads; x [32, 4096] @ W^T: 18.7 against 23.3 us
+        // with 16 in a standalone copy timed back to back, 20.1 against
+        // 21.1 us as emitted, under the kernel tracer)
+        int64_t wide_group(const gemm_request& r) { return b_vector(r) ? group_size : 2 * group_size; }
+
         wide_shape wide_plan(const gemm_request& r) {
             wide_shape sh;
             // B's rows read along N, or its columns along K where B is
             // stored transposed (then in whole groups of 16 values of K)
-            const bool b_ok = b_vector(r) || (b_column_runs(r) && r.k % group_size == 0);
+            const bool b_ok = b_vector(r) || (b_column_runs(r) && r.k % (2 * group_size) == 0);
             if (r.m < wide_min_rows || r.m > wide_max_rows || r.n < 256 || !b_ok || !big_enough(r)) return sh;
             sh.rb = (r.m + 15) / 16;
             sh.tiles = (r.n + 63) / 64;
             // About one workgroup (four waves) per compute unit, partials
             // (chunks x m x n) at most 1/4 of B (K x n), at most 32 chunks.
             const int64_t cus = std::max(r.compute_units, 8);
-            const int64_t batch_k = group_waves * group_size;
+            const int64_t batch_k = group_waves * wide_group(r);
             int64_t chunks = (cus + r.batch * sh.tiles - 1) / (r.batch * sh.tiles);
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / (4 * r.m)));
             chunks = std::min(chunks, std::max<int64_t>(1, r.k / batch_k));
@@ -273,14 +282,14 @@ namespace porch::cg {
         // us for one wave per tile and chunk with 16 chunks; eight or sixteen
         // waves a workgroup 17.5 and 21.7 us, three groups in flight 15.6.)
         std::string group_loop(int64_t per_wave, const group_text& declare, const group_load_text& loads,
-                               const group_text& mfmas) {
-            const std::string G16 = std::to_string(group_size);
+                               const group_text& mfmas, int64_t width = group_size) {
+            const std::string G16 = std::to_string(width);
             std::string s;
             if (per_wave > 0 && per_wave <= 32) {
                 auto set_of = [](int64_t t) { return "S" + std::to_string(t % group_depth); };
                 auto load_group = [&](int64_t t) {
                     return "    {\n        const idx_t kq = k0 + " + G16 + " * w + " +
-                           std::to_string(t * group_waves * group_size) + ";\n" + loads(set_of(t), "kq", "        ") +
+                           std::to_string(t * group_waves * width) + ";\n" + loads(set_of(t), "kq", "        ") +
                            "    }\n";
                 };
                 for (int d = 0; d < group_depth; ++d) s += declare(set_of(d), "    ");
@@ -922,16 +931,33 @@ namespace porch::cg {
         const std::string aslot = "a" + std::to_string(r.a.slot);
         const std::string bslot = "a" + std::to_string(r.b.slot);
         auto declare = [&](const std::string& set, const std::string& ind) {
+            if (bt)
+                return ind + "porch_v4f bv" + set + "[4][2];\n" + ind + "porch_v4f av" + set + "[" + RB + "][2];\n";
             return ind + "porch_v4f bv" + set + "[4];\n" + ind + "porch_v4f av" + set + "[" + RB + "];\n";
         };
         auto loads = [&](const std::string& set, const std::string& kq, const std::string& ind) {
             std::string t;
             if (bt) {
-                // column qc[e] at the lane's four k: one 128-bit load each
-                // (16 columns x 64 B an instruction)
+                // a group of 32 values of K in two halves s: column qc[e]
+                // at the lane's four k of half s, one 128-bit load each
+                // (16 columns x 64 B an instruction, the two halves of a
+                // column's 128 B in two)
                 t += ind + "#pragma unroll\n" + ind + "for (int e = 0; e < 4; ++e)\n";
-                t += ind + "    bv" + set + "[e] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot +
-                     " + " + operand_index(r.b, "(" + kq + " + lg * 4)", "qc[e]", batch) + "));\n";
+                t += ind + "    #pragma unroll\n" + ind + "    for (int h = 0; h < 2; ++h)\n";
+                t += ind + "        bv" + set + "[e][h] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" +
+                     bslot + " + " + operand_index(r.b, "(" + kq + " + 16 * h + lg * 4)", "qc[e]", batch) + "));\n";
+                t += ind + "#pragma unroll\n" + ind + "for (int i = 0; i < " + RB + "; ++i)\n";
+                t += ind + "    #pragma unroll\n" + ind + "    for (int h = 0; h < 2; ++h) {\n";
+                if (avec) {
+                    t += ind + "        av" + set + "[i][h] = *reinterpret_cast<const porch_v4f*>(" + aslot + " + " +
+                         operand_index(r.a, "qa[i]", "(" + kq + " + 16 * h + lg * 4)", batch) + ");\n";
+                } else {
+                    t += ind + "        #pragma unroll\n" + ind + "        for (int j = 0; j < 4; ++j)\n";
+                    t += ind + "            av" + set + "[i][h][j] = " + aslot + "[" +
+                         operand_index(r.a, "qa[i]", "(" + kq + " + 16 * h + lg * 4 + j)", batch) + "];\n";
+                }
+                t += ind + "    }\n";
+                return t;
             } else {
                 t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < 4; ++j)\n";
                 t += ind + "    bv" + set + "[j] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + bslot +
@@ -952,14 +978,24 @@ namespace porch::cg {
         };
         auto mfmas = [&](const std::string& set, const std::string& ind) {
             std::string t;
+            if (bt) {
+                t += ind + "#pragma unroll\n" + ind + "for (int h = 0; h < 2; ++h)\n";
+                t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < 4; ++j)\n";
+                t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
+                t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
+                t += ind + "            acc[i][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[i][h][j], bv" + set +
+                     "[e][h][j], acc[i][e], 0, 0, 0);\n";
+                return t;
+            }
             t += ind + "#pragma unroll\n" + ind + "for (int j = 0; j < 4; ++j)\n";
             t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e)\n";
             t += ind + "        #pragma unroll\n" + ind + "        for (int i = 0; i < " + RB + "; ++i)\n";
             t += ind + "            acc[i][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av" + set + "[i][j], bv" + set +
-                 (bt ? "[e][j]" : "[j][e]") + ", acc[i][e], 0, 0, 0);\n";
+                 "[j][e], acc[i][e], 0, 0, 0);\n";
             return t;
         };
-        s += group_loop(r.k % sh.chunk == 0 ? sh.chunk / (group_waves * group_size) : 0, declare, loads, mfmas);
+        const int64_t width = wide_group(r);
+        s += group_loop(r.k % sh.chunk == 0 ? sh.chunk / (group_waves * width) : 0, declare, loads, mfmas, width);
         const std::string G16 = std::to_string(group_size);
         // The partial last group (a chunk not a multiple of 16 values), in
         // the wave whose turn it is: lanes past the chunk read its last

@@ -445,9 +445,10 @@ def test_wide_bounds():
     assert _kinds(porch.matmul(placeholder([32, 4096]), placeholder([4096, 252])))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([16, 4096]), placeholder([4096, 254])))[0] == "gemm.mfma"
     # B stored transposed (x @ W^T): its columns read along K, in whole
-    # groups of 16 values of K
+    # groups of 32 values of K
     assert _kinds(porch.matmul(placeholder([32, 4096]), porch.transpose(placeholder([4096, 4096]))))[0] == "gemm.wide"
-    assert _kinds(porch.matmul(placeholder([32, 4080]), porch.transpose(placeholder([4096, 4080]))))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([32, 4064]), porch.transpose(placeholder([4096, 4064]))))[0] == "gemm.wide"
+    assert _kinds(porch.matmul(placeholder([32, 4080]), porch.transpose(placeholder([4096, 4080]))))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([32, 4092]), porch.transpose(placeholder([4096, 4092]))))[0] == "gemm.mfma"
     assert _kinds(porch.matmul(placeholder([8, 4092]), porch.transpose(placeholder([4096, 4092]))))[0] == "gemm.rows"
 
