@@ -130,7 +130,9 @@ namespace porch::cg {
         // against 392.4 us on the attention product, 198.6 against 211.1 at
         // [2, 8192, 64] @ [2, 64, 8192]); where the stores dominate they
         // were slower ([16, 4096, 8] @ [16, 8, 4096] 226.3 against 203.2 us,
-        // [4, 4096, 32] @ [4, 32, 4096] 78.9 against 59.6).
+        // [4, 4096, 32] @ [4, 32, 4096] 78.9 against 59.6).  In between, at
+        // [16, 4096, K] @ [16, K, 4096] timed back to back: K = 40 216.4
+        // against 214.3 us, 48 214.9 against 241.5, 56 242.8 against 269.3.
         const bool nt_store = r.k > 32;
         const std::string M = std::to_string(r.m);
         const std::string N = std::to_string(r.n);
