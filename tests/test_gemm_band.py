@@ -114,9 +114,14 @@ def test_band_bounds():
                                        placeholder([16, 128, 8192])[:, ::2, ::2]))[0] == "gemm.mfma"
 
 
+# Each emulation runs a band product's full grid on the CPU (the kernel
+# needs two workgroups a compute unit, so at least ~16 M outputs), about
+# two minutes each: the cases below cover ragged bands, ragged and single-
+# tile runs, an epilogue reading a bias, K of 8 and 40 (the non-temporal
+# stores) and, in the transposed test, B read along K.  The other cases
+# run on the GPU against the oracle.
 @needs_clang
-@pytest.mark.parametrize("name", ["bias and relu, K of 16", "ragged last band and tile, K of 8",
-                                  "runs, the last of one tile, K of 8, bias", "ragged runs, K of 40"])
+@pytest.mark.parametrize("name", ["runs, the last of one tile, K of 8, bias", "ragged runs, K of 40"])
 def test_emulated_band_products_are_exact(name):
     xs = {}
 
