@@ -231,7 +231,7 @@ namespace porch::cg {
         wide_shape wide_plan(const gemm_request& r) {
             wide_shape sh;
             // B's rows read along N, or its columns along K where B is
-            // stored transposed (then in whole groups of 16 values of K)
+            // stored transposed (then in whole groups of 32 values of K)
             const bool b_ok = b_vector(r) || (b_column_runs(r) && r.k % (2 * group_size) == 0);
             if (r.m < wide_min_rows || r.m > wide_max_rows || r.n < 256 || !b_ok || !big_enough(r)) return sh;
             sh.rb = (r.m + 15) / 16;
@@ -283,12 +283,12 @@ namespace porch::cg {
         // waves a workgroup 17.5 and 21.7 us, three groups in flight 15.6.)
         std::string group_loop(int64_t per_wave, const group_text& declare, const group_load_text& loads,
                                const group_text& mfmas, int64_t width = group_size) {
-            const std::string G16 = std::to_string(width);
+            const std::string GW = std::to_string(width);
             std::string s;
             if (per_wave > 0 && per_wave <= 32) {
                 auto set_of = [](int64_t t) { return "S" + std::to_string(t % group_depth); };
                 auto load_group = [&](int64_t t) {
-                    return "    {\n        const idx_t kq = k0 + " + G16 + " * w + " +
+                    return "    {\n        const idx_t kq = k0 + " + GW + " * w + " +
                            std::to_string(t * group_waves * width) + ";\n" + loads(set_of(t), "kq", "        ") +
                            "    }\n";
                 };
@@ -302,16 +302,16 @@ namespace porch::cg {
                 return s;
             }
             s += declare("P", "    ") + declare("Q", "    ");
-            s += "    const idx_t full = (k1 - k0) / " + G16 + ";\n";
+            s += "    const idx_t full = (k1 - k0) / " + GW + ";\n";
             s += "    const idx_t nf = full > w ? (full - w + 3) / 4 : 0;\n";
-            s += "    if (nf > 0) {\n        const idx_t kq = k0 + " + G16 + " * w;\n" + loads("P", "kq", "        ") + "    }\n";
+            s += "    if (nf > 0) {\n        const idx_t kq = k0 + " + GW + " * w;\n" + loads("P", "kq", "        ") + "    }\n";
             s += "    idx_t t = 0;\n";
             s += "    for (; t + 2 <= nf; t += 2) {\n";
-            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 1));\n" +
+            s += "        {\n            const idx_t kq = k0 + " + GW + " * (w + 4 * (t + 1));\n" +
                  loads("Q", "kq", "            ") + "        }\n";
             s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("P", "        ") +
                  "        __builtin_amdgcn_sched_barrier(0);\n";
-            s += "        {\n            const idx_t kq = k0 + " + G16 + " * (w + 4 * (t + 2 < nf ? t + 2 : t + 1));\n" +
+            s += "        {\n            const idx_t kq = k0 + " + GW + " * (w + 4 * (t + 2 < nf ? t + 2 : t + 1));\n" +
                  loads("P", "kq", "            ") + "        }\n";
             s += "        __builtin_amdgcn_sched_barrier(0);\n" + mfmas("Q", "        ") +
                  "        __builtin_amdgcn_sched_barrier(0);\n";
@@ -1001,7 +1001,6 @@ namespace porch::cg {
         // the wave whose turn it is: lanes past the chunk read its last
         // value and zero both operands.
         if (sh.chunk % group_size != 0 || r.k % group_size != 0) {
-            if (bt) throw std::logic_error("emit_gemm_wide: B read along K needs whole groups");
             if (bt) throw std::logic_error("emit_gemm_wide: B read along K needs whole groups");
             s += "    if (full * " + G16 + " < k1 - k0 && full % 4 == w) {\n";
             s += "        const idx_t kq = k0 + full * " + G16 + ";\n";
