@@ -121,12 +121,32 @@ def emulate(expr, timeout: float = 120.0, only=None, force_exact: bool = False) 
     return results
 
 
-def evaluate(expr, inputs: list[np.ndarray], force_exact: bool = False, timeout: float = 120.0) -> np.ndarray:
+# The bits of an output no workgroup wrote (a NaN with a payload that no
+# kernel computes from finite inputs) when a subset of workgroups runs.
+UNWRITTEN = np.uint32(0x7FC0DEAD)
+
+
+def edge_blocks(grid_x: int) -> list[int]:
+    """The first two and the last two workgroups of a grid of `grid_x`: with
+    the kernels' block-to-tile maps they own the first outputs and the
+    ragged last ones (the last band, run, row group or column tile)."""
+    return sorted({0, 1, grid_x - 2, grid_x - 1} & set(range(grid_x)))
+
+
+def written(out: np.ndarray) -> np.ndarray:
+    """Where `evaluate(..., only=...)` wrote the output."""
+    return np.ascontiguousarray(out, np.float32).view(np.uint32) != UNWRITTEN
+
+
+def evaluate(expr, inputs: list[np.ndarray], force_exact: bool = False, timeout: float = 120.0,
+             only=None) -> np.ndarray:
     """The graph's result computed by its generated kernels run on the CPU
     (in plan order, temporaries carried between them), for input values
     `inputs` (the serialised input order).  Arithmetic follows the host's
     libm where the kernels call device math, so only exact operations
-    (views, + - * /, max, reductions of integers) compare bit for bit."""
+    (views, + - * /, max, reductions of integers) compare bit for bit.
+    `only`: run just these block x indices of a single-kernel plan; the
+    outputs of the other blocks keep the bits UNWRITTEN (see written())."""
     import tempfile
 
     expr = porch.tensor_expr(expr)
@@ -138,6 +158,9 @@ def evaluate(expr, inputs: list[np.ndarray], force_exact: bool = False, timeout:
     temps = [np.zeros(max(int(n), 1), np.float32) for n in plan["temps"]]
     out = np.zeros(max(int(np.prod(plan["out_shape"], dtype=np.int64)) if plan["out_shape"] else 1, 1),
                    np.float32)
+    if only is not None:
+        assert len(plan["kernels"]) == 1, "a subset of workgroups needs a single-kernel plan"
+        out.view(np.uint32)[:] = UNWRITTEN
     with tempfile.TemporaryDirectory() as work:
         for i, k in enumerate(plan["kernels"]):
             slots = (buffers + temps)[: k["slots"]]
@@ -148,7 +171,24 @@ def evaluate(expr, inputs: list[np.ndarray], force_exact: bool = False, timeout:
             if force_exact:
                 source = source.replace(_ORDER_TEST, "return true;")
             ok, detail = run_kernel(source, k["name"], [b.size for b in slots] + [dest.size],
-                                    k["grid"], k["block"], timeout, values=work)
+                                    k["grid"], k["block"], timeout, only, values=work)
             assert ok, detail
             dest[:] = np.fromfile(os.path.join(work, "out.bin"), np.float32)
     return out.reshape(plan["out_shape"])
+
+
+def check_edges(expr, inputs: list[np.ndarray], want: np.ndarray, timeout: float = 600.0) -> int:
+    """Runs the first two and last two workgroups of a single-kernel plan:
+    their accesses must stay inside the buffers (both placements), they
+    must write the first and the last output, and every output they write
+    must equal `want` bit for bit.  Returns the number of outputs checked."""
+    plan = porch.plan(porch.tensor_expr(expr))
+    assert len(plan["kernels"]) == 1, plan["kernels"]
+    edges = edge_blocks(int(plan["kernels"][0]["grid"][0]))
+    results = emulate(expr, timeout=timeout, only=edges)
+    assert all(r["ok"] for r in results), results
+    got = evaluate(expr, inputs, timeout=timeout, only=edges).reshape(want.shape)
+    mask = written(got)
+    assert mask.reshape(-1)[0] and mask.reshape(-1)[-1], "the edge workgroups missed the first or last output"
+    assert np.array_equal(got[mask].view(np.uint32), np.ascontiguousarray(want, np.float32)[mask].view(np.uint32))
+    return int(mask.sum())
