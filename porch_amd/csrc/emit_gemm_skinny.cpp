@@ -604,89 +604,157 @@ namespace porch::cg {
                      "    }\n    else {\n" + body(true) + "    }\n";
                 return t;
             };
-            s += load_rows("x0", 0);
-            for (int64_t n = 0; n < rounds; ++n) {
-                const std::string cur = n % 2 == 0 ? "x0" : "x1";
-                const std::string nxt = n % 2 == 0 ? "x1" : "x0";
-                s += "    {\n";
-                // this round's values of B first: lane (li, lg) needs column
-                // li at k = base + 16 q + 4 lg + e for its 4 steps of group q.
-                // (Loads complete in issue order: B before the next round's
-                // rows, so waiting for B does not wait for them.)
-                s += "        float bv[16][4];\n";
-                s += "        const bool full = kbeg + " + std::to_string((n + 1) * rows_round) + " <= kend;\n";
-                auto b_loads = [&](bool clamp) {
-                    std::string t;
-                    if (b_column_runs(r)) {
-                        // B stored transposed (w^T of a weight w [n, K]):
-                        // the lane's four values of group q are one float4
-                        // of column li (a quad past the wave's range reads
-                        // k = 0 and is masked in the MFMAs)
-                        t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q) {\n";
-                        t += "                const idx_t k = kbeg + " + std::to_string(n * rows_round) +
-                             " + q * 16 + lg * 4;\n";
-                        t += std::string("                const idx_t kr = ") +
-                             (clamp ? "k < kend ? k : (idx_t)0" : "k") + ";\n";
-                        t += "                const porch_v4f bq = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
-                             operand_index(r.b, "kr", "qc", batch) + ");\n";
-                        t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) bv[q][e] = bq[e];\n";
-                        t += "            }\n";
-                        return t;
-                    }
-                    t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q)\n";
-                    t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) {\n";
-                    t += "                    const idx_t k = kbeg + " + std::to_string(n * rows_round) +
-                         " + q * 16 + lg * 4 + e;\n";
-                    t += std::string("                    const idx_t kr = ") + (clamp ? "k < kend ? k : (idx_t)0" : "k") +
-                         ";\n";
-                    t += "                    bv[q][e] = " + bslot + "[" + operand_index(r.b, "kr", "qc", batch) + "];\n";
-                    t += "                }\n";
+            // Every wave's range whole rounds (K = waves x a multiple of
+            // 256): no clamps and no zeroing, and each later round's values
+            // of B are loaded during the round before it, group q's right
+            // after that round's MFMAs of group q have used the registers
+            // (the loads' latency then overlaps the rest of the round:
+            // 18.3-18.7 against 19.0-19.2 us at [4096, 4096] @ [4096, 16],
+            // timed back to back; the same with the ragged rounds' clamps
+            // and branches kept was slower, 19.7-19.8 us).
+            const bool whole = kw * waves == r.k && kw % rows_round == 0;
+            auto b_group = [&](int64_t n, const std::string& q, const std::string& ind) {
+                std::string t;
+                if (b_column_runs(r)) {
+                    t += ind + "{\n";
+                    t += ind + "    const porch_v4f bq = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                         operand_index(r.b, "(kbeg + " + std::to_string(n * rows_round) + " + " + q + " * 16 + lg * 4)", "qc",
+                                       batch) + ");\n";
+                    t += ind + "    #pragma unroll\n" + ind + "    for (int e = 0; e < 4; ++e) bv[" + q + "][e] = bq[e];\n";
+                    t += ind + "}\n";
                     return t;
-                };
-                s += "        if (full) {\n" + b_loads(false) + "        }\n        else {\n" + b_loads(true) + "        }\n";
-                if (n + 1 < rounds) s += load_rows(nxt, n + 1);
-                s += "        __builtin_amdgcn_sched_barrier(0);\n";
-                // lane l holds k = base + 4 l .. + 3 of each of the 16 rows
-                // a round inside the wave's range needs no zeroing
-                s += "        if (full) {\n";
-                s += "            #pragma unroll\n            for (int rr = 0; rr < 16; ++rr)\n";
-                s += "                *reinterpret_cast<porch_v4f*>(my + rr * " + RS + " + 4 * lane) = " + cur + "[rr];\n";
-                s += "        }\n        else {\n";
-                s += "            const bool kin = kbeg + " + std::to_string(n * rows_round) + " + 4 * lane < kend;\n";
-                s += "            #pragma unroll\n            for (int rr = 0; rr < 16; ++rr)\n";
-                s += "                *reinterpret_cast<porch_v4f*>(my + rr * " + RS + " + 4 * lane) = kin ? " + cur +
-                     "[rr] : porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
-                s += "        }\n";
-                // the wave's lanes read each other's values: LDS operations
-                // of one wave complete in order, and the wave barrier keeps
-                // the compiler from moving the reads above the writes
-                s += "        __builtin_amdgcn_wave_barrier();\n";
-                s += "        __builtin_amdgcn_sched_barrier(0);\n";
-                // MFMA step e of group q: lane (li, lg) gives row li at
-                // k = base + 16 q + 4 lg + e (a float4 of the row per group)
-                auto mfma_loop = [&](bool guarded) {
-                    std::string t;
-                    t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q) {\n";
-                    t += "                const porch_v4f av = *reinterpret_cast<const porch_v4f*>(my + li * " + RS +
+                }
+                t += ind + "#pragma unroll\n" + ind + "for (int e = 0; e < 4; ++e)\n";
+                t += ind + "    bv[" + q + "][e] = " + bslot + "[" +
+                     operand_index(r.b, "(kbeg + " + std::to_string(n * rows_round) + " + " + q + " * 16 + lg * 4 + e)", "qc",
+                                   batch) + "];\n";
+                return t;
+            };
+            auto whole_rows = [&](const std::string& set, int64_t round) {
+                std::string t;
+                t += "    #pragma unroll\n    for (int rr = 0; rr < 16; ++rr) {\n";
+                t += "        const idx_t q0 = r0 + rr < " + M + " ? r0 + rr : (idx_t)" + std::to_string(r.m - 1) + ";\n";
+                t += "        " + set + "[rr] = __builtin_nontemporal_load(reinterpret_cast<const porch_v4f*>(" + aslot + " + " +
+                     operand_index(r.a, "q0", "(kbeg + " + std::to_string(round * rows_round) + " + 4 * lane)", batch) +
+                     "));\n";
+                t += "    }\n";
+                return t;
+            };
+            if (whole) {
+                s += "    float bv[16][4];\n";
+                s += whole_rows("x0", 0);
+                s += "    #pragma unroll\n    for (int q = 0; q < 16; ++q) {\n" + b_group(0, "q", "        ") + "    }\n";
+                for (int64_t n = 0; n < rounds; ++n) {
+                    const std::string cur = n % 2 == 0 ? "x0" : "x1";
+                    const std::string nxt = n % 2 == 0 ? "x1" : "x0";
+                    const bool more = n + 1 < rounds;
+                    if (more) s += whole_rows(nxt, n + 1);
+                    s += "    __builtin_amdgcn_sched_barrier(0);\n";
+                    s += "    #pragma unroll\n    for (int rr = 0; rr < 16; ++rr)\n";
+                    s += "        *reinterpret_cast<porch_v4f*>(my + rr * " + RS + " + 4 * lane) = " + cur + "[rr];\n";
+                    // the wave's lanes read each other's values (see below)
+                    s += "    __builtin_amdgcn_wave_barrier();\n";
+                    s += "    __builtin_amdgcn_sched_barrier(0);\n";
+                    s += "    #pragma unroll\n    for (int q = 0; q < 16; ++q) {\n";
+                    s += "        const porch_v4f av = *reinterpret_cast<const porch_v4f*>(my + li * " + RS +
                          " + q * 16 + lg * 4);\n";
-                    t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) {\n";
-                    if (guarded) {
-                        t += "                    const bool kin = kbeg + " + std::to_string(n * rows_round) +
-                             " + q * 16 + lg * 4 + e < kend;\n";
-                        t += "                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], kin ? bv[q][e] : 0.0f, acc, "
-                             "0, 0, 0);\n";
+                    s += "        #pragma unroll\n        for (int e = 0; e < 4; ++e)\n";
+                    s += "            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[q][e], acc, 0, 0, 0);\n";
+                    if (more) {
+                        s += "        __builtin_amdgcn_sched_barrier(0);\n";
+                        s += b_group(n + 1, "q", "        ");
+                        s += "        __builtin_amdgcn_sched_barrier(0);\n";
                     }
-                    else {
-                        t += "                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[q][e], acc, 0, 0, 0);\n";
-                    }
-                    t += "                }\n            }\n";
-                    return t;
-                };
-                s += "        if (full) {\n" + mfma_loop(false) + "        }\n        else {\n" + mfma_loop(true) +
-                     "        }\n";
-                s += "        __builtin_amdgcn_wave_barrier();\n";
-                s += "        __builtin_amdgcn_sched_barrier(0);\n";
-                s += "    }\n";
+                    s += "    }\n";
+                    s += "    __builtin_amdgcn_wave_barrier();\n";
+                    s += "    __builtin_amdgcn_sched_barrier(0);\n";
+                }
+            }
+            else {
+                s += load_rows("x0", 0);
+                for (int64_t n = 0; n < rounds; ++n) {
+                    const std::string cur = n % 2 == 0 ? "x0" : "x1";
+                    const std::string nxt = n % 2 == 0 ? "x1" : "x0";
+                    s += "    {\n";
+                    // this round's values of B first: lane (li, lg) needs column
+                    // li at k = base + 16 q + 4 lg + e for its 4 steps of group q.
+                    // (Loads complete in issue order: B before the next round's
+                    // rows, so waiting for B does not wait for them.)
+                    s += "        float bv[16][4];\n";
+                    s += "        const bool full = kbeg + " + std::to_string((n + 1) * rows_round) + " <= kend;\n";
+                    auto b_loads = [&](bool clamp) {
+                        std::string t;
+                        if (b_column_runs(r)) {
+                            // B stored transposed (w^T of a weight w [n, K]):
+                            // the lane's four values of group q are one float4
+                            // of column li (a quad past the wave's range reads
+                            // k = 0 and is masked in the MFMAs)
+                            t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q) {\n";
+                            t += "                const idx_t k = kbeg + " + std::to_string(n * rows_round) +
+                                 " + q * 16 + lg * 4;\n";
+                            t += std::string("                const idx_t kr = ") +
+                                 (clamp ? "k < kend ? k : (idx_t)0" : "k") + ";\n";
+                            t += "                const porch_v4f bq = *reinterpret_cast<const porch_v4f*>(" + bslot + " + " +
+                                 operand_index(r.b, "kr", "qc", batch) + ");\n";
+                            t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) bv[q][e] = bq[e];\n";
+                            t += "            }\n";
+                            return t;
+                        }
+                        t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q)\n";
+                        t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) {\n";
+                        t += "                    const idx_t k = kbeg + " + std::to_string(n * rows_round) +
+                             " + q * 16 + lg * 4 + e;\n";
+                        t += std::string("                    const idx_t kr = ") + (clamp ? "k < kend ? k : (idx_t)0" : "k") +
+                             ";\n";
+                        t += "                    bv[q][e] = " + bslot + "[" + operand_index(r.b, "kr", "qc", batch) + "];\n";
+                        t += "                }\n";
+                        return t;
+                    };
+                    s += "        if (full) {\n" + b_loads(false) + "        }\n        else {\n" + b_loads(true) + "        }\n";
+                    if (n + 1 < rounds) s += load_rows(nxt, n + 1);
+                    s += "        __builtin_amdgcn_sched_barrier(0);\n";
+                    // lane l holds k = base + 4 l .. + 3 of each of the 16 rows
+                    // a round inside the wave's range needs no zeroing
+                    s += "        if (full) {\n";
+                    s += "            #pragma unroll\n            for (int rr = 0; rr < 16; ++rr)\n";
+                    s += "                *reinterpret_cast<porch_v4f*>(my + rr * " + RS + " + 4 * lane) = " + cur + "[rr];\n";
+                    s += "        }\n        else {\n";
+                    s += "            const bool kin = kbeg + " + std::to_string(n * rows_round) + " + 4 * lane < kend;\n";
+                    s += "            #pragma unroll\n            for (int rr = 0; rr < 16; ++rr)\n";
+                    s += "                *reinterpret_cast<porch_v4f*>(my + rr * " + RS + " + 4 * lane) = kin ? " + cur +
+                         "[rr] : porch_v4f{0.0f, 0.0f, 0.0f, 0.0f};\n";
+                    s += "        }\n";
+                    // the wave's lanes read each other's values: LDS operations
+                    // of one wave complete in order, and the wave barrier keeps
+                    // the compiler from moving the reads above the writes
+                    s += "        __builtin_amdgcn_wave_barrier();\n";
+                    s += "        __builtin_amdgcn_sched_barrier(0);\n";
+                    // MFMA step e of group q: lane (li, lg) gives row li at
+                    // k = base + 16 q + 4 lg + e (a float4 of the row per group)
+                    auto mfma_loop = [&](bool guarded) {
+                        std::string t;
+                        t += "            #pragma unroll\n            for (int q = 0; q < 16; ++q) {\n";
+                        t += "                const porch_v4f av = *reinterpret_cast<const porch_v4f*>(my + li * " + RS +
+                             " + q * 16 + lg * 4);\n";
+                        t += "                #pragma unroll\n                for (int e = 0; e < 4; ++e) {\n";
+                        if (guarded) {
+                            t += "                    const bool kin = kbeg + " + std::to_string(n * rows_round) +
+                                 " + q * 16 + lg * 4 + e < kend;\n";
+                            t += "                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], kin ? bv[q][e] : 0.0f, acc, "
+                                 "0, 0, 0);\n";
+                        }
+                        else {
+                            t += "                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[q][e], acc, 0, 0, 0);\n";
+                        }
+                        t += "                }\n            }\n";
+                        return t;
+                    };
+                    s += "        if (full) {\n" + mfma_loop(false) + "        }\n        else {\n" + mfma_loop(true) +
+                         "        }\n";
+                    s += "        __builtin_amdgcn_wave_barrier();\n";
+                    s += "        __builtin_amdgcn_sched_barrier(0);\n";
+                    s += "    }\n";
+                }
             }
             // the waves' sums added in wave order
             s += "    __syncthreads();\n";

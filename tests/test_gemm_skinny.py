@@ -167,6 +167,17 @@ CASES = {
     "narrow rows, transposed B": (
         ([4096, 3000], [9, 3000]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
         lambda p: p, ["gemm.narrow_rows"]),
+    # every wave's range whole rounds of 256 (the next round's values of B
+    # loaded during this round's MFMAs)
+    "narrow rows, whole rounds, ragged rows and columns, relu": (
+        ([4090, 4096], [4096, 13]), lambda a, b: porch.relu(porch.matmul(a, b) - 2.0), lambda a, b: a @ b,
+        lambda p: np.maximum(p - 2.0, 0.0), ["gemm.narrow_rows"]),
+    "narrow rows, whole rounds, transposed B": (
+        ([4096, 4096], [11, 4096]), lambda a, b: porch.matmul(a, porch.transpose(b)), lambda a, b: a @ b.T,
+        lambda p: p, ["gemm.narrow_rows"]),
+    "narrow rows, four waves, whole rounds, batched": (
+        ([2, 2048, 6144], [2, 6144, 16]), lambda a, b: porch.batched_matmul(a, b) * 0.5, lambda a, b: a @ b,
+        lambda p: p * 0.5, ["gemm.narrow_rows"]),
     "six columns, batched, ragged row groups": (
         ([2, 1101, 512], [2, 512, 6]), lambda a, b: porch.batched_matmul(a, b), lambda a, b: a @ b, lambda p: p,
         ["gemm.cols"]),
@@ -280,7 +291,10 @@ def test_emulated_split_k_with_a_bias_is_exact():
                                   "wide, one chunk, epilogue in the kernel", "wide, batched", "wide, transposed A",
                                   "wide, two groups a wave, written out", "wide, transposed B, ragged columns, relu",
                                   "wide, transposed B, one chunk, epilogue in the kernel",
-                                  "wide, transposed B, batched", "narrow rows, transposed B"])
+                                  "wide, transposed B, batched", "narrow rows, transposed B",
+                                  "narrow rows, whole rounds, ragged rows and columns, relu",
+                                  "narrow rows, whole rounds, transposed B",
+                                  "narrow rows, four waves, whole rounds, batched"])
 def test_emulated_integer_products_are_exact(name):
     shapes, build, prod, epi, _ = CASES[name]
     xs = [_ints(s, i + 1) for i, s in enumerate(shapes)]
