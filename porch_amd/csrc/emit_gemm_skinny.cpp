@@ -609,7 +609,7 @@ namespace porch::cg {
             // of B are loaded during the round before it, group q's right
             // after that round's MFMAs of group q have used the registers
             // (the loads' latency then overlaps the rest of the round:
-            // 18.3-18.7 against 19.0-19.2 us at [4096, 4096] @ [4096, 16],
+            // 18.4-18.6 against 18.8-19.1 us at [4096, 4096] @ [4096, 16],
             // timed back to back; the same with the ragged rounds' clamps
             // and branches kept was slower, 19.7-19.8 us).
             const bool whole = kw * waves == r.k && kw % rows_round == 0;
