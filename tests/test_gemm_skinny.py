@@ -513,6 +513,27 @@ def test_narrow_rows_infinities_at_the_waves_ends(gpu):
 
 
 @pytest.mark.gpu
+def test_narrow_rows_infinities_at_whole_round_edges(gpu):
+    """Infinities in B's rows at the edges of whole rounds (K = 4096: 512
+    values a wave in two rounds of 256, the second round's values of B
+    loaded during the first round's MFMAs): inf or NaN exactly where the
+    oracle has them."""
+    m, k, n = 4096, 4096, 16
+    a, b = _ints([m, k], 35), _ints([k, n], 36)
+    b[255, :] = np.inf      # the first wave's first round, its last value
+    b[256, 3] = -np.inf     # its second round's first
+    b[767, 5] = np.inf      # the second wave's first round, its last value
+    b[768, 2] = -np.inf     # its second round's first
+    b[k - 1, 7] = np.inf    # the last wave's last value
+    expr = porch.matmul(gpu.tensor([m, k], a), gpu.tensor([k, n], b))
+    assert _kinds(expr) == ["gemm.narrow_rows"]
+    out = gpu.materialize(expr).cpu().reshape(m, n)
+    ref = np.asarray(host.evaluate(expr), np.float32).reshape(m, n)
+    assert np.isinf(ref).any() and np.isnan(ref).any()
+    assert np.array_equal(out, ref, equal_nan=True)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("kind, m, k, n", [("gemm.narrow", 1100, 1036, 20), ("gemm.narrow_rows", 4090, 2100, 13),
                                            ("gemm.wide", 20, 203, 300)])
 def test_clamped_edge_rows_and_columns(gpu, kind, m, k, n):
